@@ -1,0 +1,139 @@
+/* q36moe -- MI355X (gfx950) W4A8 mixture-of-experts layer, C ABI.
+ *
+ * Drop-in for the MoE FFN of the q36 engine: router logits in, combined
+ * hidden state out.  Plain pointers and sizes only; every device pointer is
+ * a HIP device allocation owned by the caller unless stated otherwise, and
+ * every stream is a hipStream_t passed as void*.
+ *
+ * Reference interfaces replaced (file:line in the q36 tree):
+ *   q36moe_weights_upload  <- upload() MXFP4 expert branch, q36_engine.cu:196-228
+ *                             (GGUF block_mxfp4 [E][M][K/32], q36.h:112-114)
+ *   q36moe_ctx_create      <- MoE scratch allocated in q36_engine_create,
+ *                             q36_engine.cu:1467-1512 (no allocation in forward)
+ *   q36moe_forward         <- moe_ffn, q36_engine.cu:1592-1654 (decode) and
+ *                             pf_moe_block, q36_engine.cu:3423-3472 (prefill),
+ *                             starting after the router matvec
+ *   q36moe_router_topk     <- k_router_topk, q36_ops.cuh:397-431
+ *   q36moe_quant_e4m3      <- k_quant_e4m3, q36_engine.cu:2411-2428
+ *   q36moe_ctx_copy_tap    <- the Q36_DEBUG routing dumps, q36_engine.cu:1648-1653
+ *   q36moe_probe_mfma      <- the block-scaled MMA calibration harness,
+ *                             test_mma_bs.cu:46-69
+ *
+ * Errors are returned, never exit(): 0 ok, Q36MOE_EINVAL for bad arguments,
+ * Q36MOE_ENOMEM for failed allocations, Q36MOE_EHIP for a HIP runtime error
+ * (the reference prints and exits instead, q36_engine.cu:45).
+ */
+#ifndef Q36MOE_H
+#define Q36MOE_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define Q36MOE_OK       0
+#define Q36MOE_EINVAL (-22)
+#define Q36MOE_ENOMEM (-12)
+#define Q36MOE_EHIP   (-1000)
+
+/* activation / output element formats */
+#define Q36MOE_FMT_F32  0
+#define Q36MOE_FMT_BF16 1
+
+/* debug taps (q36moe_ctx_copy_tap) */
+#define Q36MOE_TAP_TOPK_IDX  0  /* int32 [T][k]                         */
+#define Q36MOE_TAP_TOPK_W    1  /* f32   [T][k]                         */
+#define Q36MOE_TAP_XQ        2  /* u8    [T][d_model]  e4m3             */
+#define Q36MOE_TAP_XS        3  /* u8    [T][d_model/32] E8M0           */
+#define Q36MOE_TAP_EOFF      4  /* int32 [n_expert+1] sorted offsets    */
+#define Q36MOE_TAP_PERM      5  /* int32 [T*k] entry id per sorted slot */
+#define Q36MOE_TAP_POS       6  /* int32 [T*k] sorted slot per entry    */
+#define Q36MOE_TAP_HQ        7  /* u8    [T*k+T][d_ff] e4m3 SwiGLU rows */
+#define Q36MOE_TAP_HS        8  /* u8    [T*k+T][d_ff/32] E8M0          */
+#define Q36MOE_TAP_DNW       9  /* f32   [T*k+T][d_model] w * down rows */
+
+typedef struct q36moe_weights q36moe_weights;
+typedef struct q36moe_ctx q36moe_ctx;
+
+/* Library version string and the number of bytes one expert occupies on
+ * the device (gate+up+down, nibbles + E8M0). */
+const char *q36moe_version(void);
+size_t q36moe_expert_bytes(int d_model, int d_ff);
+
+/* Upload one layer's expert weights given as host GGUF block_mxfp4 arrays:
+ * gate/up [n_expert][d_ff][d_model/32], down [n_expert][d_model][d_ff/32]
+ * (17-byte blocks).  sh_* are the dense shared expert (same block layout,
+ * one matrix each, d_ff_sh rows) or all NULL with d_ff_sh = 0.  The blocks
+ * are repacked into the device fragment layout inside this call.
+ * Constraints: d_model and d_ff multiples of 512, d_ff_sh 0 or == d_ff,
+ * 1 <= n_expert <= 256.  E8M0 bytes of 255 (NaN in OCP MX) -> EINVAL. */
+int q36moe_weights_upload(const void *gate, const void *up, const void *down,
+                          const void *sh_gate, const void *sh_up, const void *sh_down,
+                          int n_expert, int d_model, int d_ff, int d_ff_sh,
+                          q36moe_weights **out);
+
+/* Allocate a weight set on the device without filling it; the caller fills
+ * the packed buffers returned by q36moe_weights_device_ptrs (e.g. with
+ * random bytes for synthetic benchmarks).  Packed layout per matrix:
+ * [M*K/2 nibble bytes][M*K/32 E8M0 bytes]; per expert stride for gate/up/down
+ * is the matrix size. */
+int q36moe_weights_alloc(int n_expert, int d_model, int d_ff, int d_ff_sh,
+                         q36moe_weights **out);
+int q36moe_weights_device_ptrs(const q36moe_weights *w, void **gate, void **up,
+                               void **down, void **sh_gate, void **sh_up,
+                               void **sh_down, size_t *gate_bytes, size_t *down_bytes);
+void q36moe_weights_free(q36moe_weights *w);
+
+/* Host-side repack of one [M][K] GGUF block_mxfp4 matrix into the packed
+ * device layout (and back).  Pure host code; used by upload and by tests. */
+int q36moe_pack_mxfp4(const void *gguf_blocks, int M, int K, void *packed);
+int q36moe_unpack_mxfp4(const void *packed, int M, int K, void *gguf_blocks);
+
+/* Context: per-stream scratch for up to max_tokens tokens.  All scratch is
+ * allocated here; q36moe_forward allocates nothing. */
+int q36moe_ctx_create(int max_tokens, int n_expert, int d_model, int d_ff,
+                      int top_k, void *stream, q36moe_ctx **out);
+int q36moe_ctx_set_stream(q36moe_ctx *c, void *stream);
+void q36moe_ctx_free(q36moe_ctx *c);
+
+/* The MoE layer.  x [T][d_model] (f32 or bf16, row stride d_model),
+ * logits [T][ld_logits] f32 (first n_expert columns used), shg [T] f32
+ * shared-expert gate logits or NULL, out [T][d_model] (f32 or bf16).
+ * out[t] = sum_s w[t][s] * E_{idx[t][s]}(x[t]) + sigmoid(shg[t]) * S(x[t]),
+ * E(x) = down . q8(silu(gate . q8(x)) * up . q8(x)), q8 = per-32 E8M0 +
+ * e4m3 quantisation, w = top-k softmax weights renormalised, times scale.
+ * Asynchronous on the context stream; T = 0 is a no-op. */
+int q36moe_forward(q36moe_ctx *c, const q36moe_weights *w,
+                   const void *x, int x_fmt, const float *logits, int ld_logits,
+                   const float *shg, int T, float scale, void *out, int out_fmt);
+
+/* Stage entry points (device pointers, asynchronous on `stream`). */
+int q36moe_router_topk(const float *logits, int T, int n_expert, int ld, int k,
+                       float scale, int renorm, int32_t *idx, float *wt, void *stream);
+int q36moe_quant_e4m3(const void *x, int x_fmt, int T, int K,
+                      uint8_t *xq, uint8_t *xs, void *stream);
+
+/* Copy one internal buffer of the last forward into dst (device pointer,
+ * at most `bytes`); *written receives the byte count. */
+int q36moe_ctx_copy_tap(q36moe_ctx *c, int tap, void *dst, size_t bytes, size_t *written);
+
+/* Per-stage timing of forward: when enabled, forward records HIP events
+ * around each kernel on the context stream and synchronises at its end;
+ * q36moe_ctx_stage_times adds up milliseconds per stage since the last
+ * reset (n_stages entries, names via q36moe_stage_name). */
+int q36moe_ctx_set_timing(q36moe_ctx *c, int on);
+int q36moe_ctx_stage_times(q36moe_ctx *c, double *ms, int *calls, int n_stages, int reset);
+const char *q36moe_stage_name(int stage);
+int q36moe_num_stages(void);
+
+/* One v_mfma_scale_f32_16x16x128_f8f6f4 on caller-packed operands:
+ * a, b: 64 lanes x 32 bytes; sa, sb: 64 lane scale dwords (byte 0 used);
+ * fmt_a / fmt_b: 0 e4m3, 1 e5m2, 2 e2m3, 3 e3m2, 4 e2m1; c: 64 x 4 floats. */
+int q36moe_probe_mfma(const void *a, const void *b, const uint32_t *sa,
+                      const uint32_t *sb, int fmt_a, int fmt_b, float *c, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

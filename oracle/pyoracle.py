@@ -1,0 +1,227 @@
+"""ctypes wrapper over oracle/liboracle.so (the C restatement of the q36 MoE
+arithmetic).  TEST INFRASTRUCTURE ONLY -- see oracle/q36moe_oracle.c."""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+REF_LIB_PATH = os.path.join(HERE, "_ref", "libref_dequant.so")
+
+_lib = None
+
+
+def build(ref=True):
+    """Compile liboracle.so (and _ref/ when the reference tree is present)."""
+    target = ["all"] if ref else ["liboracle.so"]
+    subprocess.run(["make", "-s", "-C", HERE] + target, check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build(ref=False)
+        L = ctypes.CDLL(LIB_PATH)
+        vp, i, f = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
+        L.or_e8m0.argtypes = [ctypes.c_uint8]
+        L.or_e8m0.restype = ctypes.c_double
+        L.or_e2m1.argtypes = [ctypes.c_uint8]
+        L.or_e2m1.restype = ctypes.c_double
+        L.or_e4m3_decode.argtypes = [ctypes.c_uint8]
+        L.or_e4m3_decode.restype = ctypes.c_float
+        L.or_e4m3_encode.argtypes = [ctypes.c_float]
+        L.or_e4m3_encode.restype = ctypes.c_uint8
+        L.or_quant_exp.argtypes = [ctypes.c_float]
+        L.or_quant_exp.restype = ctypes.c_int
+        L.or_deq_mxfp4_block.argtypes = [vp, vp]
+        L.or_deq_mxfp4_row.argtypes = [vp, i, vp]
+        L.or_quant_e4m3.argtypes = [vp, i, i, vp, vp]
+        L.or_dequant_e4m3.argtypes = [vp, vp, i, i, vp]
+        L.or_router_topk.argtypes = [vp, i, i, i, i, f, i, vp, vp]
+        L.or_sort.argtypes = [vp, i, i, vp, vp, vp]
+        L.or_gemv_mxfp4_f32.argtypes = [vp, i, i, vp, vp, vp]
+        L.or_gemv_mxfp4_f32_mt.argtypes = [vp, i, i, vp, vp, vp, i]
+        L.or_expert_h.argtypes = [vp, vp, i, i, vp, vp]
+        L.or_expert_down.argtypes = [vp, i, i, vp, vp]
+        L.or_moe_forward.argtypes = [vp, vp, vp, i, vp, i, i, f, i, vp, i, vp]
+        L.or_moe_forward_f32.argtypes = [vp, vp, vp, i, vp, i, i, f, vp, i]
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return ctypes.c_void_p(a.ctypes.data) if a is not None else None
+
+
+class _W(ctypes.Structure):
+    _fields_ = [("gate", ctypes.c_void_p), ("up", ctypes.c_void_p), ("down", ctypes.c_void_p),
+                ("sh_gate", ctypes.c_void_p), ("sh_up", ctypes.c_void_p), ("sh_down", ctypes.c_void_p),
+                ("n_expert", ctypes.c_int), ("d_model", ctypes.c_int), ("d_ff", ctypes.c_int),
+                ("d_ff_sh", ctypes.c_int)]
+
+
+def _wstruct(w):
+    keep = {k: np.ascontiguousarray(v, dtype=np.uint8) for k, v in w.items()}
+    E, FF, nb, _ = keep["gate"].shape
+    s = _W(_p(keep["gate"]), _p(keep["up"]), _p(keep["down"]),
+           _p(keep.get("sh_gate")), _p(keep.get("sh_up")), _p(keep.get("sh_down")),
+           E, nb * 32, FF, keep["sh_gate"].shape[0] if "sh_gate" in keep else 0)
+    return s, keep
+
+
+# ---- scalar / block helpers ----
+def e8m0(e):
+    return lib().or_e8m0(e)
+
+
+def e2m1(c):
+    return lib().or_e2m1(c)
+
+
+def e4m3_decode(b):
+    return lib().or_e4m3_decode(b)
+
+
+def e4m3_encode(v):
+    return lib().or_e4m3_encode(float(v))
+
+
+def e4m3_encode_array(v):
+    v = np.ascontiguousarray(v, dtype=np.float32).reshape(-1)
+    return np.array([lib().or_e4m3_encode(float(x)) for x in v], dtype=np.uint8)
+
+
+def e4m3_decode_table():
+    return np.array([lib().or_e4m3_decode(b) for b in range(256)], dtype=np.float32)
+
+
+def quant_exp(a):
+    return lib().or_quant_exp(float(a))
+
+
+def deq_mxfp4_row(blocks):
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    n = blocks.size // 17 * 32
+    out = np.empty(n, dtype=np.float32)
+    lib().or_deq_mxfp4_row(_p(blocks), n, _p(out))
+    return out
+
+
+def quant_e4m3(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    T, K = x.shape
+    xq = np.empty((T, K), dtype=np.uint8)
+    xs = np.empty((T, K // 32), dtype=np.uint8)
+    lib().or_quant_e4m3(_p(x), T, K, _p(xq), _p(xs))
+    return xq, xs
+
+
+def dequant_e4m3(xq, xs):
+    xq = np.ascontiguousarray(xq, dtype=np.uint8)
+    xs = np.ascontiguousarray(xs, dtype=np.uint8)
+    T, K = xq.shape
+    out = np.empty((T, K), dtype=np.float64)
+    lib().or_dequant_e4m3(_p(xq), _p(xs), T, K, _p(out))
+    return out
+
+
+def router_topk(logits, k=8, scale=1.0, renorm=True, n_expert=None):
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    T, ld = logits.shape
+    E = n_expert or ld
+    idx = np.empty((T, k), dtype=np.int32)
+    wt = np.empty((T, k), dtype=np.float64)
+    lib().or_router_topk(_p(logits), T, E, ld, k, scale, 1 if renorm else 0, _p(idx), _p(wt))
+    return idx, wt
+
+
+def sort_entries(idx, n_expert):
+    idx = np.ascontiguousarray(idx, dtype=np.int32).reshape(-1)
+    n = idx.size
+    off = np.empty(n_expert + 1, dtype=np.int32)
+    perm = np.empty(n, dtype=np.int32)
+    pos = np.empty(n, dtype=np.int32)
+    lib().or_sort(_p(idx), n, n_expert, _p(off), _p(perm), _p(pos))
+    return off, perm, pos
+
+
+def gemv_mxfp4(W, xq, xs, nthreads=1):
+    W = np.ascontiguousarray(W, dtype=np.uint8)
+    M, nb, _ = W.shape
+    K = nb * 32
+    xq = np.ascontiguousarray(xq, dtype=np.uint8).reshape(-1)
+    xs = np.ascontiguousarray(xs, dtype=np.uint8).reshape(-1)
+    y = np.empty(M, dtype=np.float32)
+    if nthreads > 1:
+        lib().or_gemv_mxfp4_f32_mt(_p(W), M, K, _p(xq), _p(xs), _p(y), nthreads)
+    else:
+        lib().or_gemv_mxfp4_f32(_p(W), M, K, _p(xq), _p(xs), _p(y))
+    return y
+
+
+def expert_h(gate_e, up_e, xd):
+    """fp64 SwiGLU rows of one expert for a dequantised input row."""
+    g = np.ascontiguousarray(gate_e, dtype=np.uint8)
+    u = np.ascontiguousarray(up_e, dtype=np.uint8)
+    xd = np.ascontiguousarray(xd, dtype=np.float64)
+    FF, nb, _ = g.shape
+    h = np.empty(FF, dtype=np.float64)
+    lib().or_expert_h(_p(g), _p(u), nb * 32, FF, _p(xd), _p(h))
+    return h
+
+
+def expert_down(down_e, hd):
+    d = np.ascontiguousarray(down_e, dtype=np.uint8)
+    hd = np.ascontiguousarray(hd, dtype=np.float64)
+    D, nb, _ = d.shape
+    y = np.empty(D, dtype=np.float64)
+    lib().or_expert_down(_p(d), D, nb * 32, _p(hd), _p(y))
+    return y
+
+
+def moe_forward(w, x, logits, shg=None, k=8, scale=1.0, act_mode=0, tokens=None):
+    """double [n_tok, d_model]; act_mode 0 = W4A8, 1 = W4A32."""
+    s, keep = _wstruct(w)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    T, D = x.shape
+    shg_a = np.ascontiguousarray(shg, dtype=np.float32) if shg is not None else None
+    tok = np.ascontiguousarray(tokens, dtype=np.int32) if tokens is not None else None
+    n = T if tok is None else tok.size
+    out = np.empty((n, D), dtype=np.float64)
+    lib().or_moe_forward(ctypes.byref(s), _p(x), _p(logits), logits.shape[1], _p(shg_a), T, k,
+                         scale, act_mode, _p(tok), n, _p(out))
+    return out
+
+
+def moe_forward_f32(w, x, logits, shg=None, k=8, scale=1.0, nthreads=1):
+    s, keep = _wstruct(w)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    T, D = x.shape
+    shg_a = np.ascontiguousarray(shg, dtype=np.float32) if shg is not None else None
+    out = np.empty((T, D), dtype=np.float32)
+    lib().or_moe_forward_f32(ctypes.byref(s), _p(x), _p(logits), logits.shape[1], _p(shg_a), T, k,
+                             scale, _p(out), nthreads)
+    return out
+
+
+# ---- the reference's own dequant, compiled from its header into _ref/ ----
+_ref = None
+
+
+def ref_lib():
+    """The reference's q36_deq_mxfp4 / q36_e8m0_half (oracle/_ref), or None."""
+    global _ref
+    if _ref is None and os.path.exists(REF_LIB_PATH):
+        L = ctypes.CDLL(REF_LIB_PATH)
+        L.ref_deq_mxfp4.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        L.ref_e8m0_half.argtypes = [ctypes.c_uint8]
+        L.ref_e8m0_half.restype = ctypes.c_float
+        L.ref_deq_row_mxfp4.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+        L.ref_sizeof_block_mxfp4.restype = ctypes.c_int
+        _ref = L
+    return _ref

@@ -1,0 +1,426 @@
+/* CPU oracle for the W4A8 MoE layer -- TEST INFRASTRUCTURE ONLY.
+ *
+ * A plain-C restatement of the q36 engine's MoE FFN arithmetic, used by
+ * tests/ (as the checker), __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg.  The product library never links or calls it.
+ *
+ * Pinning (what checks each function against something other than itself):
+ *   or_e8m0 / or_e2m1 / or_deq_mxfp4_*  -- the reference's own known answers
+ *       (test_dequant.c:51-61) and, exhaustively over all 16 codes x 256
+ *       exponents, the reference's q36_deq_mxfp4 compiled from its own
+ *       header (oracle/Makefile -> oracle/_ref/).
+ *   or_e4m3_encode / or_e4m3_decode     -- OCP FP8 closed forms (all 256
+ *       codes, every tie), and torch.float8_e4m3fn as an independent
+ *       library routine.
+ *   or_quant_exp / or_quant_e4m3        -- closed form of
+ *       q36_engine.cu:2421-2427 plus invariants (minimal scale, |q|<=448).
+ *   or_router_topk                      -- brute-force sort by
+ *       (logit desc, index asc) and fp64 softmax.
+ *   or_sort                             -- brute force + bijection /
+ *       histogram / scan invariants.
+ *   or_gemv_* / or_moe_forward          -- fp64 brute force on tiny shapes
+ *       and closed forms (rank-1 weights, single non-zero block, linearity
+ *       in the routing weights).
+ */
+#include "q36moe_oracle.h"
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ---------------------------------------------------------------------- */
+/* Scalars                                                                 */
+/* ---------------------------------------------------------------------- */
+
+/* E8M0 scale 2^(e-127).  The reference stores it halved next to a doubled
+ * E2M1 table (q36_dequant.cuh:84-103: e8m0_half(e)=2^(e-128), e<2 handled
+ * as fp32 denormals); the product table*half equals E2M1*2^(e-127) for all
+ * e in 0..254.  e=255 gives 2^128 here as in ggml (OCP calls it NaN). */
+double or_e8m0(uint8_t e) { return ldexp(1.0, (int)e - 127); }
+
+/* OCP E2M1: bit3 sign, bits2:1 exponent (bias 1), bit0 mantissa.
+ * Values {0,.5,1,1.5,2,3,4,6}; the reference's doubled table
+ * {0,1,2,3,4,6,8,12} (q36_dequant.cuh:84-88) is twice this. */
+double or_e2m1(uint8_t c) {
+    static const double mag[8] = {0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0};
+    double v = mag[c & 7];
+    return (c & 8) ? -v : v;
+}
+
+/* OCP E4M3FN decode: bias 7, no inf, S.1111.111 = NaN. */
+float or_e4m3_decode(uint8_t b) {
+    int s = b >> 7, e = (b >> 3) & 15, m = b & 7;
+    float v;
+    if (e == 15 && m == 7) return NAN;
+    if (e == 0) v = ldexpf((float)m, -9);
+    else        v = ldexpf((float)(8 + m), e - 10);
+    return s ? -v : v;
+}
+
+/* OCP E4M3FN encode, round-to-nearest-even, saturating to +-448 (the
+ * __NV_SATFINITE conversion the reference's __nv_fp8_e4m3 constructor
+ * performs, q36_engine.cu:2426).  NaN -> 0x7f (sign kept). */
+uint8_t or_e4m3_encode(float v) {
+    uint32_t u; memcpy(&u, &v, 4);
+    uint8_t sign = (uint8_t)((u >> 31) << 7);
+    uint32_t a = u & 0x7fffffffu;
+    if (a > 0x7f800000u) return sign | 0x7f;
+    if (a >= 0x43e00000u) return sign | 0x7e;          /* >= 448 */
+    if (a < 0x3c800000u) {                            /* < 2^-6: subnormal */
+        float f; memcpy(&f, &a, 4);
+        float q = rintf(f * 512.0f);                  /* units of 2^-9, RNE */
+        return sign | (uint8_t)q;                     /* q==8 -> 0x08 = 2^-6 */
+    }
+    int e = (int)(a >> 23) - 127;                     /* -6 .. 8 */
+    uint32_t m = a & 0x7fffffu;
+    uint32_t r = ((uint32_t)(e + 7) << 3) | (m >> 20);
+    uint32_t rb = (m >> 19) & 1u, sticky = m & 0x7ffffu, lsb = r & 1u;
+    if (rb && (sticky || lsb)) r++;
+    if (r > 0x7e) r = 0x7e;
+    return sign | (uint8_t)r;
+}
+
+/* Exponent of the per-32 activation scale: e2 = ceil(log2(amax/448)),
+ * clamped to [-127,127], -127 for an all-zero block
+ * (q36_engine.cu:2421-2423).  The quotient is the fp32 a/448 of the
+ * reference; its ceil(log2) is taken exactly from the binary exponent
+ * (a correctly rounded log2f can round 2^n(1+2^-23) down to n: that case
+ * differs by one scale step and is pinned in tests). */
+int or_quant_exp(float amax) {
+    if (!(amax > 0.0f)) return -127;
+    float q = amax / 448.0f;
+    int ex;
+    float f = frexpf(q, &ex);                         /* q = f*2^ex, f in [.5,1) */
+    int e2 = (f == 0.5f) ? ex - 1 : ex;
+    if (e2 < -127) e2 = -127;
+    if (e2 > 127) e2 = 127;
+    return e2;
+}
+
+/* 2^-e2 built from exponent bits as in q36_engine.cu:2424-2426 (e2=127
+ * yields 0.0 there, kept here). */
+static float inv_scale(int e2) {
+    uint32_t bits = (uint32_t)(127 - e2) << 23;
+    float f; memcpy(&f, &bits, 4);
+    return f;
+}
+
+/* ---------------------------------------------------------------------- */
+/* MXFP4 blocks                                                            */
+/* ---------------------------------------------------------------------- */
+
+/* Element order of q36_deq_mxfp4 (q36_dequant.cuh:106-113): element j is the
+ * low nibble of qs[j], element j+16 the high nibble. */
+void or_deq_mxfp4_block(const uint8_t *blk, float *out) {
+    double d = or_e8m0(blk[0]);
+    for (int j = 0; j < 16; j++) {
+        out[j]      = (float)(or_e2m1(blk[1 + j] & 15) * d);
+        out[j + 16] = (float)(or_e2m1(blk[1 + j] >> 4) * d);
+    }
+}
+
+void or_deq_mxfp4_row(const uint8_t *blocks, int n, float *out) {
+    for (int b = 0; b < n / 32; b++) or_deq_mxfp4_block(blocks + 17 * b, out + 32 * b);
+}
+
+/* ---------------------------------------------------------------------- */
+/* Activation quantiser: q36_engine.cu:2411-2428 (k_quant_e4m3)            */
+/* ---------------------------------------------------------------------- */
+void or_quant_e4m3(const float *X, int T, int K, uint8_t *Xq, uint8_t *Xs) {
+    int nb = K / 32;
+    for (int t = 0; t < T; t++)
+        for (int b = 0; b < nb; b++) {
+            const float *v = X + (size_t)t * K + b * 32;
+            float a = 0.0f;
+            for (int j = 0; j < 32; j++) a = fmaxf(a, fabsf(v[j]));
+            int e2 = or_quant_exp(a);
+            float mul = inv_scale(e2);
+            for (int j = 0; j < 32; j++)
+                Xq[(size_t)t * K + b * 32 + j] = or_e4m3_encode(v[j] * mul);
+            Xs[(size_t)t * nb + b] = (uint8_t)(127 + e2);
+        }
+}
+
+void or_dequant_e4m3(const uint8_t *Xq, const uint8_t *Xs, int T, int K, double *Xd) {
+    int nb = K / 32;
+    for (int t = 0; t < T; t++)
+        for (int k = 0; k < K; k++)
+            Xd[(size_t)t * K + k] = (double)or_e4m3_decode(Xq[(size_t)t * K + k]) *
+                                    or_e8m0(Xs[(size_t)t * nb + k / 32]);
+}
+
+/* ---------------------------------------------------------------------- */
+/* Router: q36_ops.cuh:397-431 (k_router_topk)                             */
+/* ---------------------------------------------------------------------- */
+/* k rounds of argmax with ties to the lower expert index (:416-423); the
+ * weight of a pick is exp(l-m)/sum_all (:424), then renormalised over the
+ * picks and multiplied by scale (:428-430).  Doubles throughout. */
+void or_router_topk(const float *logits, int T, int n_expert, int ld, int k,
+                    float scale, int renorm, int32_t *idx, double *wt) {
+    char *taken = (char *)malloc((size_t)n_expert);
+    for (int t = 0; t < T; t++) {
+        const float *l = logits + (size_t)t * ld;
+        double m = -1e30;
+        for (int j = 0; j < n_expert; j++) if (l[j] > m) m = l[j];
+        double s = 0.0;
+        for (int j = 0; j < n_expert; j++) s += exp((double)l[j] - m);
+        memset(taken, 0, (size_t)n_expert);
+        double ws = 0.0;
+        for (int r = 0; r < k; r++) {
+            int bj = -1; float bv = 0.0f;
+            for (int j = 0; j < n_expert; j++) {
+                if (taken[j]) continue;
+                if (bj < 0 || l[j] > bv) { bv = l[j]; bj = j; }
+            }
+            taken[bj] = 1;
+            idx[(size_t)t * k + r] = bj;
+            wt[(size_t)t * k + r] = exp((double)bv - m) / s;
+            ws += wt[(size_t)t * k + r];
+        }
+        for (int r = 0; r < k; r++)
+            wt[(size_t)t * k + r] = renorm ? wt[(size_t)t * k + r] / ws * scale
+                                           : wt[(size_t)t * k + r] * scale;
+    }
+    free(taken);
+}
+
+/* ---------------------------------------------------------------------- */
+/* Dispatch: the reference buckets entry ids t*8+s per expert with an       */
+/* atomic counter (q36_engine.cu:3387-3392), so order inside a bucket is     */
+/* unspecified; this build fixes it to ascending entry id.                  */
+/* ---------------------------------------------------------------------- */
+void or_sort(const int32_t *idx, int n, int n_expert,
+             int32_t *off, int32_t *perm, int32_t *pos) {
+    for (int e = 0; e <= n_expert; e++) off[e] = 0;
+    for (int i = 0; i < n; i++) off[idx[i] + 1]++;
+    for (int e = 0; e < n_expert; e++) off[e + 1] += off[e];
+    int32_t *fill = (int32_t *)malloc(sizeof(int32_t) * (size_t)(n_expert + 1));
+    memcpy(fill, off, sizeof(int32_t) * (size_t)(n_expert + 1));
+    for (int i = 0; i < n; i++) {
+        int p = fill[idx[i]]++;
+        perm[p] = i;
+        pos[i] = p;
+    }
+    free(fill);
+}
+
+/* ---------------------------------------------------------------------- */
+/* Config-1 CPU path: dequant + GEMV, fp32 accumulation.  The dequant is    */
+/* q36_deq_mxfp4 (q36_dequant.cuh:106-113) per row; the row dot follows     */
+/* the per-block order of dot_mxfp4_split (q36_ops.cuh:153-167).            */
+/* ---------------------------------------------------------------------- */
+static void gemv_rows(const uint8_t *W, int r0, int r1, int K,
+                      const float *x, float *y) {
+    float wr[32];
+    int nb = K / 32;
+    for (int r = r0; r < r1; r++) {
+        float acc = 0.0f;
+        const uint8_t *row = W + (size_t)r * nb * 17;
+        for (int b = 0; b < nb; b++) {
+            or_deq_mxfp4_block(row + 17 * b, wr);
+            float s = 0.0f;
+            for (int j = 0; j < 32; j++) s += wr[j] * x[b * 32 + j];
+            acc += s;
+        }
+        y[r] = acc;
+    }
+}
+
+static float *deq_x(const uint8_t *xq, const uint8_t *xs, int K) {
+    float *x = (float *)malloc(sizeof(float) * (size_t)K);
+    for (int k = 0; k < K; k++)
+        x[k] = or_e4m3_decode(xq[k]) * (float)or_e8m0(xs[k / 32]);
+    return x;
+}
+
+void or_gemv_mxfp4_f32(const uint8_t *W, int M, int K,
+                       const uint8_t *xq, const uint8_t *xs, float *y) {
+    float *x = deq_x(xq, xs, K);
+    gemv_rows(W, 0, M, K, x, y);
+    free(x);
+}
+
+void or_gemv_mxfp4_f32_mt(const uint8_t *W, int M, int K,
+                          const uint8_t *xq, const uint8_t *xs, float *y,
+                          int nthreads) {
+    float *x = deq_x(xq, xs, K);
+#ifdef _OPENMP
+    #pragma omp parallel num_threads(nthreads)
+    {
+        int nt = omp_get_num_threads(), id = omp_get_thread_num();
+        int r0 = (int)((long)M * id / nt), r1 = (int)((long)M * (id + 1) / nt);
+        gemv_rows(W, r0, r1, K, x, y);
+    }
+#else
+    (void)nthreads;
+    gemv_rows(W, 0, M, K, x, y);
+#endif
+    free(x);
+}
+
+/* ---------------------------------------------------------------------- */
+/* Whole layer                                                             */
+/* ---------------------------------------------------------------------- */
+static double silu_d(double g) { return g / (1.0 + exp(-g)); }
+static double sigm_d(double g) { return 1.0 / (1.0 + exp(-g)); }
+
+/* y[M] = W[M][K] . x  (GGUF MXFP4 rows, double accumulation). */
+static void mv_d(const uint8_t *W, int M, int K, const double *x, double *y) {
+    int nb = K / 32;
+    float wr[32];
+    for (int r = 0; r < M; r++) {
+        const uint8_t *row = W + (size_t)r * nb * 17;
+        double acc = 0.0;
+        for (int b = 0; b < nb; b++) {
+            or_deq_mxfp4_block(row + 17 * b, wr);
+            for (int j = 0; j < 32; j++) acc += (double)wr[j] * x[b * 32 + j];
+        }
+        y[r] = acc;
+    }
+}
+
+/* Quantise a float row with the activation rule, return dequantised doubles. */
+static void quant_roundtrip(const float *v, int K, double *out) {
+    uint8_t *q = (uint8_t *)malloc((size_t)K), *s = (uint8_t *)malloc((size_t)K / 32);
+    or_quant_e4m3(v, 1, K, q, s);
+    or_dequant_e4m3(q, s, 1, K, out);
+    free(q); free(s);
+}
+
+/* One SwiGLU expert: out = down . q(silu(gate.x) * up.x), following
+ * k_expert_gemv2 -> k_silu_mul_slots -> k_expert_gemv
+ * (q36_engine.cu:1610-1618) with the activation quantisation of the
+ * W4A8 prefill path (q36_engine.cu:2411-2428, :3437-3441) applied to x and
+ * to the SwiGLU output when act_mode==0. */
+static void expert_d(const uint8_t *g, const uint8_t *u, const uint8_t *d,
+                     int D, int FF, const double *xin, int act_mode, double *out) {
+    double *gv = (double *)malloc(sizeof(double) * (size_t)FF);
+    double *uv = (double *)malloc(sizeof(double) * (size_t)FF);
+    double *hd = (double *)malloc(sizeof(double) * (size_t)FF);
+    float *hf = (float *)malloc(sizeof(float) * (size_t)FF);
+    mv_d(g, FF, D, xin, gv);
+    mv_d(u, FF, D, xin, uv);
+    for (int f = 0; f < FF; f++) hf[f] = (float)(silu_d(gv[f]) * uv[f]);
+    if (act_mode == 0) quant_roundtrip(hf, FF, hd);
+    else for (int f = 0; f < FF; f++) hd[f] = hf[f];
+    mv_d(d, D, FF, hd, out);
+    free(gv); free(uv); free(hd); free(hf);
+}
+
+void or_expert_h(const uint8_t *gate, const uint8_t *up, int D, int FF,
+                 const double *x, double *h) {
+    double *u = (double *)malloc(sizeof(double) * (size_t)FF);
+    mv_d(gate, FF, D, x, h);
+    mv_d(up, FF, D, x, u);
+    for (int f = 0; f < FF; f++) h[f] = silu_d(h[f]) * u[f];
+    free(u);
+}
+
+void or_expert_down(const uint8_t *down, int D, int FF, const double *h, double *y) {
+    mv_d(down, D, FF, h, y);
+}
+
+void or_moe_forward(const or_weights *w, const float *x, const float *logits,
+                    int ld_logits, const float *shg, int T, int k,
+                    float scale, int act_mode, const int32_t *tokens,
+                    int n_tok, double *out) {
+    int D = w->d_model, FF = w->d_ff, E = w->n_expert;
+    size_t es = (size_t)FF * (D / 32) * 17;   /* gate/up bytes per expert */
+    size_t ds = (size_t)D * (FF / 32) * 17;   /* down bytes per expert */
+    if (!tokens) n_tok = T;
+    /* tokens are independent: the parallel loop changes no arithmetic */
+    #pragma omp parallel for schedule(dynamic, 1)
+    for (int i = 0; i < n_tok; i++) {
+        double *xd = (double *)malloc(sizeof(double) * (size_t)D);
+        double *y = (double *)malloc(sizeof(double) * (size_t)D);
+        int32_t idx[64];
+        double wt[64];
+        int t = tokens ? tokens[i] : i;
+        const float *xt = x + (size_t)t * D;
+        if (act_mode == 0) quant_roundtrip(xt, D, xd);
+        else for (int j = 0; j < D; j++) xd[j] = xt[j];
+        or_router_topk(logits + (size_t)t * ld_logits, 1, E, ld_logits, k, scale, 1, idx, wt);
+        double *o = out + (size_t)i * D;
+        for (int j = 0; j < D; j++) o[j] = 0.0;
+        /* sum over slots in top-k order, then the gated shared expert
+         * (k_moe_combine, q36_engine.cu:784-791; k_moe_combine_pf :3393-3401) */
+        for (int s = 0; s < k; s++) {
+            int e = idx[s];
+            expert_d(w->gate + es * e, w->up + es * e, w->down + ds * e, D, FF, xd, act_mode, y);
+            for (int j = 0; j < D; j++) o[j] += wt[s] * y[j];
+        }
+        if (shg && w->sh_gate) {
+            expert_d(w->sh_gate, w->sh_up, w->sh_down, D, w->d_ff_sh, xd, act_mode, y);
+            double gsh = sigm_d((double)shg[t]);
+            for (int j = 0; j < D; j++) o[j] += gsh * y[j];
+        }
+        free(xd); free(y);
+    }
+}
+
+/* ---------------------------------------------------------------------- */
+/* fp32 layer forward: the timed CPU baseline.                             */
+/* ---------------------------------------------------------------------- */
+static void mv_f(const uint8_t *W, int M, int K, const float *x, float *y,
+                 int nthreads) {
+#ifdef _OPENMP
+    #pragma omp parallel num_threads(nthreads)
+    {
+        int nt = omp_get_num_threads(), id = omp_get_thread_num();
+        int r0 = (int)((long)M * id / nt), r1 = (int)((long)M * (id + 1) / nt);
+        gemv_rows(W, r0, r1, K, x, y);
+    }
+#else
+    (void)nthreads;
+    gemv_rows(W, 0, M, K, x, y);
+#endif
+}
+
+static void quant_roundtrip_f(const float *v, int K, float *out) {
+    uint8_t *q = (uint8_t *)malloc((size_t)K), *s = (uint8_t *)malloc((size_t)K / 32);
+    or_quant_e4m3(v, 1, K, q, s);
+    for (int j = 0; j < K; j++) out[j] = or_e4m3_decode(q[j]) * (float)or_e8m0(s[j / 32]);
+    free(q); free(s);
+}
+
+void or_moe_forward_f32(const or_weights *w, const float *x, const float *logits,
+                        int ld_logits, const float *shg, int T, int k,
+                        float scale, float *out, int nthreads) {
+    int D = w->d_model, FF = w->d_ff, E = w->n_expert;
+    int FFm = FF > w->d_ff_sh ? FF : w->d_ff_sh;
+    size_t es = (size_t)FF * (D / 32) * 17, ds = (size_t)D * (FF / 32) * 17;
+    float *xf = (float *)malloc(sizeof(float) * (size_t)D);
+    float *g = (float *)malloc(sizeof(float) * (size_t)FFm);
+    float *u = (float *)malloc(sizeof(float) * (size_t)FFm);
+    float *h = (float *)malloc(sizeof(float) * (size_t)FFm);
+    float *y = (float *)malloc(sizeof(float) * (size_t)D);
+    int32_t *idx = (int32_t *)malloc(sizeof(int32_t) * (size_t)k);
+    double *wt = (double *)malloc(sizeof(double) * (size_t)k);
+    for (int t = 0; t < T; t++) {
+        quant_roundtrip_f(x + (size_t)t * D, D, xf);
+        or_router_topk(logits + (size_t)t * ld_logits, 1, E, ld_logits, k, scale, 1, idx, wt);
+        float *o = out + (size_t)t * D;
+        for (int j = 0; j < D; j++) o[j] = 0.0f;
+        int nexp = k + ((shg && w->sh_gate) ? 1 : 0);
+        for (int s = 0; s < nexp; s++) {
+            const uint8_t *G, *U, *Dn; int F; float ws;
+            if (s < k) {
+                int e = idx[s];
+                G = w->gate + es * e; U = w->up + es * e; Dn = w->down + ds * e;
+                F = FF; ws = (float)wt[s];
+            } else {
+                G = w->sh_gate; U = w->sh_up; Dn = w->sh_down; F = w->d_ff_sh;
+                ws = 1.0f / (1.0f + expf(-shg[t]));
+            }
+            mv_f(G, F, D, xf, g, nthreads);
+            mv_f(U, F, D, xf, u, nthreads);
+            for (int f = 0; f < F; f++) h[f] = g[f] / (1.0f + expf(-g[f])) * u[f];
+            quant_roundtrip_f(h, F, h);
+            mv_f(Dn, D, F, h, y, nthreads);
+            for (int j = 0; j < D; j++) o[j] += ws * y[j];
+        }
+    }
+    free(xf); free(g); free(u); free(h); free(y); free(idx); free(wt);
+}

@@ -1,0 +1,971 @@
+// q36moe: W4A8 (MXFP4 weight x FP8-e4m3 activation) mixture-of-experts
+// layer for MI355X (gfx950).  Kernels + the C ABI declared in q36moe.h.
+//
+// Pipeline of one forward (all on the context stream, no host syncs):
+//   k_route    one wavefront per token: softmax top-k + renormalised weights
+//              (q36_ops.cuh:397-431), FP8 quantisation of x with per-32
+//              E8M0 scales (q36_engine.cu:2411-2428), and per-block expert
+//              histograms + in-block ranks for the sort.
+//   k_scan     one workgroup: per-expert offsets (exclusive scans in LDS),
+//              a stable scatter of entry ids t*k+s by expert (the
+//              deterministic replacement of k_moe_dispatch,
+//              q36_engine.cu:3387-3392) and the ragged tile list.
+//   k_expert_gemm<GATEUP>  gate and up rows of one expert x one token tile on
+//              v_mfma_scale_f32_16x16x128_f8f6f4 (E2M1 weights straight from
+//              HBM in fragment order, e4m3 activations staged in LDS), fused
+//              SwiGLU and FP8 re-quantisation of h (q36_engine.cu:3436-3450).
+//   k_expert_gemm<DOWN>    down rows x token tile, scaled by the routing
+//              weight (q36_engine.cu:3451-3463).
+//   k_combine  out[t] = sum_s (w*down)[t,s] + (sigmoid(shg)*shared)[t] in slot
+//              order, bf16 or f32 (q36_engine.cu:784-791, :3393-3401).
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdlib>
+#include <cstring>
+#include <new>
+#include <type_traits>
+
+#include "q36moe.h"
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+namespace {
+
+constexpr int kMaxExperts = 256;
+constexpr int kMaxTopK = 8;
+constexpr int kRouteTPB = 64;      // tokens per k_route workgroup
+constexpr int kRouteThreads = 1024;
+constexpr int kScanThreads = 1024;
+constexpr int kLdsRow = 144;       // LDS row stride of one 128-byte K-step slice
+
+// ---------------------------------------------------------------------------
+// scalar formats
+// ---------------------------------------------------------------------------
+
+// OCP E4M3FN, round-to-nearest-even, saturating at +-448, NaN -> 0x7f.
+__device__ __forceinline__ uint32_t e4m3_encode(float v) {
+    const uint32_t u = __float_as_uint(v);
+    const uint32_t sign = (u >> 24) & 0x80u;
+    const uint32_t a = u & 0x7fffffffu;
+    if (a > 0x7f800000u) return sign | 0x7fu;
+    if (a >= 0x43e00000u) return sign | 0x7eu;
+    if (a < 0x3c800000u) {
+        const float q = __builtin_rintf(__uint_as_float(a) * 512.0f);
+        return sign | (uint32_t)q;
+    }
+    uint32_t r = (((a >> 23) - 120u) << 3) | ((a >> 20) & 7u);
+    const uint32_t rb = (a >> 19) & 1u, sticky = a & 0x7ffffu;
+    r += rb & ((sticky != 0u) | (r & 1u));
+    return sign | (r > 0x7eu ? 0x7eu : r);
+}
+
+// e2 = ceil(log2(amax/448)) from the binary exponent of the fp32 quotient,
+// clamped to [-127, 127]; -127 for an all-zero block.
+__device__ __forceinline__ int quant_exp(float amax) {
+    if (!(amax > 0.0f)) return -127;
+    const float q = amax / 448.0f;
+    int ex;
+    const float f = frexpf(q, &ex);
+    int e2 = (f == 0.5f) ? ex - 1 : ex;
+    e2 = e2 < -127 ? -127 : e2;
+    return e2 > 127 ? 127 : e2;
+}
+
+// 2^-e2 assembled from exponent bits (0.0 for e2 = 127, as in the reference).
+__device__ __forceinline__ float inv_scale(int e2) {
+    return __uint_as_float((uint32_t)(127 - e2) << 23);
+}
+
+__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
+    const uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
+
+// v_mfma_scale_f32_16x16x128_f8f6f4, A = E2M1 (cbsz 4), B = E4M3 (blgp 0).
+// Operand layout on gfx950 (measured with q36moe_probe_mfma):
+//   A (E2M1, 4 VGPRs): lane L = row L%16, 32 consecutive K 32*(L/16).. with
+//       element j in nibble j (low nibble first).
+//   B (E4M3, 8 VGPRs): lane L = column L%16; bytes 0-15 hold K 16q..16q+15,
+//       bytes 16-31 hold K 64+16q..64+16q+15, q = L/16.
+//   scales: byte 0 of sa / sb; K block kb (K 32kb..32kb+31) is scaled by the
+//       values of lane group kb (A: lane row+16kb, B: lane col+16kb).
+//   C: lane L holds rows 4*(L/16)+i, i = 0..3, of column L%16.
+//
+// Scale operands are never computed by VALU right before the MFMA: the A
+// scale dword is used as loaded with the byte picked by op_sel (SEL), the B
+// scale comes from an LDS byte load.  A VALU-shifted scale register issued
+// two wait states before v_mfma_scale was read stale on gfx950 (inf/NaN
+// from garbage E8M0 bytes).
+template <int SEL>
+__device__ __forceinline__ v4f mfma_f4xf8(const v8i &a, const v8i &b, const v4f &c,
+                                          int sa, int sb) {
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 4, 0, SEL, sa, 0, sb);
+}
+
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<I + 1, N>(f);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// routing + activation quantisation
+// ---------------------------------------------------------------------------
+
+// One wavefront routes one token.  Lane l holds logits l, l+64, l+128,
+// l+192.  k rounds of wave argmax, ties to the lower expert index
+// (q36_ops.cuh:416-423).  Weight = exp(l-m)/sum_all, renormalised over the
+// k picks and scaled (q36_ops.cuh:424-430).  Lane 0 writes idx/wt.
+__device__ void route_token(const float *__restrict__ l, int E, int k, float scale,
+                            int renorm, int lane, int32_t *idx, float *wt, int *lds_ent) {
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int e = lane + 64 * j;
+        v[j] = e < E ? l[e] : -INFINITY;
+    }
+    float m = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) s += (lane + 64 * j < E) ? expf(v[j] - m) : 0.0f;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+    uint32_t taken = 0;
+    float wr[kMaxTopK];
+    int ir[kMaxTopK];
+    float wsum = 0.0f;
+    for (int r = 0; r < k; r++) {
+        float bv = -INFINITY;
+        int bi = -1;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int e = lane + 64 * j;
+            if (e < E && !((taken >> j) & 1u) && (bi < 0 || v[j] > bv)) {
+                bv = v[j];
+                bi = e;
+            }
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(bv, o, 64);
+            const int oi = __shfl_xor(bi, o, 64);
+            if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+        if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+        const float w = expf(bv - m) / s;
+        wr[r] = w;
+        ir[r] = bi;
+        wsum += w;
+    }
+    if (lane == 0) {
+        for (int r = 0; r < k; r++) {
+            idx[r] = ir[r];
+            wt[r] = renorm ? wr[r] / wsum * scale : wr[r] * scale;
+            if (lds_ent) lds_ent[r] = ir[r];
+        }
+    }
+}
+
+// Quantise one 32-element block (per-32 E8M0 + e4m3), q36_engine.cu:2411-2428.
+__device__ __forceinline__ void quant_block32(const void *__restrict__ x, int x_fmt,
+                                              size_t off, uint8_t *__restrict__ q,
+                                              uint8_t *__restrict__ s) {
+    float v[32];
+    if (x_fmt == Q36MOE_FMT_F32) {
+        const float4 *p = reinterpret_cast<const float4 *>(static_cast<const float *>(x) + off);
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float4 t = p[i];
+            v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
+        }
+    } else {
+        const uint4 *p = reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(x) + off);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint4 t = p[i];
+            const uint32_t w[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                v[8 * i + 2 * j] = __uint_as_float(w[j] << 16);
+                v[8 * i + 2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+            }
+        }
+    }
+    float a = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; i++) a = fmaxf(a, fabsf(v[i]));
+    const int e2 = quant_exp(a);
+    const float mul = inv_scale(e2);
+    uint32_t w[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+        w[i] = e4m3_encode(v[4 * i] * mul) | (e4m3_encode(v[4 * i + 1] * mul) << 8) |
+               (e4m3_encode(v[4 * i + 2] * mul) << 16) | (e4m3_encode(v[4 * i + 3] * mul) << 24);
+    uint4 *qo = reinterpret_cast<uint4 *>(q);
+    qo[0] = make_uint4(w[0], w[1], w[2], w[3]);
+    qo[1] = make_uint4(w[4], w[5], w[6], w[7]);
+    *s = (uint8_t)(127 + e2);
+}
+
+struct RouteArgs {
+    const float *logits; int ld; int T; int E; int k; float scale;
+    const void *x; int x_fmt; int D;
+    int32_t *idx; float *wt; uint8_t *xq; uint8_t *xs;
+    int32_t *blk_cnt; int32_t *rank;
+};
+
+__global__ __launch_bounds__(kRouteThreads) void k_route(RouteArgs A) {
+    __shared__ int ent[kRouteTPB * kMaxTopK];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int t0 = blockIdx.x * kRouteTPB;
+    const int nb32 = A.D / 32;
+    for (int tl = wave; tl < kRouteTPB; tl += kRouteThreads / 64) {
+        const int t = t0 + tl;
+        if (t >= A.T) break;
+        route_token(A.logits + (size_t)t * A.ld, A.E, A.k, A.scale, 1, lane,
+                    A.idx + (size_t)t * A.k, A.wt + (size_t)t * A.k, ent + tl * A.k);
+        for (int b = lane; b < nb32; b += 64)
+            quant_block32(A.x, A.x_fmt, (size_t)t * A.D + (size_t)b * 32,
+                          A.xq + (size_t)t * A.D + (size_t)b * 32, A.xs + (size_t)t * nb32 + b);
+    }
+    __syncthreads();
+    const int ntok = min(kRouteTPB, A.T - t0);
+    const int nent = ntok * A.k;
+    // in-block rank of each entry among earlier entries of the same expert
+    for (int i = threadIdx.x; i < nent; i += kRouteThreads) {
+        const int e = ent[i];
+        int r = 0;
+        for (int j = 0; j < i; j++) r += (ent[j] == e);
+        A.rank[(size_t)t0 * A.k + i] = r;
+    }
+    // per-block histogram
+    for (int e = threadIdx.x; e < A.E; e += kRouteThreads) {
+        int c = 0;
+        for (int j = 0; j < nent; j++) c += (ent[j] == e);
+        A.blk_cnt[(size_t)blockIdx.x * A.E + e] = c;
+    }
+}
+
+__global__ __launch_bounds__(256) void k_topk(const float *logits, int T, int E, int ld, int k,
+                                             float scale, int renorm, int32_t *idx, float *wt) {
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= T) return;
+    route_token(logits + (size_t)t * ld, E, k, scale, renorm, threadIdx.x & 63,
+                idx + (size_t)t * k, wt + (size_t)t * k, nullptr);
+}
+
+__global__ __launch_bounds__(256) void k_quant(const void *x, int x_fmt, int T, int K,
+                                              uint8_t *xq, uint8_t *xs) {
+    const long nblk = (long)T * (K / 32);
+    const long b = (long)blockIdx.x * 256 + threadIdx.x;
+    if (b >= nblk) return;
+    quant_block32(x, x_fmt, (size_t)b * 32, xq + (size_t)b * 32, xs + b);
+}
+
+// ---------------------------------------------------------------------------
+// sort: offsets, stable scatter, tile list
+// ---------------------------------------------------------------------------
+struct ScanArgs {
+    const int32_t *blk_cnt; int nb; int E; int T; int k;
+    const int32_t *idx; const float *wt; const int32_t *rank; const float *shg;
+    int tn;
+    int32_t *blk_off; int32_t *e_off; int32_t *perm; int32_t *pos;
+    int32_t *row_tok; float *row_w; int4 *tiles; int32_t *ntiles;
+};
+
+__global__ __launch_bounds__(kScanThreads) void k_scan(ScanArgs A) {
+    __shared__ int s_cnt[kMaxExperts];
+    __shared__ int s_off[kMaxExperts + 1];
+    __shared__ int s_toff[kMaxExperts + 2];
+    const int tid = threadIdx.x;
+    for (int e = tid; e < A.E; e += kScanThreads) {
+        int run = 0;
+        for (int b = 0; b < A.nb; b++) {
+            const int c = A.blk_cnt[(size_t)b * A.E + e];
+            A.blk_off[(size_t)b * A.E + e] = run;
+            run += c;
+        }
+        s_cnt[e] = run;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        int o = 0, to = 0;
+        for (int e = 0; e < A.E; e++) {
+            s_off[e] = o;
+            s_toff[e] = to;
+            o += s_cnt[e];
+            to += (s_cnt[e] + A.tn - 1) / A.tn;
+        }
+        s_off[A.E] = o;
+        s_toff[A.E] = to;
+        const int nsh = A.shg ? (A.T + A.tn - 1) / A.tn : 0;
+        s_toff[A.E + 1] = to + nsh;
+        *A.ntiles = to + nsh;
+    }
+    __syncthreads();
+    const int n = A.T * A.k;
+    for (int e = tid; e <= A.E; e += kScanThreads) A.e_off[e] = s_off[e];
+    for (int i = tid; i < n; i += kScanThreads) {
+        const int t = i / A.k;
+        const int b = t / kRouteTPB;
+        const int e = A.idx[i];
+        const int p = s_off[e] + A.blk_off[(size_t)b * A.E + e] + A.rank[i];
+        A.perm[p] = i;
+        A.pos[i] = p;
+        A.row_tok[p] = t;
+        A.row_w[p] = A.wt[i];
+    }
+    if (A.shg) {
+        for (int t = tid; t < A.T; t += kScanThreads) {
+            A.row_tok[n + t] = t;
+            A.row_w[n + t] = 1.0f / (1.0f + expf(-A.shg[t]));
+        }
+    }
+    for (int e = tid; e < A.E; e += kScanThreads) {
+        const int c = s_cnt[e];
+        for (int j = 0; j * A.tn < c; j++) {
+            const int p0 = s_off[e] + j * A.tn;
+            A.tiles[s_toff[e] + j] = make_int4(e, p0, min(p0 + A.tn, s_off[e] + c), 0);
+        }
+    }
+    if (A.shg) {
+        const int base = s_toff[A.E];
+        for (int j = tid; j * A.tn < A.T; j += kScanThreads) {
+            const int p0 = n + j * A.tn;
+            A.tiles[base + j] = make_int4(A.E, p0, min(p0 + A.tn, n + A.T), 0);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// grouped expert GEMM on scaled MFMA
+// ---------------------------------------------------------------------------
+enum { MODE_GATEUP = 0, MODE_DOWN = 1 };
+
+struct GemmArgs {
+    const uint8_t *wa, *wb;   // routed experts: gate/up (GATEUP) or down (DOWN)
+    const uint8_t *sa, *sb;   // shared expert matrices (tile.x == E)
+    size_t wstride;           // bytes per expert matrix
+    int E, M;                 // routed experts, rows per matrix
+    const int4 *tiles; const int32_t *ntiles;
+    const uint8_t *bq, *bs;   // B rows: x by token (GATEUP) / h by sorted slot (DOWN)
+    const int32_t *row_tok; const float *row_w;
+    uint8_t *hq, *hs;         // GATEUP output rows (sorted slot)
+    float *dnw;               // DOWN output rows (sorted slot), weighted
+    int ldo;                  // output row length
+};
+
+// Workgroup = 4 waves arranged WM x WN; each wave owns TM row tiles (per
+// matrix) x TNW token tiles of 16.  Rows per workgroup = WM*TM*16, tokens =
+// WN*TNW*16.  KD = reduction length (d_model for gate/up, d_ff for down).
+template <int MODE, int WM, int WN, int TM, int TNW, int KD>
+__global__ __launch_bounds__(256) void k_expert_gemm(GemmArgs A) {
+    static_assert(WM * WN == 4, "four waves");
+    static_assert(MODE != MODE_GATEUP || TM == 2, "gate/up waves own one 32-row h block");
+    constexpr int NMAT = MODE == MODE_GATEUP ? 2 : 1;
+    constexpr int TN = WN * TNW * 16;
+    constexpr int ROWS = WM * TM * 16;
+    constexpr int NKT = KD / 128;
+    constexpr int NSD = NKT / 4;
+    static_assert(KD % 512 == 0, "K multiple of 512");
+
+    __shared__ __align__(16) uint8_t sB[TN * kLdsRow];
+    __shared__ uint32_t sS[TN];      // 4 E8M0 bytes (K blocks of this K-step) per row
+    __shared__ int sRow[TN];
+
+    const int ti = blockIdx.x;
+    if (ti >= *A.ntiles) return;
+    const int4 tile = A.tiles[ti];
+    const int e = tile.x, p0 = tile.y, p1 = tile.z;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave % WM, wn = wave / WM;
+    const int rb = blockIdx.y * ROWS;
+
+    const uint8_t *W[NMAT];
+    W[0] = e < A.E ? A.wa + (size_t)e * A.wstride : A.sa;
+    if constexpr (NMAT == 2) W[1] = e < A.E ? A.wb + (size_t)e * A.wstride : A.sb;
+    const size_t nib_bytes = (size_t)A.M * KD / 2;
+
+    for (int i = tid; i < TN; i += 256) {
+        const int p = p0 + i;
+        sRow[i] = p < p1 ? (MODE == MODE_GATEUP ? A.row_tok[p] : p) : -1;
+    }
+
+    uint32_t sa[NMAT][TM][NSD];
+#pragma unroll
+    for (int m = 0; m < NMAT; m++)
+#pragma unroll
+        for (int tm = 0; tm < TM; tm++) {
+            const int mt = (rb >> 4) + wm * TM + tm;
+            const uint32_t *sp =
+                reinterpret_cast<const uint32_t *>(W[m] + nib_bytes + ((size_t)mt * 64 + lane) * NKT);
+#pragma unroll
+            for (int d = 0; d < NSD; d++) sa[m][tm][d] = sp[d];
+        }
+
+    v4f acc[NMAT][TM][TNW];
+#pragma unroll
+    for (int m = 0; m < NMAT; m++)
+#pragma unroll
+        for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+            for (int n = 0; n < TNW; n++) acc[m][tm][n] = v4f{0.f, 0.f, 0.f, 0.f};
+    __syncthreads();
+
+    const uint8_t *sSb = reinterpret_cast<const uint8_t *>(sS);
+    static_for<0, NKT>([&](auto KT) {
+        constexpr int kt = decltype(KT)::value;
+        for (int c = tid; c < TN * 8; c += 256) {
+            const int r = c >> 3, q = c & 7;
+            const int row = sRow[r];
+            uint4 v = make_uint4(0u, 0u, 0u, 0u);
+            if (row >= 0)
+                v = *reinterpret_cast<const uint4 *>(A.bq + (size_t)row * KD + kt * 128 + q * 16);
+            *reinterpret_cast<uint4 *>(sB + r * kLdsRow + q * 16) = v;
+        }
+        for (int r = tid; r < TN; r += 256) {
+            const int row = sRow[r];
+            sS[r] = row >= 0
+                        ? *reinterpret_cast<const uint32_t *>(A.bs + (size_t)row * (KD / 32) + kt * 4)
+                        : 0x7f7f7f7fu;
+        }
+        v8i a[NMAT][TM];
+#pragma unroll
+        for (int m = 0; m < NMAT; m++)
+#pragma unroll
+            for (int tm = 0; tm < TM; tm++) {
+                const int mt = (rb >> 4) + wm * TM + tm;
+                const uint4 q = *reinterpret_cast<const uint4 *>(
+                    W[m] + ((size_t)mt * NKT + kt) * 1024 + (size_t)lane * 16);
+                a[m][tm] = v8i{(int)q.x, (int)q.y, (int)q.z, (int)q.w, 0, 0, 0, 0};
+            }
+        __syncthreads();
+#pragma unroll
+        for (int n = 0; n < TNW; n++) {
+            // e4m3 operand: lane group q carries K 16q..16q+15 in bytes 0-15 and
+            // K 64+16q..64+16q+15 in bytes 16-31; the scale of physical K block
+            // kb (32 values) is read from lane group kb.
+            const int r = (wn * TNW + n) * 16 + (lane & 15);
+            const uint8_t *bp = sB + r * kLdsRow + (lane >> 4) * 16;
+            const uint4 b0 = *reinterpret_cast<const uint4 *>(bp);
+            const uint4 b1 = *reinterpret_cast<const uint4 *>(bp + 64);
+            const v8i b = v8i{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w,
+                              (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+            const int sbv = sSb[r * 4 + (lane >> 4)];
+#pragma unroll
+            for (int m = 0; m < NMAT; m++)
+#pragma unroll
+                for (int tm = 0; tm < TM; tm++)
+                    acc[m][tm][n] = mfma_f4xf8<kt & 3>(a[m][tm], b, acc[m][tm][n],
+                                                       (int)sa[m][tm][kt >> 2], sbv);
+        }
+        __syncthreads();
+    });
+
+    if constexpr (MODE == MODE_GATEUP) {
+        const int ffb = rb + wm * 32;   // this wave's 32-row h block
+#pragma unroll
+        for (int n = 0; n < TNW; n++) {
+            float h[2][4];
+            float amax = 0.0f;
+#pragma unroll
+            for (int tm = 0; tm < 2; tm++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    h[tm][i] = silu(acc[0][tm][n][i]) * acc[1][tm][n][i];
+                    amax = fmaxf(amax, fabsf(h[tm][i]));
+                }
+            amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+            amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+            const int e2 = quant_exp(amax);
+            const float mul = inv_scale(e2);
+            const int p = p0 + (wn * TNW + n) * 16 + (lane & 15);
+            if (p < p1) {
+#pragma unroll
+                for (int tm = 0; tm < 2; tm++) {
+                    const uint32_t w = e4m3_encode(h[tm][0] * mul) |
+                                       (e4m3_encode(h[tm][1] * mul) << 8) |
+                                       (e4m3_encode(h[tm][2] * mul) << 16) |
+                                       (e4m3_encode(h[tm][3] * mul) << 24);
+                    *reinterpret_cast<uint32_t *>(A.hq + (size_t)p * A.ldo + ffb + tm * 16 +
+                                                  4 * (lane >> 4)) = w;
+                }
+                if (lane < 16) A.hs[(size_t)p * (A.ldo / 32) + ffb / 32] = (uint8_t)(127 + e2);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int n = 0; n < TNW; n++) {
+            const int p = p0 + (wn * TNW + n) * 16 + (lane & 15);
+            if (p < p1) {
+                const float w = A.row_w[p];
+#pragma unroll
+                for (int tm = 0; tm < TM; tm++) {
+                    const int row = rb + (wm * TM + tm) * 16 + 4 * (lane >> 4);
+                    const v4f c = acc[0][tm][n];
+                    *reinterpret_cast<float4 *>(A.dnw + (size_t)p * A.ldo + row) =
+                        make_float4(c[0] * w, c[1] * w, c[2] * w, c[3] * w);
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// combine
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_combine(const float *__restrict__ dnw,
+                                                const int32_t *__restrict__ pos, int T, int k,
+                                                int D, int has_sh, void *out, int out_fmt) {
+    const int t = blockIdx.x;
+    const int n = T * k;
+    for (int j = threadIdx.x * 4; j < D; j += 256 * 4) {
+        float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int s = 0; s < k; s++) {
+            const int p = pos[(size_t)t * k + s];
+            const float4 v = *reinterpret_cast<const float4 *>(dnw + (size_t)p * D + j);
+            a.x += v.x; a.y += v.y; a.z += v.z; a.w += v.w;
+        }
+        if (has_sh) {
+            const float4 v = *reinterpret_cast<const float4 *>(dnw + (size_t)(n + t) * D + j);
+            a.x += v.x; a.y += v.y; a.z += v.z; a.w += v.w;
+        }
+        if (out_fmt == Q36MOE_FMT_F32) {
+            *reinterpret_cast<float4 *>(static_cast<float *>(out) + (size_t)t * D + j) = a;
+        } else {
+            const uint32_t lo = f32_to_bf16(a.x) | (f32_to_bf16(a.y) << 16);
+            const uint32_t hi = f32_to_bf16(a.z) | (f32_to_bf16(a.w) << 16);
+            *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(out) + (size_t)t * D + j) =
+                make_uint2(lo, hi);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// calibration probe: one scaled MFMA on caller-packed lane operands
+// ---------------------------------------------------------------------------
+template <int FA, int FB>
+__global__ void k_probe(const v8i *a, const v8i *b, const uint32_t *sa, const uint32_t *sb,
+                        v4f *c) {
+    const int l = threadIdx.x;
+    v4f acc = {0.f, 0.f, 0.f, 0.f};
+    acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a[l], b[l], acc, FA, FB, 0,
+                                                           (int)sa[l], 0, (int)sb[l]);
+    c[l] = acc;
+}
+
+template <int FA>
+hipError_t launch_probe_b(int fb, const v8i *a, const v8i *b, const uint32_t *sa,
+                          const uint32_t *sb, v4f *c, hipStream_t s) {
+    switch (fb) {
+        case 0: hipLaunchKernelGGL((k_probe<FA, 0>), dim3(1), dim3(64), 0, s, a, b, sa, sb, c); break;
+        case 1: hipLaunchKernelGGL((k_probe<FA, 1>), dim3(1), dim3(64), 0, s, a, b, sa, sb, c); break;
+        case 2: hipLaunchKernelGGL((k_probe<FA, 2>), dim3(1), dim3(64), 0, s, a, b, sa, sb, c); break;
+        case 3: hipLaunchKernelGGL((k_probe<FA, 3>), dim3(1), dim3(64), 0, s, a, b, sa, sb, c); break;
+        default: hipLaunchKernelGGL((k_probe<FA, 4>), dim3(1), dim3(64), 0, s, a, b, sa, sb, c); break;
+    }
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+enum Stage { ST_ROUTE = 0, ST_SCAN, ST_GATEUP, ST_DOWN, ST_COMBINE, ST_COUNT };
+const char *const kStageNames[ST_COUNT] = {"route", "scan", "gateup", "down", "combine"};
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+}  // namespace
+
+struct q36moe_weights {
+    int E, D, FF, FFsh;
+    uint8_t *gate, *up, *down;       // [E][packed matrix]
+    uint8_t *sh_gate, *sh_up, *sh_down;
+    size_t gu_bytes, dn_bytes;       // one packed matrix
+    void *base;                      // single device allocation
+};
+
+struct q36moe_ctx {
+    int dev;
+    hipStream_t stream;
+    int max_T, E, D, FF, K;
+    int nb_max;
+    size_t tile_cap;
+    void *base;
+    int32_t *topk_idx; float *topk_w; int32_t *rank;
+    uint8_t *xq, *xs;
+    int32_t *blk_cnt, *blk_off, *e_off, *perm, *pos, *row_tok;
+    float *row_w;
+    int4 *tiles; int32_t *ntiles;
+    uint8_t *hq, *hs;
+    float *dnw;
+    int last_T, last_sh;
+    int timing;
+    hipEvent_t ev[ST_COUNT + 1];
+    double ms[ST_COUNT];
+    int calls[ST_COUNT];
+};
+
+namespace {
+
+int hip_rc(hipError_t e) { return e == hipSuccess ? Q36MOE_OK : Q36MOE_EHIP; }
+
+bool dims_ok(int E, int D, int FF) {
+    return E >= 1 && E <= kMaxExperts && D > 0 && FF > 0 && D % 512 == 0 && FF % 512 == 0;
+}
+
+int alloc_weights(int E, int D, int FF, int FFsh, q36moe_weights **out) {
+    if (!out || !dims_ok(E, D, FF) || !(FFsh == 0 || FFsh == FF)) return Q36MOE_EINVAL;
+    q36moe_weights *w = new (std::nothrow) q36moe_weights();
+    if (!w) return Q36MOE_ENOMEM;
+    w->E = E; w->D = D; w->FF = FF; w->FFsh = FFsh;
+    const size_t m = (size_t)D * FF;
+    w->gu_bytes = m / 2 + m / 32;
+    w->dn_bytes = w->gu_bytes;
+    const size_t routed = align256(w->gu_bytes * E);
+    const size_t total = 3 * routed + (FFsh ? 3 * align256(w->gu_bytes) : 0);
+    if (hipMalloc(&w->base, total) != hipSuccess) {
+        delete w;
+        return Q36MOE_ENOMEM;
+    }
+    uint8_t *p = static_cast<uint8_t *>(w->base);
+    w->gate = p; w->up = p + routed; w->down = p + 2 * routed;
+    if (FFsh) {
+        uint8_t *q = p + 3 * routed;
+        w->sh_gate = q; w->sh_up = q + align256(w->gu_bytes); w->sh_down = q + 2 * align256(w->gu_bytes);
+    } else {
+        w->sh_gate = w->sh_up = w->sh_down = nullptr;
+    }
+    *out = w;
+    return Q36MOE_OK;
+}
+
+template <int MODE, int WM, int WN, int TM, int TNW, int KD>
+void launch_gemm(const GemmArgs &a, int tiles, int rows, hipStream_t s) {
+    constexpr int ROWS = WM * TM * 16;
+    hipLaunchKernelGGL((k_expert_gemm<MODE, WM, WN, TM, TNW, KD>), dim3(tiles, rows / ROWS),
+                       dim3(256), 0, s, a);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *q36moe_version(void) { return "q36moe 0.1 gfx950"; }
+
+int q36moe_weights_alloc(int n_expert, int d_model, int d_ff, int d_ff_sh, q36moe_weights **out) {
+    return alloc_weights(n_expert, d_model, d_ff, d_ff_sh, out);
+}
+
+int q36moe_weights_upload(const void *gate, const void *up, const void *down, const void *sh_gate,
+                          const void *sh_up, const void *sh_down, int n_expert, int d_model,
+                          int d_ff, int d_ff_sh, q36moe_weights **out) {
+    if (!gate || !up || !down || !out) return Q36MOE_EINVAL;
+    if (d_ff_sh && (!sh_gate || !sh_up || !sh_down)) return Q36MOE_EINVAL;
+    q36moe_weights *w = nullptr;
+    int rc = alloc_weights(n_expert, d_model, d_ff, d_ff_sh, &w);
+    if (rc) return rc;
+    const size_t gu_src = (size_t)d_ff * (d_model / 32) * 17;
+    const size_t dn_src = (size_t)d_model * (d_ff / 32) * 17;
+    uint8_t *host = static_cast<uint8_t *>(malloc(w->gu_bytes));
+    if (!host) {
+        q36moe_weights_free(w);
+        return Q36MOE_ENOMEM;
+    }
+    struct Job { const uint8_t *src; size_t src_stride; uint8_t *dst; int M, K, n; };
+    const Job jobs[6] = {
+        {static_cast<const uint8_t *>(gate), gu_src, w->gate, d_ff, d_model, n_expert},
+        {static_cast<const uint8_t *>(up), gu_src, w->up, d_ff, d_model, n_expert},
+        {static_cast<const uint8_t *>(down), dn_src, w->down, d_model, d_ff, n_expert},
+        {static_cast<const uint8_t *>(sh_gate), gu_src, w->sh_gate, d_ff, d_model, d_ff_sh ? 1 : 0},
+        {static_cast<const uint8_t *>(sh_up), gu_src, w->sh_up, d_ff, d_model, d_ff_sh ? 1 : 0},
+        {static_cast<const uint8_t *>(sh_down), dn_src, w->sh_down, d_model, d_ff, d_ff_sh ? 1 : 0},
+    };
+    for (const Job &j : jobs) {
+        for (int e = 0; e < j.n && rc == 0; e++) {
+            rc = q36moe_pack_mxfp4(j.src + j.src_stride * e, j.M, j.K, host);
+            if (rc == 0)
+                rc = hip_rc(hipMemcpy(j.dst + w->gu_bytes * e, host, w->gu_bytes, hipMemcpyHostToDevice));
+        }
+    }
+    free(host);
+    if (rc) {
+        q36moe_weights_free(w);
+        return rc;
+    }
+    *out = w;
+    return Q36MOE_OK;
+}
+
+int q36moe_weights_device_ptrs(const q36moe_weights *w, void **gate, void **up, void **down,
+                               void **sh_gate, void **sh_up, void **sh_down, size_t *gate_bytes,
+                               size_t *down_bytes) {
+    if (!w) return Q36MOE_EINVAL;
+    if (gate) *gate = w->gate;
+    if (up) *up = w->up;
+    if (down) *down = w->down;
+    if (sh_gate) *sh_gate = w->sh_gate;
+    if (sh_up) *sh_up = w->sh_up;
+    if (sh_down) *sh_down = w->sh_down;
+    if (gate_bytes) *gate_bytes = w->gu_bytes;
+    if (down_bytes) *down_bytes = w->dn_bytes;
+    return Q36MOE_OK;
+}
+
+void q36moe_weights_free(q36moe_weights *w) {
+    if (!w) return;
+    if (w->base) (void)hipFree(w->base);
+    delete w;
+}
+
+int q36moe_ctx_create(int max_tokens, int n_expert, int d_model, int d_ff, int top_k, void *stream,
+                      q36moe_ctx **out) {
+    if (!out || max_tokens < 1 || !dims_ok(n_expert, d_model, d_ff) || top_k < 1 ||
+        top_k > kMaxTopK || top_k > n_expert)
+        return Q36MOE_EINVAL;
+    q36moe_ctx *c = new (std::nothrow) q36moe_ctx();
+    if (!c) return Q36MOE_ENOMEM;
+    if (hipGetDevice(&c->dev) != hipSuccess) {
+        delete c;
+        return Q36MOE_EHIP;
+    }
+    c->stream = static_cast<hipStream_t>(stream);
+    c->max_T = max_tokens; c->E = n_expert; c->D = d_model; c->FF = d_ff; c->K = top_k;
+    c->nb_max = (max_tokens + kRouteTPB - 1) / kRouteTPB;
+    const size_t n = (size_t)max_tokens * top_k;
+    const size_t rows = n + max_tokens;            // routed entries + shared rows
+    c->tile_cap = n / 16 + (size_t)(n < (size_t)n_expert ? n : n_expert) + (max_tokens + 15) / 16 + 16;
+    size_t off = 0;
+    auto take = [&off](size_t bytes) { size_t o = off; off = align256(off + bytes); return o; };
+    const size_t o_idx = take(n * 4), o_w = take(n * 4), o_rank = take(n * 4);
+    const size_t o_xq = take((size_t)max_tokens * d_model), o_xs = take((size_t)max_tokens * d_model / 32);
+    const size_t o_bc = take((size_t)c->nb_max * n_expert * 4), o_bo = take((size_t)c->nb_max * n_expert * 4);
+    const size_t o_eo = take((size_t)(n_expert + 1) * 4), o_perm = take(n * 4), o_pos = take(n * 4);
+    const size_t o_rt = take(rows * 4), o_rw = take(rows * 4);
+    const size_t o_tiles = take(c->tile_cap * 16), o_nt = take(4);
+    const size_t o_hq = take(rows * d_ff), o_hs = take(rows * d_ff / 32);
+    const size_t o_dnw = take(rows * d_model * 4);
+    if (hipMalloc(&c->base, off) != hipSuccess) {
+        delete c;
+        return Q36MOE_ENOMEM;
+    }
+    uint8_t *b = static_cast<uint8_t *>(c->base);
+    c->topk_idx = reinterpret_cast<int32_t *>(b + o_idx);
+    c->topk_w = reinterpret_cast<float *>(b + o_w);
+    c->rank = reinterpret_cast<int32_t *>(b + o_rank);
+    c->xq = b + o_xq; c->xs = b + o_xs;
+    c->blk_cnt = reinterpret_cast<int32_t *>(b + o_bc);
+    c->blk_off = reinterpret_cast<int32_t *>(b + o_bo);
+    c->e_off = reinterpret_cast<int32_t *>(b + o_eo);
+    c->perm = reinterpret_cast<int32_t *>(b + o_perm);
+    c->pos = reinterpret_cast<int32_t *>(b + o_pos);
+    c->row_tok = reinterpret_cast<int32_t *>(b + o_rt);
+    c->row_w = reinterpret_cast<float *>(b + o_rw);
+    c->tiles = reinterpret_cast<int4 *>(b + o_tiles);
+    c->ntiles = reinterpret_cast<int32_t *>(b + o_nt);
+    c->hq = b + o_hq; c->hs = b + o_hs;
+    c->dnw = reinterpret_cast<float *>(b + o_dnw);
+    for (int i = 0; i <= ST_COUNT; i++) {
+        if (hipEventCreate(&c->ev[i]) != hipSuccess) {
+            for (int j = 0; j < i; j++) (void)hipEventDestroy(c->ev[j]);
+            (void)hipFree(c->base);
+            delete c;
+            return Q36MOE_EHIP;
+        }
+    }
+    *out = c;
+    return Q36MOE_OK;
+}
+
+int q36moe_ctx_set_stream(q36moe_ctx *c, void *stream) {
+    if (!c) return Q36MOE_EINVAL;
+    c->stream = static_cast<hipStream_t>(stream);
+    return Q36MOE_OK;
+}
+
+void q36moe_ctx_free(q36moe_ctx *c) {
+    if (!c) return;
+    for (int i = 0; i <= ST_COUNT; i++) (void)hipEventDestroy(c->ev[i]);
+    if (c->base) (void)hipFree(c->base);
+    delete c;
+}
+
+int q36moe_forward(q36moe_ctx *c, const q36moe_weights *w, const void *x, int x_fmt,
+                   const float *logits, int ld_logits, const float *shg, int T, float scale,
+                   void *out, int out_fmt) {
+    if (!c || !w || T < 0 || T > c->max_T) return Q36MOE_EINVAL;
+    if (w->E != c->E || w->D != c->D || w->FF != c->FF) return Q36MOE_EINVAL;
+    if ((x_fmt != Q36MOE_FMT_F32 && x_fmt != Q36MOE_FMT_BF16) ||
+        (out_fmt != Q36MOE_FMT_F32 && out_fmt != Q36MOE_FMT_BF16))
+        return Q36MOE_EINVAL;
+    // kernels are instantiated for the q36 shape (q36.h:78-84)
+    if (c->D != 2048 || c->FF != 512) return Q36MOE_EINVAL;
+    if (T == 0) return Q36MOE_OK;
+    if (!x || !logits || !out || ld_logits < c->E) return Q36MOE_EINVAL;
+    if (shg && !w->sh_gate) return Q36MOE_EINVAL;
+    const int has_sh = shg != nullptr;
+    const int E = c->E, D = c->D, FF = c->FF, K = c->K;
+    const int n = T * K;
+    const int nb = (T + kRouteTPB - 1) / kRouteTPB;
+    const bool wide = n >= 2048;
+    const int tn = wide ? 128 : 16;
+    int tiles = n / tn + (n < E ? n : E) + (has_sh ? (T + tn - 1) / tn : 0);
+    tiles = (tiles + 7) & ~7;
+    hipStream_t s = c->stream;
+    auto mark = [&](int st) {
+        if (c->timing) (void)hipEventRecord(c->ev[st], s);
+    };
+
+    mark(ST_ROUTE);
+    RouteArgs ra{logits, ld_logits, T, E, K, scale, x, x_fmt, D,
+                 c->topk_idx, c->topk_w, c->xq, c->xs, c->blk_cnt, c->rank};
+    hipLaunchKernelGGL(k_route, dim3(nb), dim3(kRouteThreads), 0, s, ra);
+
+    mark(ST_SCAN);
+    ScanArgs sa{c->blk_cnt, nb, E, T, K, c->topk_idx, c->topk_w, c->rank, shg, tn,
+                c->blk_off, c->e_off, c->perm, c->pos, c->row_tok, c->row_w, c->tiles, c->ntiles};
+    hipLaunchKernelGGL(k_scan, dim3(1), dim3(kScanThreads), 0, s, sa);
+
+    mark(ST_GATEUP);
+    GemmArgs ga{};
+    ga.wa = w->gate; ga.wb = w->up; ga.sa = w->sh_gate; ga.sb = w->sh_up;
+    ga.wstride = w->gu_bytes; ga.E = E; ga.M = FF;
+    ga.tiles = c->tiles; ga.ntiles = c->ntiles;
+    ga.bq = c->xq; ga.bs = c->xs; ga.row_tok = c->row_tok; ga.row_w = c->row_w;
+    ga.hq = c->hq; ga.hs = c->hs; ga.ldo = FF;
+    GemmArgs da = ga;
+    da.wa = w->down; da.wb = nullptr; da.sa = w->sh_down; da.sb = nullptr;
+    da.wstride = w->dn_bytes; da.M = D;
+    da.bq = c->hq; da.bs = c->hs; da.dnw = c->dnw; da.ldo = D;
+    if (wide) launch_gemm<MODE_GATEUP, 2, 2, 2, 4, 2048>(ga, tiles, FF, s);
+    else launch_gemm<MODE_GATEUP, 4, 1, 2, 1, 2048>(ga, tiles, FF, s);
+
+    mark(ST_DOWN);
+    if (wide) launch_gemm<MODE_DOWN, 2, 2, 4, 4, 512>(da, tiles, D, s);
+    else launch_gemm<MODE_DOWN, 4, 1, 2, 1, 512>(da, tiles, D, s);
+
+    mark(ST_COMBINE);
+    hipLaunchKernelGGL(k_combine, dim3(T), dim3(256), 0, s, c->dnw, c->pos, T, K, D, has_sh, out,
+                       out_fmt);
+    mark(ST_COUNT);
+    c->last_T = T;
+    c->last_sh = has_sh;
+    if (hipGetLastError() != hipSuccess) return Q36MOE_EHIP;
+    if (c->timing) {
+        if (hipEventSynchronize(c->ev[ST_COUNT]) != hipSuccess) return Q36MOE_EHIP;
+        for (int st = 0; st < ST_COUNT; st++) {
+            float ms = 0.f;
+            if (hipEventElapsedTime(&ms, c->ev[st], c->ev[st + 1]) != hipSuccess) return Q36MOE_EHIP;
+            c->ms[st] += ms;
+            c->calls[st]++;
+        }
+    }
+    return Q36MOE_OK;
+}
+
+int q36moe_router_topk(const float *logits, int T, int n_expert, int ld, int k, float scale,
+                       int renorm, int32_t *idx, float *wt, void *stream) {
+    if (T < 0 || n_expert < 1 || n_expert > kMaxExperts || ld < n_expert || k < 1 ||
+        k > kMaxTopK || k > n_expert)
+        return Q36MOE_EINVAL;
+    if (T == 0) return Q36MOE_OK;
+    if (!logits || !idx || !wt) return Q36MOE_EINVAL;
+    hipLaunchKernelGGL(k_topk, dim3((T + 3) / 4), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       logits, T, n_expert, ld, k, scale, renorm, idx, wt);
+    return hip_rc(hipGetLastError());
+}
+
+int q36moe_quant_e4m3(const void *x, int x_fmt, int T, int K, uint8_t *xq, uint8_t *xs,
+                      void *stream) {
+    if (T < 0 || K <= 0 || K % 32 != 0 || (x_fmt != Q36MOE_FMT_F32 && x_fmt != Q36MOE_FMT_BF16))
+        return Q36MOE_EINVAL;
+    if (T == 0) return Q36MOE_OK;
+    if (!x || !xq || !xs) return Q36MOE_EINVAL;
+    const long nblk = (long)T * (K / 32);
+    hipLaunchKernelGGL(k_quant, dim3((unsigned)((nblk + 255) / 256)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), x, x_fmt, T, K, xq, xs);
+    return hip_rc(hipGetLastError());
+}
+
+int q36moe_ctx_copy_tap(q36moe_ctx *c, int tap, void *dst, size_t bytes, size_t *written) {
+    if (!c || !dst) return Q36MOE_EINVAL;
+    const size_t T = (size_t)c->last_T, n = T * c->K, rows = n + (c->last_sh ? T : 0);
+    const void *src = nullptr;
+    size_t sz = 0;
+    switch (tap) {
+        case Q36MOE_TAP_TOPK_IDX: src = c->topk_idx; sz = n * 4; break;
+        case Q36MOE_TAP_TOPK_W: src = c->topk_w; sz = n * 4; break;
+        case Q36MOE_TAP_XQ: src = c->xq; sz = T * c->D; break;
+        case Q36MOE_TAP_XS: src = c->xs; sz = T * c->D / 32; break;
+        case Q36MOE_TAP_EOFF: src = c->e_off; sz = (size_t)(c->E + 1) * 4; break;
+        case Q36MOE_TAP_PERM: src = c->perm; sz = n * 4; break;
+        case Q36MOE_TAP_POS: src = c->pos; sz = n * 4; break;
+        case Q36MOE_TAP_HQ: src = c->hq; sz = rows * c->FF; break;
+        case Q36MOE_TAP_HS: src = c->hs; sz = rows * c->FF / 32; break;
+        case Q36MOE_TAP_DNW: src = c->dnw; sz = rows * c->D * 4; break;
+        default: return Q36MOE_EINVAL;
+    }
+    if (bytes < sz) return Q36MOE_EINVAL;
+    if (written) *written = sz;
+    if (sz == 0) return Q36MOE_OK;
+    return hip_rc(hipMemcpyAsync(dst, src, sz, hipMemcpyDeviceToDevice, c->stream));
+}
+
+int q36moe_ctx_set_timing(q36moe_ctx *c, int on) {
+    if (!c) return Q36MOE_EINVAL;
+    c->timing = on ? 1 : 0;
+    return Q36MOE_OK;
+}
+
+int q36moe_ctx_stage_times(q36moe_ctx *c, double *ms, int *calls, int n_stages, int reset) {
+    if (!c || n_stages < 0) return Q36MOE_EINVAL;
+    for (int i = 0; i < n_stages && i < ST_COUNT; i++) {
+        if (ms) ms[i] = c->ms[i];
+        if (calls) calls[i] = c->calls[i];
+    }
+    if (reset)
+        for (int i = 0; i < ST_COUNT; i++) {
+            c->ms[i] = 0.0;
+            c->calls[i] = 0;
+        }
+    return Q36MOE_OK;
+}
+
+const char *q36moe_stage_name(int stage) {
+    return (stage >= 0 && stage < ST_COUNT) ? kStageNames[stage] : nullptr;
+}
+
+int q36moe_num_stages(void) { return ST_COUNT; }
+
+int q36moe_probe_mfma(const void *a, const void *b, const uint32_t *sa, const uint32_t *sb,
+                      int fmt_a, int fmt_b, float *c, void *stream) {
+    if (!a || !b || !sa || !sb || !c || fmt_a < 0 || fmt_a > 4 || fmt_b < 0 || fmt_b > 4)
+        return Q36MOE_EINVAL;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const v8i *av = static_cast<const v8i *>(a);
+    const v8i *bv = static_cast<const v8i *>(b);
+    v4f *cv = reinterpret_cast<v4f *>(c);
+    hipError_t e;
+    switch (fmt_a) {
+        case 0: e = launch_probe_b<0>(fmt_b, av, bv, sa, sb, cv, s); break;
+        case 1: e = launch_probe_b<1>(fmt_b, av, bv, sa, sb, cv, s); break;
+        case 2: e = launch_probe_b<2>(fmt_b, av, bv, sa, sb, cv, s); break;
+        case 3: e = launch_probe_b<3>(fmt_b, av, bv, sa, sb, cv, s); break;
+        default: e = launch_probe_b<4>(fmt_b, av, bv, sa, sb, cv, s); break;
+    }
+    return hip_rc(e);
+}
+
+}  // extern "C"

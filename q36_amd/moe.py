@@ -1,0 +1,315 @@
+"""Python host mirror of the q36 MoE layer over the C ABI of libq36moe.so.
+
+The layer keeps the reference's boundary: router logits in, combined hidden
+state out (moe_ffn, q36_engine.cu:1592-1654; pf_moe_block,
+q36_engine.cu:3423-3472).  torch supplies device memory and the stream; all
+compute runs in the HIP kernels of libq36moe.so.  There is no CPU fallback:
+a missing library, a tensor that is not on the GPU or a non-zero return code
+raises.
+"""
+import ctypes
+import os
+
+import numpy as np
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libq36moe.so")
+
+FMT_F32 = 0
+FMT_BF16 = 1
+
+TAP_TOPK_IDX, TAP_TOPK_W, TAP_XQ, TAP_XS, TAP_EOFF, TAP_PERM, TAP_POS, TAP_HQ, TAP_HS, TAP_DNW = range(10)
+
+_ERRORS = {-22: "EINVAL", -12: "ENOMEM", -1000: "EHIP"}
+
+_lib = None
+
+
+class Q36MoEError(RuntimeError):
+    pass
+
+
+def lib():
+    """The loaded C library (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise Q36MoEError(f"{LIB_PATH} is missing: build it with `python -m q36_amd.build`")
+    L = ctypes.CDLL(LIB_PATH)
+    vp, i, sz, f = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t, ctypes.c_float
+    pp = ctypes.POINTER(ctypes.c_void_p)
+    L.q36moe_version.restype = ctypes.c_char_p
+    L.q36moe_expert_bytes.argtypes = [i, i]
+    L.q36moe_expert_bytes.restype = sz
+    L.q36moe_weights_upload.argtypes = [vp] * 6 + [i] * 4 + [pp]
+    L.q36moe_weights_alloc.argtypes = [i] * 4 + [pp]
+    L.q36moe_weights_device_ptrs.argtypes = [vp] + [pp] * 6 + [ctypes.POINTER(sz)] * 2
+    L.q36moe_weights_free.argtypes = [vp]
+    L.q36moe_weights_free.restype = None
+    L.q36moe_pack_mxfp4.argtypes = [vp, i, i, vp]
+    L.q36moe_unpack_mxfp4.argtypes = [vp, i, i, vp]
+    L.q36moe_ctx_create.argtypes = [i] * 5 + [vp, pp]
+    L.q36moe_ctx_set_stream.argtypes = [vp, vp]
+    L.q36moe_ctx_free.argtypes = [vp]
+    L.q36moe_ctx_free.restype = None
+    L.q36moe_forward.argtypes = [vp, vp, vp, i, vp, i, vp, i, f, vp, i]
+    L.q36moe_router_topk.argtypes = [vp, i, i, i, i, f, i, vp, vp, vp]
+    L.q36moe_quant_e4m3.argtypes = [vp, i, i, i, vp, vp, vp]
+    L.q36moe_ctx_copy_tap.argtypes = [vp, i, vp, sz, ctypes.POINTER(sz)]
+    L.q36moe_ctx_set_timing.argtypes = [vp, i]
+    L.q36moe_ctx_stage_times.argtypes = [vp, ctypes.POINTER(ctypes.c_double),
+                                         ctypes.POINTER(ctypes.c_int), i, i]
+    L.q36moe_stage_name.argtypes = [i]
+    L.q36moe_stage_name.restype = ctypes.c_char_p
+    L.q36moe_num_stages.argtypes = []
+    L.q36moe_probe_mfma.argtypes = [vp, vp, vp, vp, i, i, vp, vp]
+    _lib = L
+    return L
+
+
+def check(rc, what):
+    if rc != 0:
+        raise Q36MoEError(f"{what} returned {rc} ({_ERRORS.get(rc, '?')})")
+
+
+def _stream(stream=None):
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+def _dev(t, name, dtype=None):
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise Q36MoEError(f"{name} must be a GPU tensor")
+    if not t.is_contiguous():
+        raise Q36MoEError(f"{name} must be contiguous")
+    if dtype is not None and t.dtype != dtype:
+        raise Q36MoEError(f"{name} must be {dtype}, got {t.dtype}")
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _host_u8(a):
+    a = np.ascontiguousarray(a, dtype=np.uint8)
+    return a, ctypes.c_void_p(a.ctypes.data)
+
+
+# ---------------------------------------------------------------------------
+# weights
+# ---------------------------------------------------------------------------
+class MoEWeights:
+    """One layer's routed experts (+ optional shared expert) on the device,
+    in the packed fragment layout (mirrors the MXFP4 branch of upload(),
+    q36_engine.cu:196-228)."""
+
+    def __init__(self, handle, n_expert, d_model, d_ff, d_ff_sh):
+        self._h = handle
+        self.n_expert, self.d_model, self.d_ff, self.d_ff_sh = n_expert, d_model, d_ff, d_ff_sh
+
+    @classmethod
+    def upload(cls, gate, up, down, sh_gate=None, sh_up=None, sh_down=None):
+        """gate/up [E, d_ff, d_model/32, 17], down [E, d_model, d_ff/32, 17]
+        GGUF block_mxfp4 bytes (numpy uint8)."""
+        E, d_ff, nbk, _ = gate.shape
+        d_model = nbk * 32
+        keep = []
+        ptrs = []
+        for a in (gate, up, down):
+            a, p = _host_u8(a)
+            keep.append(a)
+            ptrs.append(p)
+        d_ff_sh = 0
+        if sh_gate is not None:
+            d_ff_sh = sh_gate.shape[0]
+            for a in (sh_gate, sh_up, sh_down):
+                a, p = _host_u8(a)
+                keep.append(a)
+                ptrs.append(p)
+        else:
+            ptrs += [None, None, None]
+        h = ctypes.c_void_p()
+        check(lib().q36moe_weights_upload(*ptrs, E, d_model, d_ff, d_ff_sh, ctypes.byref(h)),
+              "q36moe_weights_upload")
+        return cls(h, E, d_model, d_ff, d_ff_sh)
+
+    @classmethod
+    def alloc(cls, n_expert, d_model, d_ff, d_ff_sh=0):
+        h = ctypes.c_void_p()
+        check(lib().q36moe_weights_alloc(n_expert, d_model, d_ff, d_ff_sh, ctypes.byref(h)),
+              "q36moe_weights_alloc")
+        return cls(h, n_expert, d_model, d_ff, d_ff_sh)
+
+    def device_ptrs(self):
+        """dict name -> (device address, bytes of the whole region)."""
+        p = [ctypes.c_void_p() for _ in range(6)]
+        gb, db = ctypes.c_size_t(), ctypes.c_size_t()
+        check(lib().q36moe_weights_device_ptrs(self._h, *[ctypes.byref(x) for x in p],
+                                               ctypes.byref(gb), ctypes.byref(db)),
+              "q36moe_weights_device_ptrs")
+        E = self.n_expert
+        out = {"gate": (p[0].value, gb.value * E), "up": (p[1].value, gb.value * E),
+               "down": (p[2].value, db.value * E)}
+        if self.d_ff_sh:
+            out.update({"sh_gate": (p[3].value, gb.value), "sh_up": (p[4].value, gb.value),
+                        "sh_down": (p[5].value, db.value)})
+        return out
+
+    def free(self):
+        if self._h:
+            lib().q36moe_weights_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def pack_mxfp4(blocks):
+    """Host repack of one [M, K/32, 17] GGUF matrix to the device layout."""
+    M, nb, _ = blocks.shape
+    K = nb * 32
+    src, p = _host_u8(blocks)
+    out = np.empty(M * K // 2 + M * K // 32, dtype=np.uint8)
+    check(lib().q36moe_pack_mxfp4(p, M, K, ctypes.c_void_p(out.ctypes.data)), "q36moe_pack_mxfp4")
+    return out
+
+
+def unpack_mxfp4(packed, M, K):
+    src, p = _host_u8(packed)
+    out = np.empty((M, K // 32, 17), dtype=np.uint8)
+    check(lib().q36moe_unpack_mxfp4(p, M, K, ctypes.c_void_p(out.ctypes.data)),
+          "q36moe_unpack_mxfp4")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# the layer
+# ---------------------------------------------------------------------------
+class MoELayer:
+    """Scratch + launch context for the MoE forward (moe_ffn / pf_moe_block
+    boundary).  All scratch is allocated at construction."""
+
+    def __init__(self, max_tokens, n_expert=256, d_model=2048, d_ff=512, top_k=8, stream=None):
+        self.max_tokens, self.n_expert, self.d_model, self.d_ff, self.top_k = (
+            max_tokens, n_expert, d_model, d_ff, top_k)
+        self._h = ctypes.c_void_p()
+        check(lib().q36moe_ctx_create(max_tokens, n_expert, d_model, d_ff, top_k, _stream(stream),
+                                      ctypes.byref(self._h)), "q36moe_ctx_create")
+        self.last_T = 0
+        self.last_shared = False
+
+    def set_stream(self, stream):
+        check(lib().q36moe_ctx_set_stream(self._h, _stream(stream)), "q36moe_ctx_set_stream")
+
+    def forward(self, weights, x, logits, shg=None, scale=1.0, out_dtype=torch.bfloat16, out=None):
+        """x [T, d_model] f32|bf16, logits [T, >=n_expert] f32, shg [T] f32 or
+        None -> out [T, d_model] (bf16 or f32)."""
+        T = x.shape[0]
+        xf = FMT_F32 if x.dtype == torch.float32 else FMT_BF16
+        if x.dtype not in (torch.float32, torch.bfloat16):
+            raise Q36MoEError("x must be float32 or bfloat16")
+        if out is None:
+            out = torch.empty((T, self.d_model), dtype=out_dtype, device=x.device)
+        of = FMT_F32 if out.dtype == torch.float32 else FMT_BF16
+        if logits.dim() != 2 or logits.shape[0] != T:
+            raise Q36MoEError("logits must be [T, n_expert]")
+        ld = logits.stride(0)
+        if logits.stride(1) != 1:
+            raise Q36MoEError("logits rows must be contiguous")
+        lp = ctypes.c_void_p(logits.data_ptr()) if T else None
+        if T and (not logits.is_cuda or logits.dtype != torch.float32):
+            raise Q36MoEError("logits must be a float32 GPU tensor")
+        sp = _dev(shg, "shg", torch.float32) if shg is not None else None
+        xp = _dev(x, "x") if T else None
+        op = _dev(out, "out") if T else None
+        check(lib().q36moe_forward(self._h, weights._h, xp, xf, lp, ld, sp, T, float(scale), op, of),
+              "q36moe_forward")
+        self.last_T = T
+        self.last_shared = shg is not None
+        return out
+
+    def tap(self, which):
+        """Copy of an internal buffer of the last forward (see TAP_*)."""
+        T, k, D, FF, E = self.last_T, self.top_k, self.d_model, self.d_ff, self.n_expert
+        rows = T * k + (T if self.last_shared else 0)
+        shapes = {
+            TAP_TOPK_IDX: ((T, k), torch.int32), TAP_TOPK_W: ((T, k), torch.float32),
+            TAP_XQ: ((T, D), torch.uint8), TAP_XS: ((T, D // 32), torch.uint8),
+            TAP_EOFF: ((E + 1,), torch.int32), TAP_PERM: ((T * k,), torch.int32),
+            TAP_POS: ((T * k,), torch.int32), TAP_HQ: ((rows, FF), torch.uint8),
+            TAP_HS: ((rows, FF // 32), torch.uint8), TAP_DNW: ((rows, D), torch.float32),
+        }
+        shape, dt = shapes[which]
+        dst = torch.empty(shape, dtype=dt, device="cuda")
+        n = ctypes.c_size_t()
+        check(lib().q36moe_ctx_copy_tap(self._h, which, ctypes.c_void_p(dst.data_ptr()),
+                                        dst.numel() * dst.element_size(), ctypes.byref(n)),
+              "q36moe_ctx_copy_tap")
+        return dst
+
+    def set_timing(self, on):
+        check(lib().q36moe_ctx_set_timing(self._h, 1 if on else 0), "q36moe_ctx_set_timing")
+
+    def stage_times(self, reset=False):
+        """dict stage -> (total ms, calls) since the last reset."""
+        n = lib().q36moe_num_stages()
+        ms = (ctypes.c_double * n)()
+        calls = (ctypes.c_int * n)()
+        check(lib().q36moe_ctx_stage_times(self._h, ms, calls, n, 1 if reset else 0),
+              "q36moe_ctx_stage_times")
+        return {lib().q36moe_stage_name(i).decode(): (ms[i], calls[i]) for i in range(n)}
+
+    def free(self):
+        if self._h:
+            lib().q36moe_ctx_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+# ---------------------------------------------------------------------------
+# stage entry points
+# ---------------------------------------------------------------------------
+def router_topk(logits, k=8, scale=1.0, renorm=True, n_expert=None):
+    """k_router_topk (q36_ops.cuh:397-431): -> idx int32 [T,k], wt f32 [T,k]."""
+    T = logits.shape[0]
+    E = n_expert or logits.shape[1]
+    idx = torch.empty((T, k), dtype=torch.int32, device=logits.device)
+    wt = torch.empty((T, k), dtype=torch.float32, device=logits.device)
+    if logits.stride(1) != 1:
+        raise Q36MoEError("logits rows must be contiguous")
+    lp = ctypes.c_void_p(logits.data_ptr()) if T else None
+    if T and (not logits.is_cuda or logits.dtype != torch.float32):
+        raise Q36MoEError("logits must be a float32 GPU tensor")
+    check(lib().q36moe_router_topk(lp, T, E, logits.stride(0), k, float(scale), 1 if renorm else 0,
+                                   ctypes.c_void_p(idx.data_ptr()), ctypes.c_void_p(wt.data_ptr()),
+                                   _stream()), "q36moe_router_topk")
+    return idx, wt
+
+
+def quant_e4m3(x):
+    """k_quant_e4m3 (q36_engine.cu:2411-2428): x [T,K] f32|bf16 ->
+    (xq u8 [T,K] e4m3, xs u8 [T,K/32] E8M0)."""
+    T, K = x.shape
+    xq = torch.empty((T, K), dtype=torch.uint8, device=x.device)
+    xs = torch.empty((T, K // 32), dtype=torch.uint8, device=x.device)
+    fmt = FMT_F32 if x.dtype == torch.float32 else FMT_BF16
+    xp = _dev(x, "x") if T else None
+    check(lib().q36moe_quant_e4m3(xp, fmt, T, K, ctypes.c_void_p(xq.data_ptr()),
+                                  ctypes.c_void_p(xs.data_ptr()), _stream()), "q36moe_quant_e4m3")
+    return xq, xs
+
+
+def probe_mfma(a, b, sa, sb, fmt_a, fmt_b):
+    """One scaled 16x16x128 MFMA: a, b uint8 [64, 32]; sa, sb int32/uint32 [64]."""
+    c = torch.empty((64, 4), dtype=torch.float32, device=a.device)
+    check(lib().q36moe_probe_mfma(_dev(a, "a"), _dev(b, "b"), _dev(sa, "sa"), _dev(sb, "sb"),
+                                  fmt_a, fmt_b, ctypes.c_void_p(c.data_ptr()), _stream()),
+          "q36moe_probe_mfma")
+    return c

@@ -1,0 +1,42 @@
+"""Writes tests/golden/mxfp4_dequant_ref.npz: MXFP4 blocks and their values
+as computed by the reference's own q36_deq_mxfp4 / q36_e8m0_half, compiled
+from /root/reference/q36_dequant.cuh into oracle/_ref/ by oracle/Makefile.
+
+    make -C oracle && python tests/golden/make_golden.py
+
+The fixture is data only (inputs and the reference's outputs)."""
+import ctypes
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
+from oracle import pyoracle  # noqa: E402
+
+
+def main():
+    ref = pyoracle.ref_lib()
+    if ref is None:
+        raise SystemExit("oracle/_ref/libref_dequant.so missing: run `make -C oracle` with the reference tree present")
+    rng = np.random.default_rng(20261201)
+    n = 1024
+    blocks = np.frombuffer(rng.bytes(n * 17), dtype=np.uint8).reshape(n, 17).copy()
+    # exponent bytes over the whole finite E8M0 range, the benchmark range
+    # [119, 127] and the denormal-handling edge e < 2 of q36_e8m0_half
+    blocks[:, 0] = rng.integers(0, 255, size=n).astype(np.uint8)
+    blocks[:64, 0] = np.arange(64) % 3            # 0, 1, 2
+    blocks[64:256, 0] = 119 + rng.integers(0, 9, size=192)
+    vals = np.empty((n, 32), dtype=np.float32)
+    for i in range(n):
+        ref.ref_deq_mxfp4(ctypes.c_void_p(blocks[i].ctypes.data),
+                          ctypes.c_void_p(vals[i].ctypes.data))
+    e8m0_half = np.array([ref.ref_e8m0_half(e) for e in range(256)], dtype=np.float32)
+    np.savez_compressed(os.path.join(HERE, "mxfp4_dequant_ref.npz"), blocks=blocks, values=vals,
+                        e8m0_half=e8m0_half)
+    print("wrote", n, "blocks")
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,391 @@
+"""GPU parity of the HIP path against the CPU oracle, called through the C ABI
+(q36_amd.moe is a thin ctypes mirror).  Bars:
+  * routing indices, sort offsets / permutation, FP8 activation codes and
+    E8M0 scales: bit-exact;
+  * routing weights: |dw| <= 2e-6 * w (fp32 exp/div vs fp64);
+  * staged layer parity, per token row t (fp32 result, before bf16 rounding):
+      1. gate/up + SwiGLU + h quantisation: GPU e4m3 codes / E8M0 scales equal
+         the oracle's quantisation of fp32(h) except at rounding midpoints
+         (fp32 vs fp64 accumulation), counted and capped at 1%;
+      2. down + combine from the GPU's own h rows vs fp64:
+           max relative error  max_i |y_ti - ref_ti| / max_i |ref_ti|   <= 2e-3
+           element-wise  |y_ti - ref_ti| / max(|ref_ti|, 0.05 max_i |ref_ti|) <= 2e-3
+      3. end to end vs the fp64 oracle, reported; asserted only as a gross
+         error backstop (<= 1e-2): a single midpoint flip of a large h code
+         (up to 1/16 of the value) moves outputs by up to ~2e-3 of the row
+         max, so stages 1+2 carry the 2e-3 bar on identical quantised inputs;
+    an element-wise bound needs the floor near zero, and bf16's own half-ulp
+    is up to 2^-8 relative, above 2e-3, so the bars apply to the fp32 result;
+  * bf16 output: the RNE bf16 rounding of the f32 output, bit for bit.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from q36_amd import moe, synth
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+FLOOR = 5e-2
+
+
+def _metrics(name, **kv):
+    path = os.environ.get("Q36_METRICS_FILE")
+    if path:
+        with open(path, "a") as f:
+            f.write(json.dumps({"test": name, **kv}) + "\n")
+
+
+@pytest.fixture(scope="module")
+def dev():
+    assert torch.cuda.is_available(), "GPU tests need a GPU"
+    return torch.device("cuda:0")
+
+
+# ---------------------------------------------------------------------------
+# MFMA calibration (the analogue of test_mma_bs.cu for gfx950)
+# ---------------------------------------------------------------------------
+E2M1 = np.array([0, .5, 1, 1.5, 2, 3, 4, 6, -0., -.5, -1, -1.5, -2, -3, -4, -6])
+
+
+def _e4m3_table():
+    return torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).double().numpy()
+
+
+def _fp4_k(q, n):
+    return 32 * q + n
+
+
+def _fp8_k(q, i):
+    return 64 * (i >> 4) + 16 * q + (i & 15)
+
+
+def _interp(lanes, scales, fmt, tab, transpose):
+    """Logical operand [16][128] (A) or [128][16] (B) from lane bytes, with
+    the gfx950 layout: E2M1 lane group q holds K 32q..32q+31 (nibble n -> K
+    32q+n); E4M3 byte i of lane group q holds K 64*(i>>4)+16q+(i&15); the scale
+    of K block kb comes from lane group kb."""
+    M = np.zeros((16, 128))
+    for L in range(64):
+        r, q = L % 16, L // 16
+        for i in range(32):
+            if fmt == 4:
+                byte = lanes[L, i // 2]
+                code = (byte >> 4) if (i & 1) else (byte & 15)
+                k, v = _fp4_k(q, i), E2M1[code]
+            else:
+                k, v = _fp8_k(q, i), tab[lanes[L, i]]
+            M[r, k] = v * 2.0 ** (int(scales[r + 16 * (k // 32)] & 255) - 127)
+    return M.T if transpose else M
+
+
+def _lanes(C):
+    out = np.zeros((64, 4))
+    for L in range(64):
+        for i in range(4):
+            out[L, i] = C[4 * (L // 16) + i, L % 16]
+    return out
+
+
+def _rand_fp8(rng, shape):
+    b = rng.integers(0, 256, size=shape).astype(np.uint8)
+    b[(b & 0x7F) == 0x7F] = 0x38
+    return b
+
+
+@pytest.mark.parametrize("fmt_a,spread", [(4, True), (0, True), (4, False), (0, False)])
+def test_mfma_probe_layout(dev, fmt_a, spread):
+    """Calibrates the operand / scale / output layout of the scaled MFMA the
+    kernels use (the role of test_mma_bs.cu on sm_120a): random codes and
+    scales, upper scale bytes random to show that only byte 0 is read."""
+    rng = np.random.default_rng(100 + fmt_a)
+    tab = _e4m3_table()
+    if fmt_a == 4:
+        codes = rng.integers(0, 16, size=(64, 32)).astype(np.uint8)
+        a_lane = np.zeros((64, 32), dtype=np.uint8)
+        a_lane[:, :16] = codes[:, 0::2] | (codes[:, 1::2] << 4)
+    else:
+        a_lane = _rand_fp8(rng, (64, 32))
+    b_lane = _rand_fp8(rng, (64, 32))
+    hi = lambda: rng.integers(0, 1 << 24, size=64).astype(np.uint32) << 8
+    lo, hi_e = (120, 135) if spread else (127, 128)
+    sa = rng.integers(lo, hi_e, size=64).astype(np.uint32) | hi()
+    sb = rng.integers(lo, hi_e, size=64).astype(np.uint32) | hi()
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    c = moe.probe_mfma(t(a_lane), t(b_lane), t(sa.view(np.int32)), t(sb.view(np.int32)), fmt_a, 0)
+    got = c.double().cpu().numpy()
+    A = _interp(a_lane, sa, fmt_a, tab, False)
+    B = _interp(b_lane, sb, 0, tab, True)
+    want = _lanes(A @ B)
+    err = np.abs(got - want).max() / np.abs(want).max()
+    _metrics("mfma_probe", fmt_a=fmt_a, spread=spread, err=float(err))
+    # a wrong layout gives O(1) errors.  The MFMA's internal accumulation of
+    # full-range e4m3 products is not exact fp32: ~5e-5 of max|C| measured on
+    # gfx950 with either scale range, so the bar is 2e-4.
+    assert err < 2e-4, err
+
+
+# ---------------------------------------------------------------------------
+# stage entry points
+# ---------------------------------------------------------------------------
+def _quant_inputs(rng):
+    x = (rng.standard_normal((64, 2048)) * 10.0 ** rng.uniform(-4, 4, (64, 1))).astype(np.float32)
+    x[0, :32] = 0.0
+    x[1, :32] = 1e-40
+    x[2, :64] = np.float32(2.0 ** -5) * np.float32(1 + 2.0 ** -23) * 448   # log2 edge amax
+    # exact e4m3 midpoints after scaling (amax 448 -> e2 = 0)
+    tab = _e4m3_table()
+    fin = np.sort(np.unique(tab[np.isfinite(tab) & (tab >= 0)]))
+    mids = ((fin[:-1] + fin[1:]) / 2).astype(np.float32)
+    x[3, :] = np.resize(np.concatenate([[448.0], mids]), 2048)
+    x[3, ::32] = 448.0
+    return x
+
+
+def test_quant_stage_bit_exact(dev, oracle):
+    rng = np.random.default_rng(21)
+    x = _quant_inputs(rng)
+    xq, xs = moe.quant_e4m3(torch.from_numpy(x).to(dev))
+    oq, os_ = oracle.quant_e4m3(x)
+    np.testing.assert_array_equal(xs.cpu().numpy(), os_)
+    np.testing.assert_array_equal(xq.cpu().numpy(), oq)
+    # bf16 input: the oracle sees the same values widened to f32
+    xb = torch.from_numpy(x).to(dev).to(torch.bfloat16)
+    bq, bs = moe.quant_e4m3(xb)
+    oq, os_ = oracle.quant_e4m3(xb.float().cpu().numpy())
+    np.testing.assert_array_equal(bs.cpu().numpy(), os_)
+    np.testing.assert_array_equal(bq.cpu().numpy(), oq)
+
+
+@pytest.mark.parametrize("E,ld,k", [(256, 256, 8), (256, 257, 8), (100, 128, 4), (64, 64, 1)])
+def test_router_stage(dev, oracle, E, ld, k):
+    rng = np.random.default_rng(22 + E + k)
+    T = 300
+    lg = rng.standard_normal((T, ld)).astype(np.float32)
+    lg[0] = 0.25
+    lg[1, 5:40] = 2.0
+    lg[2] = np.round(lg[2] * 2) / 2
+    idx, wt = moe.router_topk(torch.from_numpy(lg).to(dev), k=k, n_expert=E)
+    oi, ow = oracle.router_topk(lg, k, n_expert=E)
+    np.testing.assert_array_equal(idx.cpu().numpy(), oi)
+    err = np.abs(wt.cpu().double().numpy() - ow) / ow
+    _metrics("router_stage", E=E, k=k, max_rel_w=float(err.max()))
+    assert err.max() <= 2e-6
+
+
+# ---------------------------------------------------------------------------
+# the layer
+# ---------------------------------------------------------------------------
+@pytest.fixture(scope="module")
+def layer_w():
+    w = synth.expert_weights(2026, shared=True)
+    dw = moe.MoEWeights.upload(w["gate"], w["up"], w["down"], w["sh_gate"], w["sh_up"], w["sh_down"])
+    return w, dw
+
+
+def _row_err(y, ref):
+    scale = np.abs(ref).max(axis=1, keepdims=True)
+    rel = np.abs(y - ref) / np.maximum(np.abs(ref), FLOOR * scale)
+    return float(rel.max()), float((np.abs(y - ref).max(axis=1) / scale[:, 0]).max())
+
+
+def _bf16_of(y32):
+    return torch.from_numpy(y32.astype(np.float32)).to(torch.bfloat16).float().numpy()
+
+
+def _run_layer(dev, dw, x, lg, shg, max_tokens=None, x_dtype=torch.float32):
+    T = x.shape[0]
+    layer = moe.MoELayer(max_tokens or max(T, 1))
+    xt = torch.from_numpy(x).to(dev).to(x_dtype)
+    lt = torch.from_numpy(lg).to(dev)
+    st = torch.from_numpy(shg).to(dev) if shg is not None else None
+    y32 = layer.forward(dw, xt, lt, st, out_dtype=torch.float32)
+    y16 = layer.forward(dw, xt, lt, st, out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    return layer, y32.cpu().numpy(), y16.float().cpu().numpy()
+
+
+def _check_routing(layer, oracle, lg, E=256, k=8):
+    oi, ow = oracle.router_topk(lg, k)
+    gi = layer.tap(moe.TAP_TOPK_IDX).cpu().numpy()
+    np.testing.assert_array_equal(gi, oi)
+    gw = layer.tap(moe.TAP_TOPK_W).cpu().double().numpy()
+    assert np.abs(gw - ow).max() <= 2e-6
+    off, perm, pos = oracle.sort_entries(gi, E)
+    np.testing.assert_array_equal(layer.tap(moe.TAP_EOFF).cpu().numpy(), off)
+    np.testing.assert_array_equal(layer.tap(moe.TAP_PERM).cpu().numpy(), perm)
+    np.testing.assert_array_equal(layer.tap(moe.TAP_POS).cpu().numpy(), pos)
+    return gi
+
+
+def _fp8_mid_distance(v):
+    """Distance of |v| (in fp8 units) to the nearest e4m3 rounding midpoint."""
+    tab = _e4m3_table()
+    fin = np.sort(np.unique(np.abs(tab[np.isfinite(tab)])))
+    mids = (fin[:-1] + fin[1:]) / 2
+    a = np.abs(v)
+    return np.abs(a[:, None] - mids[None, :]).min(axis=1)
+
+
+def _check_h_rows(oracle, w, x, gi, perm, hq, hs, rows, n_expert=256, k=8):
+    """Gate/up + SwiGLU + h quantisation, row by row: the GPU's e4m3 codes and
+    E8M0 scales equal the oracle's quantisation of fp32(h), except codes whose
+    fp64 value lies within 1e-4 * blockmax of a rounding midpoint (fp32 vs
+    fp64 accumulation order) and scales whose block amax lies within 1e-4 of a
+    power-of-two boundary.  Returns the number of such flips."""
+    xq, xs = oracle.quant_e4m3(x)
+    xd = oracle.dequant_e4m3(xq, xs)
+    flips = 0
+    T = x.shape[0]
+    for p in rows:
+        if p < T * k:
+            i = perm[p]
+            t, e = i // k, gi[i // k, i % k]
+            hg = oracle.expert_h(w["gate"][e], w["up"][e], xd[t])
+        else:
+            t = p - T * k
+            hg = oracle.expert_h(w["sh_gate"], w["sh_up"], xd[t])
+        oq, os_ = oracle.quant_e4m3(hg.astype(np.float32)[None])
+        for b in range(hg.size // 32):
+            sl = slice(32 * b, 32 * b + 32)
+            if hs[p, b] != os_[0, b]:
+                amax = np.abs(hg[sl]).max() / 448.0
+                rel = abs(amax / 2.0 ** np.round(np.log2(amax)) - 1)
+                assert rel < 1e-4, f"row {p} block {b}: scale {hs[p, b]} vs {os_[0, b]}"
+                flips += 1
+                continue
+            bad = np.nonzero(hq[p, sl] != oq[0, sl])[0]
+            if bad.size:
+                v = hg[sl] * 2.0 ** -(int(os_[0, b]) - 127)
+                d = _fp8_mid_distance(v[bad])
+                assert np.all(d <= 1e-4 * np.abs(v).max()), f"row {p} block {b}: codes {bad}"
+                flips += bad.size
+    return flips
+
+
+def _check_layer(name, dev, oracle, layer_w, x, lg, shg, sample=None, x_dtype=torch.float32):
+    w, dw = layer_w
+    T = x.shape[0]
+    layer, y32, y16 = _run_layer(dev, dw, x, lg, shg, x_dtype=x_dtype)
+    gi = _check_routing(layer, oracle, lg)
+    oq, os_ = oracle.quant_e4m3(x)
+    np.testing.assert_array_equal(layer.tap(moe.TAP_XQ).cpu().numpy(), oq)
+    np.testing.assert_array_equal(layer.tap(moe.TAP_XS).cpu().numpy(), os_)
+    # bf16 output is the RNE rounding of the f32 output
+    np.testing.assert_array_equal(y16, _bf16_of(y32))
+    toks = np.arange(T, dtype=np.int32) if sample is None else np.asarray(sample, np.int32)
+    perm = layer.tap(moe.TAP_PERM).cpu().numpy()
+    pos = layer.tap(moe.TAP_POS).cpu().numpy()
+    hq = layer.tap(moe.TAP_HQ).cpu().numpy()
+    hs = layer.tap(moe.TAP_HS).cpu().numpy()
+    # stage 1: gate/up/SwiGLU/h quantisation on the rows of the sampled tokens
+    rows = [int(pos[t * 8 + s]) for t in toks for s in range(8)]
+    if shg is not None:
+        rows += [T * 8 + int(t) for t in toks]
+    flips = _check_h_rows(oracle, w, x, gi, perm, hq, hs, rows)
+    # stage 2: down + combine from the GPU's own h
+    _, ow = oracle.router_topk(lg, 8)
+    ref_h = np.zeros((toks.size, x.shape[1]))
+    for j, t in enumerate(toks):
+        for s in range(8):
+            p = int(pos[t * 8 + s])
+            hd = oracle.dequant_e4m3(hq[p:p + 1], hs[p:p + 1])[0]
+            ref_h[j] += ow[t, s] * oracle.expert_down(w["down"][gi[t, s]], hd)
+        if shg is not None:
+            p = T * 8 + int(t)
+            hd = oracle.dequant_e4m3(hq[p:p + 1], hs[p:p + 1])[0]
+            ref_h[j] += 1 / (1 + np.exp(-float(shg[t]))) * oracle.expert_down(w["sh_down"], hd)
+    el_h, norm_h = _row_err(y32[toks], ref_h)
+    # stage 3: end to end against the full fp64 oracle
+    ref = oracle.moe_forward(w, x, lg, shg, tokens=toks)
+    el, normwise = _row_err(y32[toks], ref)
+    _, bf16_norm = _row_err(y16[toks], ref)
+    ref32 = oracle.moe_forward(w, x, lg, shg, act_mode=1, tokens=toks)
+    drift = float(np.abs(ref32 - ref).max() / np.abs(ref).max())
+    _metrics(name, T=int(T), tokens_checked=int(toks.size), h_rows=len(rows), h_flips=int(flips),
+             stage2_max_rel=norm_h, stage2_elementwise=el_h, e2e_max_rel=normwise,
+             e2e_elementwise=el, bf16_max_rel=bf16_norm, distinct_experts=int(np.unique(gi).size),
+             w4a32_drift=drift)
+    assert flips <= 0.01 * len(rows) * hq.shape[1]
+    assert norm_h <= TOL and el_h <= TOL, f"{name}: down/combine error {norm_h:.3g} / {el_h:.3g}"
+    assert normwise <= 1e-2, f"{name}: end-to-end max relative error {normwise:.3g}"
+    return layer
+
+
+def test_forward_decode1(dev, oracle, layer_w):
+    x, lg, _ = synth.config_inputs("decode1", 1)
+    _check_layer("decode1", dev, oracle, layer_w, x, lg, None)
+
+
+@pytest.mark.parametrize("T", [2, 7, 16, 33])
+def test_forward_small_batches(dev, oracle, layer_w, T):
+    rng = np.random.default_rng(300 + T)
+    x, lg = synth.hidden(rng, T), synth.normal_logits(rng, T)
+    _check_layer(f"small{T}", dev, oracle, layer_w, x, lg, None)
+
+
+def test_forward_ragged64_zipf(dev, oracle, layer_w):
+    x, lg, _ = synth.config_inputs("ragged64", 2)
+    _check_layer("ragged64", dev, oracle, layer_w, x, lg, None)
+
+
+def test_forward_prefill4096(dev, oracle, layer_w):
+    x, lg, _ = synth.config_inputs("prefill4096", 3)
+    rng = np.random.default_rng(33)
+    sample = np.sort(rng.choice(4096, size=48, replace=False))
+    _check_layer("prefill4096", dev, oracle, layer_w, x, lg, None, sample=sample)
+
+
+def test_forward_mixed_shared(dev, oracle, layer_w):
+    x, lg, shg = synth.config_inputs("mixed", 4)
+    rng = np.random.default_rng(44)
+    sample = np.concatenate([np.arange(6), 6 + np.sort(rng.choice(4000, size=40, replace=False))])
+    _check_layer("mixed", dev, oracle, layer_w, x, lg, shg, sample=sample)
+
+
+def test_forward_shared_small(dev, oracle, layer_w):
+    rng = np.random.default_rng(55)
+    x, lg = synth.hidden(rng, 5), synth.normal_logits(rng, 5)
+    shg = rng.standard_normal(5).astype(np.float32)
+    _check_layer("shared5", dev, oracle, layer_w, x, lg, shg)
+
+
+def test_forward_bf16_input(dev, oracle, layer_w):
+    """bf16 activations: the oracle sees the same values widened to f32."""
+    rng = np.random.default_rng(66)
+    x, lg = synth.hidden(rng, 9), synth.normal_logits(rng, 9)
+    xb = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    _check_layer("bf16_in", dev, oracle, layer_w, xb, lg, None, x_dtype=torch.bfloat16)
+
+
+def test_forward_deterministic_and_reusable(dev, layer_w):
+    """Two runs give identical bits; a smaller call after a larger one on the
+    same context matches a fresh context."""
+    _, dw = layer_w
+    rng = np.random.default_rng(77)
+    x, lg = synth.hidden(rng, 300), synth.normal_logits(rng, 300)
+    layer = moe.MoELayer(300)
+    xt, lt = torch.from_numpy(x).to(dev), torch.from_numpy(lg).to(dev)
+    a = layer.forward(dw, xt, lt, out_dtype=torch.float32).clone()
+    b = layer.forward(dw, xt, lt, out_dtype=torch.float32).clone()
+    assert torch.equal(a, b)
+    small = layer.forward(dw, xt[:3], lt[:3], out_dtype=torch.float32).clone()
+    fresh = moe.MoELayer(3).forward(dw, xt[:3], lt[:3], out_dtype=torch.float32)
+    assert torch.equal(small, fresh)
+
+
+def test_forward_empty_and_errors(dev, layer_w):
+    _, dw = layer_w
+    layer = moe.MoELayer(4)
+    x = torch.zeros((0, 2048), device=dev)
+    lg = torch.zeros((0, 256), device=dev)
+    out = layer.forward(dw, x, lg)
+    assert out.shape == (0, 2048)
+    with pytest.raises(moe.Q36MoEError):
+        layer.forward(dw, torch.zeros((5, 2048), device=dev), torch.zeros((5, 256), device=dev))
+    with pytest.raises(moe.Q36MoEError):
+        moe.MoELayer(4).forward(dw, torch.zeros((1, 2048)), torch.zeros((1, 256)))
