@@ -1,0 +1,229 @@
+"""Benchmark of the W4A8 MoE layer on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config decode1]
+
+A step is one MoE layer forward (router logits in, combined bf16 hidden out)
+over one batch of synthetic inputs already resident in HBM.  Weights rotate
+over --layers distinct seeded layers (40 x 428 MB = 17 GB by default) so the
+256 MB MALL cannot serve them.  Prints ONE JSON line (rank 0).
+
+Workload (configs of the q36 MoE layer, hidden 2048, 256 experts, top-8,
+expert FF 512, MXFP4 weights, e4m3 activations with per-32 E8M0 scales):
+  decode1      T=1, N(0,1) router logits (the headline configuration)
+  ragged64     T=64, Zipf(1.1) expert popularity
+  prefill4096  T=4096, N(0,1) logits
+  mixed        T=4006 (6x1 decode + 3000 + 1000 prefill) + shared expert
+
+The roofline object is for the dominant kernel of the configuration, timed
+with HIP events around that kernel on the stream it runs on; cpu_baseline is
+the C oracle's fp32 layer forward (oracle/liboracle.so) on host cores.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
+MFMA_FP8_PEAK_TFS = 5000.0   # dense FP8 MFMA (scaled f8f6f4 with an e4m3 operand)
+D, E, FF, K = 2048, 256, 512, 8
+MAT_BYTES = D * FF // 2 + D * FF // 32         # one packed expert matrix, 557,056 B
+EXPERT_BYTES = 3 * MAT_BYTES                   # gate + up + down, 1,671,168 B
+
+CONFIGS = {
+    "decode1": dict(T=1, shared=False, steps=2000, warmup=200),
+    "ragged64": dict(T=64, shared=False, steps=1000, warmup=100),
+    "prefill4096": dict(T=4096, shared=False, steps=100, warmup=10),
+    "mixed": dict(T=4006, shared=True, steps=100, warmup=10),
+}
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=None)
+    ap.add_argument("--warmup", type=int, default=None)
+    ap.add_argument("--config", default="decode1", choices=sorted(CONFIGS))
+    ap.add_argument("--layers", type=int, default=40)
+    ap.add_argument("--inputs", type=int, default=16, help="distinct input batches cycled")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--seed", type=int, default=1234)
+    return ap.parse_args()
+
+
+def make_inputs(cfg_name, T, n, seed, dev):
+    import torch
+    from q36_amd import synth
+    xs, ls, ss = [], [], []
+    for j in range(n):
+        rng = np.random.default_rng(seed + j)
+        x = synth.hidden(rng, T)
+        if cfg_name == "ragged64":
+            lg = synth.zipf_logits(rng, T)
+        else:
+            lg = synth.normal_logits(rng, T)
+        xs.append(torch.from_numpy(x).to(dev))
+        ls.append(torch.from_numpy(lg).to(dev))
+        ss.append(torch.from_numpy(rng.standard_normal(T).astype(np.float32)).to(dev))
+    return xs, ls, ss
+
+
+def distinct_experts(layer, moe):
+    idx = layer.tap(moe.TAP_TOPK_IDX).cpu().numpy()
+    return int(np.unique(idx).size)
+
+
+def kernel_bytes(stage, T, U, shared):
+    """Algorithmic HBM bytes of one launch of a stage.  U = distinct routed
+    experts hit; P = routed (token, slot) rows, plus T shared rows."""
+    P = T * K + (T if shared else 0)
+    Ue = U + (1 if shared else 0)
+    xq = T * D + T * D // 32
+    hq = P * FF + P * FF // 32
+    if stage == "gateup":
+        # gate+up weights of the hit experts, the e4m3 activations, h out
+        return Ue * 2 * MAT_BYTES + xq + hq
+    if stage == "down":
+        # down weights, h in, weighted f32 rows out
+        return Ue * MAT_BYTES + hq + P * D * 4
+    raise ValueError(stage)
+
+
+def kernel_flops(stage, T, shared):
+    P = T * K + (T if shared else 0)
+    return P * (2 * D * 2 * FF if stage == "gateup" else 2 * FF * D)
+
+
+def cpu_baseline(cfg_name, T, seconds, shared):
+    """The C oracle's fp32 layer forward on host cores over a bounded sample
+    of tokens of the same configuration."""
+    from oracle import pyoracle
+    from q36_amd import synth
+    pyoracle.lib()
+    nth = len(os.sched_getaffinity(0))
+    w = synth.expert_weights(7, shared=shared)
+    rng = np.random.default_rng(8)
+    n = 0
+    t0 = time.perf_counter()
+    tokens = 0
+    while time.perf_counter() - t0 < seconds:
+        Tb = min(T, 4)
+        x = synth.hidden(rng, Tb)
+        lg = synth.zipf_logits(rng, Tb) if cfg_name == "ragged64" else synth.normal_logits(rng, Tb)
+        shg = rng.standard_normal(Tb).astype(np.float32) if shared else None
+        t1 = time.perf_counter()
+        pyoracle.moe_forward_f32(w, x, lg, shg, nthreads=nth)
+        n += time.perf_counter() - t1
+        tokens += Tb
+    return {"value": tokens / n, "unit": "tokens/s", "cores": nth, "kind": "port",
+            "sample": f"{tokens} tokens of {cfg_name} (batches of <=4) through or_moe_forward_f32, "
+                      f"{n:.1f} s, OpenMP {nth} threads"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU; --gpus must be 1 "
+                                   "(expert-parallel sharding is described in DESIGN.md, not run)"}))
+        sys.exit(2)
+    import torch
+    from q36_amd import moe
+
+    cfg = CONFIGS[args.config]
+    T, shared = cfg["T"], cfg["shared"]
+    steps = args.steps if args.steps is not None else cfg["steps"]
+    warmup = args.warmup if args.warmup is not None else cfg["warmup"]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream()
+
+    layers = []
+    for l in range(args.layers):
+        w = moe.MoEWeights.alloc(E, D, FF, FF if shared else 0)
+        w.fill_synthetic(args.seed * 1000 + l)
+        layers.append(w)
+    xs, ls, ss = make_inputs(args.config, T, args.inputs, args.seed, dev)
+    layer = moe.MoELayer(T, stream=stream)
+    out = torch.empty((T, D), dtype=torch.bfloat16, device=dev)
+    torch.cuda.synchronize()
+
+    def step(i):
+        j = i % args.inputs
+        layer.forward(layers[i % args.layers], xs[j], ls[j], ss[j] if shared else None,
+                      out=out)
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    for i in range(steps):
+        step(warmup + i)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / steps
+
+    # per-stage pass: HIP events around each kernel on the context stream
+    layer.set_timing(True)
+    layer.stage_times(reset=True)
+    U_sum = 0
+    n_stage = min(steps, 200)
+    for i in range(n_stage):
+        step(i)
+        U_sum += distinct_experts(layer, moe)
+    stages = layer.stage_times(reset=True)
+    layer.set_timing(False)
+    U = U_sum / n_stage
+    st_us = {k: 1e3 * v[0] / max(v[1], 1) for k, v in stages.items()}
+    dom = "gateup" if st_us["gateup"] >= st_us["down"] else "down"
+    prefill = T >= 256
+    if prefill:
+        fl = kernel_flops(dom, T, shared)
+        ach = fl / (st_us[dom] * 1e-6) / 1e12
+        roof = {"bound": "mfma", "achieved": ach, "peak": MFMA_FP8_PEAK_TFS, "unit": "TFLOP/s",
+                "frac": ach / MFMA_FP8_PEAK_TFS, "traffic": None, "kernel": dom,
+                "kernel_us": st_us[dom], "flops_per_launch": fl,
+                "hbm_gbs": kernel_bytes(dom, T, U, shared) / (st_us[dom] * 1e-6) / 1e9}
+    else:
+        by = kernel_bytes(dom, T, U, shared)
+        ach = by / (st_us[dom] * 1e-6) / 1e9
+        roof = {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": ach / HBM_PEAK_GBS, "traffic": None, "kernel": dom,
+                "kernel_us": st_us[dom], "bytes_per_launch": by}
+
+    layer_bytes = (U + (1 if shared else 0)) * EXPERT_BYTES + T * (D * 4 + E * 4 + D * 2)
+    res = {
+        "metric": "MoE layer tokens/s (W4A8, 1 GPU)",
+        "value": T / (ms * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": ms,
+        "us_per_layer": ms * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8e4m3 x mxfp4 (fp32 accumulate, bf16 out)",
+        "data": "synthetic (seeded MXFP4 weights filled on device, N(0,1) x and logits)",
+        "config": {"workload": args.config, "tokens": T, "d_model": D, "n_expert": E,
+                   "top_k": K, "d_ff": FF, "shared_expert": shared,
+                   "weight_layers_rotated": args.layers},
+        "layer_hbm_fraction": layer_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "distinct_experts_avg": U,
+        "stage_us": st_us,
+        "roofline": roof,
+    }
+    if not args.no_cpu:
+        res["cpu_baseline"] = cpu_baseline(args.config, T, args.cpu_seconds, shared)
+    print(json.dumps(res))
+
+
+if __name__ == "__main__":
+    main()

@@ -85,6 +85,14 @@ int q36moe_weights_device_ptrs(const q36moe_weights *w, void **gate, void **up,
                                void **sh_down, size_t *gate_bytes, size_t *down_bytes);
 void q36moe_weights_free(q36moe_weights *w);
 
+/* Fill every packed matrix of w on the device with seeded synthetic MXFP4
+ * data: E2M1 codes uniform over the 16 values, E8M0 exponent bytes uniform
+ * in [127+exp_lo, 127+exp_hi] (a counter-based hash of seed and byte index,
+ * so the same seed gives the same bytes).  For benchmarks that need many
+ * distinct layers resident in HBM. */
+int q36moe_weights_fill_synthetic(q36moe_weights *w, uint64_t seed, int exp_lo, int exp_hi,
+                                  void *stream);
+
 /* Host-side repack of one [M][K] GGUF block_mxfp4 matrix into the packed
  * device layout (and back).  Pure host code; used by upload and by tests. */
 int q36moe_pack_mxfp4(const void *gguf_blocks, int M, int K, void *packed);

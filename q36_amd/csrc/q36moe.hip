@@ -554,6 +554,31 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ dnw,
 }
 
 // ---------------------------------------------------------------------------
+// synthetic weights (benchmarks)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+
+// Region [0, nib) gets uniform bytes, [nib, nib + scl) exponent bytes in
+// [lo, lo + span); 16 bytes per thread.
+__global__ __launch_bounds__(256) void k_fill(uint8_t *dst, size_t nib, size_t scl, uint64_t seed,
+                                             int lo, int span) {
+    const size_t i = ((size_t)blockIdx.x * 256 + threadIdx.x) * 16;
+    if (i >= nib + scl) return;
+    const uint64_t a = mix64(seed ^ (i * 0x9e3779b97f4a7c15ull));
+    const uint64_t b = mix64(a ^ 0x632be59bd9b4e019ull);
+    uint8_t v[16];
+    for (int j = 0; j < 16; j++) {
+        const uint8_t r = (uint8_t)((j < 8 ? a : b) >> (8 * (j & 7)));
+        v[j] = (i + j < nib) ? r : (uint8_t)(lo + (int)(((uint32_t)r * (uint32_t)span) >> 8));
+    }
+    *reinterpret_cast<uint4 *>(dst + i) = *reinterpret_cast<const uint4 *>(v);
+}
+
+// ---------------------------------------------------------------------------
 // calibration probe: one scaled MFMA on caller-packed lane operands
 // ---------------------------------------------------------------------------
 template <int FA, int FB>
@@ -707,6 +732,29 @@ int q36moe_weights_upload(const void *gate, const void *up, const void *down, co
     }
     *out = w;
     return Q36MOE_OK;
+}
+
+int q36moe_weights_fill_synthetic(q36moe_weights *w, uint64_t seed, int exp_lo, int exp_hi,
+                                  void *stream) {
+    if (!w || exp_lo > exp_hi || exp_lo < -127 || exp_hi > 127) return Q36MOE_EINVAL;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const size_t m = (size_t)w->D * w->FF, nib = m / 2, scl = m / 32;
+    uint8_t *mats[3] = {w->gate, w->up, w->down};
+    uint64_t salt = 1;
+    for (int k = 0; k < 3; k++)
+        for (int e = 0; e < w->E; e++, salt++) {
+            hipLaunchKernelGGL(k_fill, dim3((unsigned)((nib + scl) / 16 / 256 + 1)), dim3(256), 0, s,
+                               mats[k] + w->gu_bytes * e, nib, scl, seed * 0x100000001b3ull + salt,
+                               127 + exp_lo, exp_hi - exp_lo + 1);
+        }
+    if (w->FFsh) {
+        uint8_t *sh[3] = {w->sh_gate, w->sh_up, w->sh_down};
+        for (int k = 0; k < 3; k++, salt++)
+            hipLaunchKernelGGL(k_fill, dim3((unsigned)((nib + scl) / 16 / 256 + 1)), dim3(256), 0, s,
+                               sh[k], nib, scl, seed * 0x100000001b3ull + salt, 127 + exp_lo,
+                               exp_hi - exp_lo + 1);
+    }
+    return hip_rc(hipGetLastError());
 }
 
 int q36moe_weights_device_ptrs(const q36moe_weights *w, void **gate, void **up, void **down,

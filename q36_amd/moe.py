@@ -46,6 +46,7 @@ def lib():
     L.q36moe_weights_upload.argtypes = [vp] * 6 + [i] * 4 + [pp]
     L.q36moe_weights_alloc.argtypes = [i] * 4 + [pp]
     L.q36moe_weights_device_ptrs.argtypes = [vp] + [pp] * 6 + [ctypes.POINTER(sz)] * 2
+    L.q36moe_weights_fill_synthetic.argtypes = [vp, ctypes.c_uint64, i, i, vp]
     L.q36moe_weights_free.argtypes = [vp]
     L.q36moe_weights_free.restype = None
     L.q36moe_pack_mxfp4.argtypes = [vp, i, i, vp]
@@ -138,6 +139,12 @@ class MoEWeights:
         check(lib().q36moe_weights_alloc(n_expert, d_model, d_ff, d_ff_sh, ctypes.byref(h)),
               "q36moe_weights_alloc")
         return cls(h, n_expert, d_model, d_ff, d_ff_sh)
+
+    def fill_synthetic(self, seed, exp_lo=-8, exp_hi=0, stream=None):
+        """Seeded synthetic MXFP4 contents written on the device."""
+        check(lib().q36moe_weights_fill_synthetic(self._h, seed, exp_lo, exp_hi, _stream(stream)),
+              "q36moe_weights_fill_synthetic")
+        return self
 
     def device_ptrs(self):
         """dict name -> (device address, bytes of the whole region)."""
