@@ -122,6 +122,16 @@ int q36moe_router_topk(const float *logits, int T, int n_expert, int ld, int k,
 int q36moe_quant_e4m3(const void *x, int x_fmt, int T, int K,
                       uint8_t *xq, uint8_t *xs, void *stream);
 
+/* Execution path of q36moe_forward.  The sorted path (route + sort + grouped
+ * expert GEMMs + combine) serves any T; the direct path (two kernels, no
+ * sort, slots combined in registers) serves T <= 16.  mode 0 picks the
+ * direct path for T <= 16, 1 forces sorted, 2 forces direct (EINVAL from
+ * forward when T > 16).  last_path: 0 sorted, 1 direct.  With the direct
+ * path the PERM/POS taps are the identity (rows in entry order) and the
+ * EOFF/DNW taps are unavailable. */
+int q36moe_ctx_set_path(q36moe_ctx *c, int mode);
+int q36moe_ctx_last_path(const q36moe_ctx *c);
+
 /* Copy one internal buffer of the last forward into dst (device pointer,
  * at most `bytes`); *written receives the byte count. */
 int q36moe_ctx_copy_tap(q36moe_ctx *c, int tap, void *dst, size_t bytes, size_t *written);

@@ -39,6 +39,7 @@ constexpr int kRouteTPB = 64;      // tokens per k_route workgroup
 constexpr int kRouteThreads = 1024;
 constexpr int kScanThreads = 1024;
 constexpr int kLdsRow = 144;       // LDS row stride of one 128-byte K-step slice
+constexpr int kDirectMaxT = 16;    // largest batch routed to the direct (unsorted) path
 
 // ---------------------------------------------------------------------------
 // scalar formats
@@ -176,6 +177,59 @@ __device__ void route_token(const float *__restrict__ l, int E, int k, float sca
             if (lds_ent) lds_ent[r] = ir[r];
         }
     }
+}
+
+// The pick of one slot s only, returned to every lane (same arithmetic and
+// tie order as route_token; renormalised weight, times scale).
+__device__ __forceinline__ void route_token_slot(const float *__restrict__ l, int E, int k, float scale,
+                                                 int s, int lane, int &e_out, float &w_out) {
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int e = lane + 64 * j;
+        v[j] = e < E ? l[e] : -INFINITY;
+    }
+    float m = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    float sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) sum += (lane + 64 * j < E) ? expf(v[j] - m) : 0.0f;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+    uint32_t taken = 0;
+    float wsum = 0.0f, ws = 0.0f;
+    int es = 0;
+    for (int r = 0; r < k; r++) {
+        float bv = -INFINITY;
+        int bi = -1;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int e = lane + 64 * j;
+            if (e < E && !((taken >> j) & 1u) && (bi < 0 || v[j] > bv)) {
+                bv = v[j];
+                bi = e;
+            }
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(bv, o, 64);
+            const int oi = __shfl_xor(bi, o, 64);
+            if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+        if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+        const float w = expf(bv - m) / sum;
+        wsum += w;
+        if (r == s) {
+            ws = w;
+            es = bi;
+        }
+    }
+    e_out = es;
+    w_out = ws / wsum * scale;
 }
 
 // Quantise one 32-element block (per-32 E8M0 + e4m3), q36_engine.cu:2411-2428.
@@ -524,6 +578,218 @@ __global__ __launch_bounds__(256) void k_expert_gemm(GemmArgs A) {
 }
 
 // ---------------------------------------------------------------------------
+// direct path for small batches (decode): no sort, two kernels
+// ---------------------------------------------------------------------------
+struct DirectArgs {
+    const float *logits; int ld; int T; int E; int k; float scale;
+    const void *x; int x_fmt;
+    const float *shg;
+    const uint8_t *gate, *up, *down;            // routed experts (packed)
+    const uint8_t *sh_gate, *sh_up, *sh_down;   // shared expert (packed) or null
+    size_t wstride;                             // bytes per packed matrix
+    int32_t *idx; float *wt;                    // routing of each entry
+    int32_t *pos; int32_t *perm;                // identity maps (entry order)
+    uint8_t *xq; uint8_t *xs;                   // quantised x (tap)
+    float *hf;                                  // [entries][FF] fp32 SwiGLU rows
+    uint8_t *hq; uint8_t *hs;                   // quantised h (tap)
+    void *out; int out_fmt;
+};
+
+constexpr int kDD = 2048;   // d_model of the instantiated kernels
+constexpr int kDF = 512;    // d_ff
+
+// Quantise 8 consecutive values held by one lane; lanes 4j..4j+3 form one
+// 32-value block (amax via two xor-shuffles).  Writes 8 e4m3 bytes and,
+// from the first lane of the block, the E8M0 byte.
+__device__ __forceinline__ void quant8_lane(const float (&v)[8], int lane, uint8_t *q, uint8_t *sc) {
+    float a = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) a = fmaxf(a, fabsf(v[i]));
+    a = fmaxf(a, __shfl_xor(a, 1, 64));
+    a = fmaxf(a, __shfl_xor(a, 2, 64));
+    const int e2 = quant_exp(a);
+    const float mul = inv_scale(e2);
+    const uint32_t w0 = e4m3_encode(v[0] * mul) | (e4m3_encode(v[1] * mul) << 8) |
+                        (e4m3_encode(v[2] * mul) << 16) | (e4m3_encode(v[3] * mul) << 24);
+    const uint32_t w1 = e4m3_encode(v[4] * mul) | (e4m3_encode(v[5] * mul) << 8) |
+                        (e4m3_encode(v[6] * mul) << 16) | (e4m3_encode(v[7] * mul) << 24);
+    *reinterpret_cast<uint2 *>(q) = make_uint2(w0, w1);
+    if ((lane & 3) == 0) *sc = (uint8_t)(127 + e2);
+}
+
+__device__ __forceinline__ void load8(const void *x, int fmt, size_t off, float (&v)[8]) {
+    if (fmt == Q36MOE_FMT_F32) {
+        const float4 *p = reinterpret_cast<const float4 *>(static_cast<const float *>(x) + off);
+        const float4 a = p[0], b = p[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+        const uint4 t = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(x) + off);
+        const uint32_t w[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            v[2 * j] = __uint_as_float(w[j] << 16);
+            v[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+        }
+    }
+}
+
+// Entry i (token t, slot s; or the shared expert of token t for i >= T*k)
+// x 16 rows of gate and up.  Wave w reduces K range [512w, 512w+512): it
+// quantises exactly that range of x into LDS, so no cross-wave exchange is
+// needed before the MFMAs.  Partial sums meet in LDS in wave order.
+__global__ __launch_bounds__(256) void k_direct_gateup(DirectArgs A) {
+    __shared__ __align__(16) uint8_t sx[kDD + 32];   // + 32 zero bytes
+    __shared__ uint8_t sxs[kDD / 32];
+    __shared__ float red[4][2][16];
+    const int i = blockIdx.x, ft = blockIdx.y;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int nr = A.T * A.k;
+    const bool routed = i < nr;
+    const int t = routed ? i / A.k : i - nr;
+    const int s = routed ? i % A.k : 0;
+
+    // issue this wave's x loads first (512 values, 8 per lane)
+    float xv[8];
+    load8(A.x, A.x_fmt, (size_t)t * kDD + wave * 512 + lane * 8, xv);
+
+    int e = A.E;
+    float wgt = 0.0f;
+    if (routed) {
+        // every wave routes the token (no barrier needed to share the result)
+        route_token_slot(A.logits + (size_t)t * A.ld, A.E, A.k, A.scale, s, lane, e, wgt);
+    } else {
+        wgt = 1.0f / (1.0f + expf(-A.shg[t]));
+    }
+    const uint8_t *Wg = (e < A.E) ? A.gate + (size_t)e * A.wstride : A.sh_gate;
+    const uint8_t *Wu = (e < A.E) ? A.up + (size_t)e * A.wstride : A.sh_up;
+    const size_t nib = (size_t)kDF * kDD / 2;
+    uint4 ag[4], au[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const size_t o = ((size_t)ft * (kDD / 128) + wave * 4 + j) * 1024 + (size_t)lane * 16;
+        ag[j] = *reinterpret_cast<const uint4 *>(Wg + o);
+        au[j] = *reinterpret_cast<const uint4 *>(Wu + o);
+    }
+    const size_t so = nib + ((size_t)ft * 64 + lane) * (kDD / 128) + wave * 4;
+    const int sag = *reinterpret_cast<const int *>(Wg + so);
+    const int sau = *reinterpret_cast<const int *>(Wu + so);
+
+    quant8_lane(xv, lane, sx + wave * 512 + lane * 8, sxs + wave * 16 + (lane >> 2));
+    if (threadIdx.x < 8) reinterpret_cast<uint32_t *>(sx + kDD)[threadIdx.x] = 0u;
+    __syncthreads();
+
+    // B fragment: column 0 is the token; lanes of other columns read zeros
+    const int q = lane >> 4;
+    const bool col0 = (lane & 15) == 0;
+    v4f cg = {0.f, 0.f, 0.f, 0.f}, cu = {0.f, 0.f, 0.f, 0.f};
+    static_for<0, 4>([&](auto J) {
+        constexpr int j = decltype(J)::value;
+        const int kt = wave * 4 + j;
+        const uint8_t *b0p = col0 ? sx + kt * 128 + 16 * q : sx + kDD;
+        const uint8_t *b1p = col0 ? sx + kt * 128 + 64 + 16 * q : sx + kDD + 16;
+        const uint4 b0 = *reinterpret_cast<const uint4 *>(b0p);
+        const uint4 b1 = *reinterpret_cast<const uint4 *>(b1p);
+        const v8i b = v8i{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w,
+                          (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+        const int sb = sxs[kt * 4 + q];
+        const v8i a0 = v8i{(int)ag[j].x, (int)ag[j].y, (int)ag[j].z, (int)ag[j].w, 0, 0, 0, 0};
+        const v8i a1 = v8i{(int)au[j].x, (int)au[j].y, (int)au[j].z, (int)au[j].w, 0, 0, 0, 0};
+        cg = mfma_f4xf8<j>(a0, b, cg, sag, sb);
+        cu = mfma_f4xf8<j>(a1, b, cu, sau, sb);
+    });
+    if (col0) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            red[wave][0][4 * q + r] = cg[r];
+            red[wave][1][4 * q + r] = cu[r];
+        }
+    }
+    __syncthreads();
+    if (wave == 0 && lane < 16) {
+        const float g = red[0][0][lane] + red[1][0][lane] + red[2][0][lane] + red[3][0][lane];
+        const float u = red[0][1][lane] + red[1][1][lane] + red[2][1][lane] + red[3][1][lane];
+        A.hf[(size_t)i * kDF + ft * 16 + lane] = silu(g) * u;
+    }
+    if (ft == 0) {
+        if (threadIdx.x == 0 && routed) {
+            A.idx[i] = e;
+            A.wt[i] = wgt;
+            A.pos[i] = i;
+            A.perm[i] = i;
+        }
+        if (routed && s == 0) {    // quantised x of token t (tap)
+            for (int c = threadIdx.x; c < kDD / 16; c += 256)
+                *reinterpret_cast<uint4 *>(A.xq + (size_t)t * kDD + c * 16) =
+                    *reinterpret_cast<const uint4 *>(sx + c * 16);
+            if (threadIdx.x < kDD / 32) A.xs[(size_t)t * (kDD / 32) + threadIdx.x] = sxs[threadIdx.x];
+        }
+    }
+}
+
+// Token t x 16 output rows; wave s handles slot s (wave k: shared expert):
+// quantises its SwiGLU row, multiplies by the 16x512 down tile, scales by
+// the routing weight; wave 0 adds the slots in order (k_moe_combine order,
+// q36_engine.cu:784-791) and writes the output rows.
+__global__ __launch_bounds__(576) void k_direct_down(DirectArgs A) {
+    __shared__ __align__(16) uint8_t sh[kMaxTopK + 1][kDF + 32];
+    __shared__ uint8_t shs[kMaxTopK + 1][kDF / 32];
+    __shared__ float red[kMaxTopK + 1][16];
+    const int rt = blockIdx.x, t = blockIdx.y;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int nslot = blockDim.x >> 6;
+    const int nr = A.T * A.k;
+    const bool routed = wave < A.k;
+    const int i = routed ? t * A.k + wave : nr + t;
+    const int e = routed ? A.idx[i] : A.E;
+    const float wgt = routed ? A.wt[i] : 1.0f / (1.0f + expf(-A.shg[t]));
+    const uint8_t *W = (e < A.E) ? A.down + (size_t)e * A.wstride : A.sh_down;
+    const size_t nib = (size_t)kDD * kDF / 2;
+    uint4 a[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+        a[j] = *reinterpret_cast<const uint4 *>(W + ((size_t)rt * 4 + j) * 1024 + (size_t)lane * 16);
+    const int sa = *reinterpret_cast<const int *>(W + nib + ((size_t)rt * 64 + lane) * 4);
+
+    float hv[8];
+    load8(A.hf, Q36MOE_FMT_F32, (size_t)i * kDF + lane * 8, hv);
+    quant8_lane(hv, lane, &sh[wave][lane * 8], &shs[wave][lane >> 2]);
+    if (lane < 8) reinterpret_cast<uint32_t *>(&sh[wave][kDF])[lane] = 0u;
+    if (rt == 0) {   // quantised h (tap)
+        *reinterpret_cast<uint2 *>(A.hq + (size_t)i * kDF + lane * 8) =
+            *reinterpret_cast<const uint2 *>(&sh[wave][lane * 8]);
+        if ((lane & 3) == 0) A.hs[(size_t)i * (kDF / 32) + (lane >> 2)] = shs[wave][lane >> 2];
+    }
+    __syncthreads();
+    const int q = lane >> 4;
+    const bool col0 = (lane & 15) == 0;
+    v4f c = {0.f, 0.f, 0.f, 0.f};
+    static_for<0, 4>([&](auto J) {
+        constexpr int j = decltype(J)::value;
+        const uint8_t *b0p = col0 ? &sh[wave][j * 128 + 16 * q] : &sh[wave][kDF];
+        const uint8_t *b1p = col0 ? &sh[wave][j * 128 + 64 + 16 * q] : &sh[wave][kDF + 16];
+        const uint4 b0 = *reinterpret_cast<const uint4 *>(b0p);
+        const uint4 b1 = *reinterpret_cast<const uint4 *>(b1p);
+        const v8i b = v8i{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w,
+                          (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+        const int sb = shs[wave][j * 4 + q];
+        const v8i av = v8i{(int)a[j].x, (int)a[j].y, (int)a[j].z, (int)a[j].w, 0, 0, 0, 0};
+        c = mfma_f4xf8<j>(av, b, c, sa, sb);
+    });
+    if (col0) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) red[wave][4 * q + r] = c[r] * wgt;
+    }
+    __syncthreads();
+    if (wave == 0 && lane < 16) {
+        float acc = 0.0f;
+        for (int sl = 0; sl < nslot; sl++) acc += red[sl][lane];
+        const size_t o = (size_t)t * kDD + rt * 16 + lane;
+        if (A.out_fmt == Q36MOE_FMT_F32) static_cast<float *>(A.out)[o] = acc;
+        else static_cast<uint16_t *>(A.out)[o] = (uint16_t)f32_to_bf16(acc);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // combine
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ dnw,
@@ -636,7 +902,9 @@ struct q36moe_ctx {
     int4 *tiles; int32_t *ntiles;
     uint8_t *hq, *hs;
     float *dnw;
-    int last_T, last_sh;
+    float *hf;                      // direct path: fp32 SwiGLU rows
+    int path_mode;                  // 0 auto, 1 sorted, 2 direct
+    int last_T, last_sh, last_path;
     int timing;
     hipEvent_t ev[ST_COUNT + 1];
     double ms[ST_COUNT];
@@ -805,6 +1073,8 @@ int q36moe_ctx_create(int max_tokens, int n_expert, int d_model, int d_ff, int t
     const size_t o_tiles = take(c->tile_cap * 16), o_nt = take(4);
     const size_t o_hq = take(rows * d_ff), o_hs = take(rows * d_ff / 32);
     const size_t o_dnw = take(rows * d_model * 4);
+    const size_t direct_rows = (size_t)(max_tokens < kDirectMaxT ? max_tokens : kDirectMaxT) * (top_k + 1);
+    const size_t o_hf = take(direct_rows * d_ff * 4);
     if (hipMalloc(&c->base, off) != hipSuccess) {
         delete c;
         return Q36MOE_ENOMEM;
@@ -825,6 +1095,7 @@ int q36moe_ctx_create(int max_tokens, int n_expert, int d_model, int d_ff, int t
     c->ntiles = reinterpret_cast<int32_t *>(b + o_nt);
     c->hq = b + o_hq; c->hs = b + o_hs;
     c->dnw = reinterpret_cast<float *>(b + o_dnw);
+    c->hf = reinterpret_cast<float *>(b + o_hf);
     for (int i = 0; i <= ST_COUNT; i++) {
         if (hipEventCreate(&c->ev[i]) != hipSuccess) {
             for (int j = 0; j < i; j++) (void)hipEventDestroy(c->ev[j]);
@@ -876,6 +1147,23 @@ int q36moe_forward(q36moe_ctx *c, const q36moe_weights *w, const void *x, int x_
         if (c->timing) (void)hipEventRecord(c->ev[st], s);
     };
 
+    const bool direct = c->path_mode == 2 ? (T <= kDirectMaxT)
+                        : c->path_mode == 1 ? false : (T <= kDirectMaxT);
+    if (c->path_mode == 2 && !direct) return Q36MOE_EINVAL;
+    if (direct) {
+        DirectArgs da{logits, ld_logits, T, E, K, scale, x, x_fmt, shg,
+                      w->gate, w->up, w->down, w->sh_gate, w->sh_up, w->sh_down, w->gu_bytes,
+                      c->topk_idx, c->topk_w, c->pos, c->perm, c->xq, c->xs, c->hf, c->hq, c->hs,
+                      out, out_fmt};
+        mark(ST_ROUTE);
+        mark(ST_SCAN);
+        mark(ST_GATEUP);
+        hipLaunchKernelGGL(k_direct_gateup, dim3(n + (has_sh ? T : 0), FF / 16), dim3(256), 0, s, da);
+        mark(ST_DOWN);
+        hipLaunchKernelGGL(k_direct_down, dim3(D / 16, T), dim3(64 * (K + has_sh)), 0, s, da);
+        mark(ST_COMBINE);
+        mark(ST_COUNT);
+    } else {
     mark(ST_ROUTE);
     RouteArgs ra{logits, ld_logits, T, E, K, scale, x, x_fmt, D,
                  c->topk_idx, c->topk_w, c->xq, c->xs, c->blk_cnt, c->rank};
@@ -908,8 +1196,10 @@ int q36moe_forward(q36moe_ctx *c, const q36moe_weights *w, const void *x, int x_
     hipLaunchKernelGGL(k_combine, dim3(T), dim3(256), 0, s, c->dnw, c->pos, T, K, D, has_sh, out,
                        out_fmt);
     mark(ST_COUNT);
+    }
     c->last_T = T;
     c->last_sh = has_sh;
+    c->last_path = direct ? 1 : 0;
     if (hipGetLastError() != hipSuccess) return Q36MOE_EHIP;
     if (c->timing) {
         if (hipEventSynchronize(c->ev[ST_COUNT]) != hipSuccess) return Q36MOE_EHIP;
@@ -957,12 +1247,16 @@ int q36moe_ctx_copy_tap(q36moe_ctx *c, int tap, void *dst, size_t bytes, size_t 
         case Q36MOE_TAP_TOPK_W: src = c->topk_w; sz = n * 4; break;
         case Q36MOE_TAP_XQ: src = c->xq; sz = T * c->D; break;
         case Q36MOE_TAP_XS: src = c->xs; sz = T * c->D / 32; break;
-        case Q36MOE_TAP_EOFF: src = c->e_off; sz = (size_t)(c->E + 1) * 4; break;
+        case Q36MOE_TAP_EOFF:
+            if (c->last_path == 1) return Q36MOE_EINVAL;   // the direct path does not sort
+            src = c->e_off; sz = (size_t)(c->E + 1) * 4; break;
         case Q36MOE_TAP_PERM: src = c->perm; sz = n * 4; break;
         case Q36MOE_TAP_POS: src = c->pos; sz = n * 4; break;
         case Q36MOE_TAP_HQ: src = c->hq; sz = rows * c->FF; break;
         case Q36MOE_TAP_HS: src = c->hs; sz = rows * c->FF / 32; break;
-        case Q36MOE_TAP_DNW: src = c->dnw; sz = rows * c->D * 4; break;
+        case Q36MOE_TAP_DNW:
+            if (c->last_path == 1) return Q36MOE_EINVAL;   // combined in registers
+            src = c->dnw; sz = rows * c->D * 4; break;
         default: return Q36MOE_EINVAL;
     }
     if (bytes < sz) return Q36MOE_EINVAL;
@@ -970,6 +1264,14 @@ int q36moe_ctx_copy_tap(q36moe_ctx *c, int tap, void *dst, size_t bytes, size_t 
     if (sz == 0) return Q36MOE_OK;
     return hip_rc(hipMemcpyAsync(dst, src, sz, hipMemcpyDeviceToDevice, c->stream));
 }
+
+int q36moe_ctx_set_path(q36moe_ctx *c, int mode) {
+    if (!c || mode < 0 || mode > 2) return Q36MOE_EINVAL;
+    c->path_mode = mode;
+    return Q36MOE_OK;
+}
+
+int q36moe_ctx_last_path(const q36moe_ctx *c) { return c ? c->last_path : Q36MOE_EINVAL; }
 
 int q36moe_ctx_set_timing(q36moe_ctx *c, int on) {
     if (!c) return Q36MOE_EINVAL;

@@ -59,6 +59,8 @@ def lib():
     L.q36moe_router_topk.argtypes = [vp, i, i, i, i, f, i, vp, vp, vp]
     L.q36moe_quant_e4m3.argtypes = [vp, i, i, i, vp, vp, vp]
     L.q36moe_ctx_copy_tap.argtypes = [vp, i, vp, sz, ctypes.POINTER(sz)]
+    L.q36moe_ctx_set_path.argtypes = [vp, i]
+    L.q36moe_ctx_last_path.argtypes = [vp]
     L.q36moe_ctx_set_timing.argtypes = [vp, i]
     L.q36moe_ctx_stage_times.argtypes = [vp, ctypes.POINTER(ctypes.c_double),
                                          ctypes.POINTER(ctypes.c_int), i, i]
@@ -255,6 +257,17 @@ class MoELayer:
                                         dst.numel() * dst.element_size(), ctypes.byref(n)),
               "q36moe_ctx_copy_tap")
         return dst
+
+    PATH_AUTO, PATH_SORTED, PATH_DIRECT = 0, 1, 2
+
+    def set_path(self, mode):
+        """0 auto (direct for T <= 16), 1 sorted, 2 direct."""
+        check(lib().q36moe_ctx_set_path(self._h, mode), "q36moe_ctx_set_path")
+
+    @property
+    def last_path(self):
+        """0 sorted, 1 direct."""
+        return lib().q36moe_ctx_last_path(self._h)
 
     def set_timing(self, on):
         check(lib().q36moe_ctx_set_timing(self._h, 1 if on else 0), "q36moe_ctx_set_timing")

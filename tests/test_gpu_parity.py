@@ -197,9 +197,10 @@ def _bf16_of(y32):
     return torch.from_numpy(y32.astype(np.float32)).to(torch.bfloat16).float().numpy()
 
 
-def _run_layer(dev, dw, x, lg, shg, max_tokens=None, x_dtype=torch.float32):
+def _run_layer(dev, dw, x, lg, shg, max_tokens=None, x_dtype=torch.float32, path=0):
     T = x.shape[0]
     layer = moe.MoELayer(max_tokens or max(T, 1))
+    layer.set_path(path)
     xt = torch.from_numpy(x).to(dev).to(x_dtype)
     lt = torch.from_numpy(lg).to(dev)
     st = torch.from_numpy(shg).to(dev) if shg is not None else None
@@ -215,10 +216,15 @@ def _check_routing(layer, oracle, lg, E=256, k=8):
     np.testing.assert_array_equal(gi, oi)
     gw = layer.tap(moe.TAP_TOPK_W).cpu().double().numpy()
     assert np.abs(gw - ow).max() <= 2e-6
-    off, perm, pos = oracle.sort_entries(gi, E)
-    np.testing.assert_array_equal(layer.tap(moe.TAP_EOFF).cpu().numpy(), off)
-    np.testing.assert_array_equal(layer.tap(moe.TAP_PERM).cpu().numpy(), perm)
-    np.testing.assert_array_equal(layer.tap(moe.TAP_POS).cpu().numpy(), pos)
+    if layer.last_path == 0:        # sorted path: offsets and permutation bit-exact
+        off, perm, pos = oracle.sort_entries(gi, E)
+        np.testing.assert_array_equal(layer.tap(moe.TAP_EOFF).cpu().numpy(), off)
+        np.testing.assert_array_equal(layer.tap(moe.TAP_PERM).cpu().numpy(), perm)
+        np.testing.assert_array_equal(layer.tap(moe.TAP_POS).cpu().numpy(), pos)
+    else:                           # direct path: rows stay in entry order
+        ident = np.arange(gi.size, dtype=np.int32)
+        np.testing.assert_array_equal(layer.tap(moe.TAP_PERM).cpu().numpy(), ident)
+        np.testing.assert_array_equal(layer.tap(moe.TAP_POS).cpu().numpy(), ident)
     return gi
 
 
@@ -267,10 +273,12 @@ def _check_h_rows(oracle, w, x, gi, perm, hq, hs, rows, n_expert=256, k=8):
     return flips
 
 
-def _check_layer(name, dev, oracle, layer_w, x, lg, shg, sample=None, x_dtype=torch.float32):
+def _check_layer(name, dev, oracle, layer_w, x, lg, shg, sample=None, x_dtype=torch.float32,
+                 path=0):
     w, dw = layer_w
     T = x.shape[0]
-    layer, y32, y16 = _run_layer(dev, dw, x, lg, shg, x_dtype=x_dtype)
+    layer, y32, y16 = _run_layer(dev, dw, x, lg, shg, x_dtype=x_dtype, path=path)
+    name = f"{name}/{'direct' if layer.last_path == 1 else 'sorted'}"
     gi = _check_routing(layer, oracle, lg)
     oq, os_ = oracle.quant_e4m3(x)
     np.testing.assert_array_equal(layer.tap(moe.TAP_XQ).cpu().numpy(), oq)
@@ -316,16 +324,46 @@ def _check_layer(name, dev, oracle, layer_w, x, lg, shg, sample=None, x_dtype=to
     return layer
 
 
-def test_forward_decode1(dev, oracle, layer_w):
+PATHS = [pytest.param(1, id="sorted"), pytest.param(2, id="direct")]
+
+
+@pytest.mark.parametrize("path", PATHS)
+def test_forward_decode1(dev, oracle, layer_w, path):
     x, lg, _ = synth.config_inputs("decode1", 1)
-    _check_layer("decode1", dev, oracle, layer_w, x, lg, None)
+    _check_layer("decode1", dev, oracle, layer_w, x, lg, None, path=path)
 
 
-@pytest.mark.parametrize("T", [2, 7, 16, 33])
-def test_forward_small_batches(dev, oracle, layer_w, T):
+@pytest.mark.parametrize("path", PATHS)
+@pytest.mark.parametrize("T", [2, 7, 16])
+def test_forward_small_batches(dev, oracle, layer_w, T, path):
     rng = np.random.default_rng(300 + T)
     x, lg = synth.hidden(rng, T), synth.normal_logits(rng, T)
-    _check_layer(f"small{T}", dev, oracle, layer_w, x, lg, None)
+    _check_layer(f"small{T}", dev, oracle, layer_w, x, lg, None, path=path)
+
+
+def test_forward_small33(dev, oracle, layer_w):
+    rng = np.random.default_rng(333)
+    x, lg = synth.hidden(rng, 33), synth.normal_logits(rng, 33)
+    _check_layer("small33", dev, oracle, layer_w, x, lg, None)
+
+
+@pytest.mark.parametrize("T", [1, 5, 16])
+def test_direct_equals_sorted_inputs(dev, layer_w, T):
+    """Both paths see the same routing and quantised x; their outputs agree
+    to the stage-2 bar (they differ only in accumulation order)."""
+    _, dw = layer_w
+    rng = np.random.default_rng(900 + T)
+    x, lg = synth.hidden(rng, T), synth.normal_logits(rng, T)
+    outs, taps = [], []
+    for path in (1, 2):
+        layer, y32, _ = _run_layer(dev, dw, x, lg, None, path=path)
+        outs.append(y32)
+        taps.append([layer.tap(m).cpu().numpy() for m in (moe.TAP_TOPK_IDX, moe.TAP_TOPK_W,
+                                                          moe.TAP_XQ, moe.TAP_XS)])
+    for a, b in zip(*taps):
+        np.testing.assert_array_equal(a, b)
+    _, normwise = _row_err(outs[1], outs[0].astype(np.float64))
+    assert normwise <= TOL
 
 
 def test_forward_ragged64_zipf(dev, oracle, layer_w):
@@ -347,11 +385,12 @@ def test_forward_mixed_shared(dev, oracle, layer_w):
     _check_layer("mixed", dev, oracle, layer_w, x, lg, shg, sample=sample)
 
 
-def test_forward_shared_small(dev, oracle, layer_w):
+@pytest.mark.parametrize("path", PATHS)
+def test_forward_shared_small(dev, oracle, layer_w, path):
     rng = np.random.default_rng(55)
     x, lg = synth.hidden(rng, 5), synth.normal_logits(rng, 5)
     shg = rng.standard_normal(5).astype(np.float32)
-    _check_layer("shared5", dev, oracle, layer_w, x, lg, shg)
+    _check_layer("shared5", dev, oracle, layer_w, x, lg, shg, path=path)
 
 
 def test_forward_bf16_input(dev, oracle, layer_w):
@@ -360,6 +399,8 @@ def test_forward_bf16_input(dev, oracle, layer_w):
     x, lg = synth.hidden(rng, 9), synth.normal_logits(rng, 9)
     xb = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
     _check_layer("bf16_in", dev, oracle, layer_w, xb, lg, None, x_dtype=torch.bfloat16)
+    _check_layer("bf16_in", dev, oracle, layer_w, xb[:4], lg[:4], None, x_dtype=torch.bfloat16,
+                 path=2)
 
 
 def test_forward_deterministic_and_reusable(dev, layer_w):
