@@ -123,14 +123,22 @@ int q36moe_quant_e4m3(const void *x, int x_fmt, int T, int K,
                       uint8_t *xq, uint8_t *xs, void *stream);
 
 /* Execution path of q36moe_forward.  The sorted path (route + sort + grouped
- * expert GEMMs + combine) serves any T; the direct path (two kernels, no
- * sort, slots combined in registers) serves T <= 16.  mode 0 picks the
- * direct path for T <= 16, 1 forces sorted, 2 forces direct (EINVAL from
- * forward when T > 16).  last_path: 0 sorted, 1 direct.  With the direct
- * path the PERM/POS taps are the identity (rows in entry order) and the
- * EOFF/DNW taps are unavailable. */
+ * expert GEMMs + combine) serves any T; the direct path (no sort, slots
+ * combined in registers) serves T <= 16 as two kernels (gate/up, then down),
+ * or as one kernel whose down-role workgroups wait on per-token counters
+ * (mode 3; measured slower on MI355X: each device-scope poll is a memory
+ * round trip).  mode 0 picks the two-kernel direct path for T <= 16, 1
+ * forces sorted, 2 forces direct, 3 forces the one-kernel direct path
+ * (EINVAL from forward when T > 16 in modes 2/3).  last_path: 0 sorted, 1
+ * direct.  With the direct path the PERM/POS taps are the identity (rows in
+ * entry order) and the EOFF/DNW taps are unavailable. */
 int q36moe_ctx_set_path(q36moe_ctx *c, int mode);
 int q36moe_ctx_last_path(const q36moe_ctx *c);
+
+/* Synchronises the context stream and reports whether any bounded
+ * inter-workgroup wait of the one-kernel direct path gave up since the last
+ * check (Q36MOE_EHIP; the wait counters are reset).  0 otherwise. */
+int q36moe_ctx_check(q36moe_ctx *c);
 
 /* Copy one internal buffer of the last forward into dst (device pointer,
  * at most `bytes`); *written receives the byte count. */

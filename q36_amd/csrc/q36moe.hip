@@ -29,6 +29,22 @@
 #include "q36moe.h"
 
 typedef int v8i __attribute__((ext_vector_type(8)));
+
+#ifdef Q36MOE_TRACE
+__device__ unsigned long long g_q36_trace[64];
+__device__ unsigned long long g_q36_wg[2 * 4096];
+#define Q36_TRACE_WG(n)                                                                  \
+    do {                                                                                 \
+        if (threadIdx.x == 0) g_q36_wg[2 * (blockIdx.y * gridDim.x + blockIdx.x) + (n)] = wall_clock64(); \
+    } while (0)
+#define Q36_TRACE_AT(n)                                                                  \
+    do {                                                                                 \
+        if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) g_q36_trace[n] = wall_clock64(); \
+    } while (0)
+#else
+#define Q36_TRACE_AT(n) do {} while (0)
+#define Q36_TRACE_WG(n) do {} while (0)
+#endif
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 namespace {
@@ -120,116 +136,162 @@ __device__ __forceinline__ void static_for(F &&f) {
 // routing + activation quantisation
 // ---------------------------------------------------------------------------
 
-// One wavefront routes one token.  Lane l holds logits l, l+64, l+128,
-// l+192.  k rounds of wave argmax, ties to the lower expert index
-// (q36_ops.cuh:416-423).  Weight = exp(l-m)/sum_all, renormalised over the
-// k picks and scaled (q36_ops.cuh:424-430).  Lane 0 writes idx/wt.
-__device__ void route_token(const float *__restrict__ l, int E, int k, float scale,
-                            int renorm, int lane, int32_t *idx, float *wt, int *lds_ent) {
-    float v[4];
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int e = lane + 64 * j;
-        v[j] = e < E ? l[e] : -INFINITY;
-    }
-    float m = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-    float s = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 4; j++) s += (lane + 64 * j < E) ? expf(v[j] - m) : 0.0f;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
-    uint32_t taken = 0;
-    float wr[kMaxTopK];
-    int ir[kMaxTopK];
-    float wsum = 0.0f;
-    for (int r = 0; r < k; r++) {
-        float bv = -INFINITY;
-        int bi = -1;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int e = lane + 64 * j;
-            if (e < E && !((taken >> j) & 1u) && (bi < 0 || v[j] > bv)) {
-                bv = v[j];
-                bi = e;
-            }
-        }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const float ov = __shfl_xor(bv, o, 64);
-            const int oi = __shfl_xor(bi, o, 64);
-            if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) {
-                bv = ov;
-                bi = oi;
-            }
-        }
-        if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
-        const float w = expf(bv - m) / s;
-        wr[r] = w;
-        ir[r] = bi;
-        wsum += w;
-    }
-    if (lane == 0) {
-        for (int r = 0; r < k; r++) {
-            idx[r] = ir[r];
-            wt[r] = renorm ? wr[r] / wsum * scale : wr[r] * scale;
-            if (lds_ent) lds_ent[r] = ir[r];
-        }
-    }
+// Order-preserving key of a float logit (larger value -> larger key); NaN
+// maps to 0 so it is never picked (the reference's `v > best` never takes
+// a NaN either).
+__device__ __forceinline__ uint32_t logit_key(float f) {
+    const uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return 0u;
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// The pick of one slot s only, returned to every lane (same arithmetic and
-// tie order as route_token; renormalised weight, times scale).
-__device__ __forceinline__ void route_token_slot(const float *__restrict__ l, int E, int k, float scale,
-                                                 int s, int lane, int &e_out, float &w_out) {
-    float v[4];
+__device__ __forceinline__ int popc_ballot(bool p) { return __popcll(__ballot(p)); }
+
+// Top-k routing of one token by one wavefront, without serial cross-lane
+// argmax rounds:
+//   1. the k-th largest key is found by a radix search over the key bits
+//      whose counts are ballots, stopping as soon as exactly k keys clear the
+//      threshold; ties at the threshold take the lowest expert indices;
+//   2. the k picks are written to LDS in ascending index order (mbcnt
+//      prefix) and read back by every lane;
+//   3. lane r < k owns pick r: its slot is its rank under (value desc, index
+//      asc) -- the order of the reference's k rounds of warp argmax with ties
+//      to the lower index (q36_ops.cuh:409-427) -- and its weight is
+//      exp(l_r - max) / sum_q exp(l_q - max) * scale, the reference's
+//      exp(l-m)/sum_all renormalised over the picks (q36_ops.cuh:424-430), in
+//      which the full denominator cancels; the sum runs in index order.
+// `lds` is 2*kMaxTopK words private to the wave.
+struct Pick {
+    int idx;     // expert index of pick `lane` (lanes < k)
+    int slot;    // its rank in (value desc, index asc) order
+    float w;     // renormalised weight times scale
+};
+
+// exp(x) on the hardware exp2 (v_exp_f32), about 1 ulp; routing weights only.
+__device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
+
+__device__ __forceinline__ float key_val(uint32_t kk) {
+    return __uint_as_float((kk & 0x80000000u) ? (kk & 0x7fffffffu) : ~kk);
+}
+
+__device__ __forceinline__ Pick route_pick(const float *__restrict__ l, int E, int k, float scale,
+                                           uint32_t *lds) {
+    const int lane = __lane_id();
+    uint32_t key[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const int e = lane + 64 * j;
-        v[j] = e < E ? l[e] : -INFINITY;
+        const float v = l[e < E ? e : E - 1];
+        key[j] = e < E ? logit_key(v) : 0u;
     }
-    float m = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
+#ifdef Q36MOE_TRACE
+    if (key[0] == 12345u) key[0] = 0u;
+#endif
+    Q36_TRACE_AT(10);
+    // two key bits per step: the three candidate counts are independent
+    uint32_t tau = 0;
+    int cnt_tau = E;
+    for (int bit = 30; bit >= 0 && cnt_tau != k; bit -= 2) {
+        const uint32_t c1 = tau | (1u << bit), c2 = tau | (2u << bit), c3 = tau | (3u << bit);
+        const int n1 = popc_ballot(key[0] >= c1) + popc_ballot(key[1] >= c1) +
+                       popc_ballot(key[2] >= c1) + popc_ballot(key[3] >= c1);
+        const int n2 = popc_ballot(key[0] >= c2) + popc_ballot(key[1] >= c2) +
+                       popc_ballot(key[2] >= c2) + popc_ballot(key[3] >= c2);
+        const int n3 = popc_ballot(key[0] >= c3) + popc_ballot(key[1] >= c3) +
+                       popc_ballot(key[2] >= c3) + popc_ballot(key[3] >= c3);
+        if (n3 >= k) { tau = c3; cnt_tau = n3; }
+        else if (n2 >= k) { tau = c2; cnt_tau = n2; }
+        else if (n1 >= k) { tau = c1; cnt_tau = n1; }
+    }
+    Q36_TRACE_AT(11);
+    int need = k;
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-    float sum = 0.0f;
+    for (int j = 0; j < 4; j++) need -= popc_ballot(key[j] > tau);
+    int base = 0;
 #pragma unroll
-    for (int j = 0; j < 4; j++) sum += (lane + 64 * j < E) ? expf(v[j] - m) : 0.0f;
+    for (int j = 0; j < 4; j++) {
+        uint64_t eq = __ballot(key[j] == tau);
+        uint64_t take = 0;
+        while (need > 0 && eq) {
+            take |= eq & (~eq + 1);
+            eq &= eq - 1;
+            need--;
+        }
+        const uint64_t sel = __ballot(key[j] > tau) | take;
+        const int pos = base + (int)__builtin_amdgcn_mbcnt_hi(
+                                   (uint32_t)(sel >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)sel, 0u));
+        if ((sel >> lane) & 1ull) {
+            lds[pos] = key[j];
+            lds[kMaxTopK + pos] = (uint32_t)(lane + 64 * j);
+        }
+        base += __popcll(sel);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    Q36_TRACE_AT(12);
+    uint32_t gk[kMaxTopK];
+    int gi[kMaxTopK];
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
-    uint32_t taken = 0;
-    float wsum = 0.0f, ws = 0.0f;
-    int es = 0;
-    for (int r = 0; r < k; r++) {
-        float bv = -INFINITY;
-        int bi = -1;
+    for (int q = 0; q < kMaxTopK; q++) {
+        gk[q] = q < k ? lds[q] : 0u;
+        gi[q] = q < k ? (int)lds[kMaxTopK + q] : 0x7fffffff;
+    }
+    const int me = lane < k ? lane : 0;
+    const uint32_t mk = lds[me];
+    const int mi = (int)lds[kMaxTopK + me];
+    uint32_t kmax = gk[0];
+#pragma unroll
+    for (int q = 1; q < kMaxTopK; q++) kmax = gk[q] > kmax ? gk[q] : kmax;
+    const float vmax = key_val(kmax);
+    float wsum = 0.0f;
+    int rank = 0;
+#pragma unroll
+    for (int q = 0; q < kMaxTopK; q++) {
+        if (q < k) {
+            wsum += fast_exp(key_val(gk[q]) - vmax);
+            rank += (gk[q] > mk || (gk[q] == mk && gi[q] < mi)) ? 1 : 0;
+        }
+    }
+    Pick P;
+    P.idx = mi;
+    P.slot = rank;
+    P.w = fast_exp(key_val(mk) - vmax) * __builtin_amdgcn_rcpf(wsum) * scale;
+#ifdef Q36MOE_TRACE
+    if (P.w == 12345.f) P.slot = 0;
+#endif
+    Q36_TRACE_AT(13);
+    return P;
+}
+
+// One wavefront routes one token (k_router_topk, q36_ops.cuh:397-431) and
+// writes idx/wt in slot order.  renorm = 0 gives the plain softmax
+// probabilities exp(l - max) / sum_all times scale instead.
+__device__ void route_token(const float *__restrict__ l, int E, int k, float scale, int renorm,
+                            int32_t *idx, float *wt, int *lds_ent, uint32_t *lds) {
+    const Pick P = route_pick(l, E, k, scale, lds);
+    const int lane = __lane_id();
+    float w = P.w;
+    if (!renorm) {
+        float vmax = -INFINITY;
+#pragma unroll
+        for (int q = 0; q < kMaxTopK; q++)
+            if (q < k) vmax = fmaxf(vmax, key_val(lds[q]));
+        float denom = 0.0f;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const int e = lane + 64 * j;
-            if (e < E && !((taken >> j) & 1u) && (bi < 0 || v[j] > bv)) {
-                bv = v[j];
-                bi = e;
-            }
+            denom += e < E ? expf(l[e] - vmax) : 0.0f;
         }
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const float ov = __shfl_xor(bv, o, 64);
-            const int oi = __shfl_xor(bi, o, 64);
-            if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) {
-                bv = ov;
-                bi = oi;
-            }
-        }
-        if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
-        const float w = expf(bv - m) / sum;
-        wsum += w;
-        if (r == s) {
-            ws = w;
-            es = bi;
-        }
+        for (int o = 32; o > 0; o >>= 1) denom += __shfl_xor(denom, o, 64);
+        w = expf(key_val(lds[lane < k ? lane : 0]) - vmax) / denom * scale;
     }
-    e_out = es;
-    w_out = ws / wsum * scale;
+    if (lane < k) {
+        idx[P.slot] = P.idx;
+        wt[P.slot] = w;
+        if (lds_ent) lds_ent[P.slot] = P.idx;
+    }
 }
 
 // Quantise one 32-element block (per-32 E8M0 + e4m3), q36_engine.cu:2411-2428.
@@ -282,14 +344,15 @@ struct RouteArgs {
 
 __global__ __launch_bounds__(kRouteThreads) void k_route(RouteArgs A) {
     __shared__ int ent[kRouteTPB * kMaxTopK];
+    __shared__ uint32_t rlds[kRouteThreads / 64][2 * kMaxTopK];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int t0 = blockIdx.x * kRouteTPB;
     const int nb32 = A.D / 32;
     for (int tl = wave; tl < kRouteTPB; tl += kRouteThreads / 64) {
         const int t = t0 + tl;
         if (t >= A.T) break;
-        route_token(A.logits + (size_t)t * A.ld, A.E, A.k, A.scale, 1, lane,
-                    A.idx + (size_t)t * A.k, A.wt + (size_t)t * A.k, ent + tl * A.k);
+        route_token(A.logits + (size_t)t * A.ld, A.E, A.k, A.scale, 1,
+                    A.idx + (size_t)t * A.k, A.wt + (size_t)t * A.k, ent + tl * A.k, rlds[wave]);
         for (int b = lane; b < nb32; b += 64)
             quant_block32(A.x, A.x_fmt, (size_t)t * A.D + (size_t)b * 32,
                           A.xq + (size_t)t * A.D + (size_t)b * 32, A.xs + (size_t)t * nb32 + b);
@@ -314,10 +377,11 @@ __global__ __launch_bounds__(kRouteThreads) void k_route(RouteArgs A) {
 
 __global__ __launch_bounds__(256) void k_topk(const float *logits, int T, int E, int ld, int k,
                                              float scale, int renorm, int32_t *idx, float *wt) {
+    __shared__ uint32_t rlds[4][2 * kMaxTopK];
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= T) return;
-    route_token(logits + (size_t)t * ld, E, k, scale, renorm, threadIdx.x & 63,
-                idx + (size_t)t * k, wt + (size_t)t * k, nullptr);
+    route_token(logits + (size_t)t * ld, E, k, scale, renorm, idx + (size_t)t * k, wt + (size_t)t * k,
+                nullptr, rlds[threadIdx.x >> 6]);
 }
 
 __global__ __launch_bounds__(256) void k_quant(const void *x, int x_fmt, int T, int K,
@@ -593,6 +657,9 @@ struct DirectArgs {
     float *hf;                                  // [entries][FF] fp32 SwiGLU rows
     uint8_t *hq; uint8_t *hs;                   // quantised h (tap)
     void *out; int out_fmt;
+    // fused kernel only: per-token arrival / departure counters (zero
+    // between calls), error flag, and the number of gate/up workgroups
+    uint32_t *arrive; uint32_t *depart; uint32_t *err; int n_gateup_wg;
 };
 
 constexpr int kDD = 2048;   // d_model of the instantiated kernels
@@ -637,17 +704,28 @@ __device__ __forceinline__ void load8(const void *x, int fmt, size_t off, float 
 // x 16 rows of gate and up.  Wave w reduces K range [512w, 512w+512): it
 // quantises exactly that range of x into LDS, so no cross-wave exchange is
 // needed before the MFMAs.  Partial sums meet in LDS in wave order.
-__global__ __launch_bounds__(256) void k_direct_gateup(DirectArgs A) {
-    __shared__ __align__(16) uint8_t sx[kDD + 32];   // + 32 zero bytes
-    __shared__ uint8_t sxs[kDD / 32];
-    __shared__ float red[4][2][16];
-    const int i = blockIdx.x, ft = blockIdx.y;
+struct DirectGateupLds {
+    __align__(16) uint8_t sx[kDD + 32];   // + 32 zero bytes
+    uint8_t sxs[kDD / 32];
+    float red[4][2][16];
+    uint32_t rlds[4][2 * kMaxTopK];
+};
+
+template <bool FUSED>
+__device__ __forceinline__ void direct_gateup_body(const DirectArgs &A, int i, int ft,
+                                                   DirectGateupLds &L_) {
+    uint8_t *sx = L_.sx;
+    uint8_t *sxs = L_.sxs;
+    auto &red = L_.red;
+    auto &rlds = L_.rlds;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int nr = A.T * A.k;
     const bool routed = i < nr;
     const int t = routed ? i / A.k : i - nr;
     const int s = routed ? i % A.k : 0;
 
+    Q36_TRACE_AT(0);
+    Q36_TRACE_WG(0);
     // issue this wave's x loads first (512 values, 8 per lane)
     float xv[8];
     load8(A.x, A.x_fmt, (size_t)t * kDD + wave * 512 + lane * 8, xv);
@@ -656,7 +734,12 @@ __global__ __launch_bounds__(256) void k_direct_gateup(DirectArgs A) {
     float wgt = 0.0f;
     if (routed) {
         // every wave routes the token (no barrier needed to share the result)
-        route_token_slot(A.logits + (size_t)t * A.ld, A.E, A.k, A.scale, s, lane, e, wgt);
+        const Pick P = route_pick(A.logits + (size_t)t * A.ld, A.E, A.k, A.scale, rlds[wave]);
+        const uint64_t m = __ballot(lane < A.k && P.slot == s);
+        const int L = __builtin_ctzll(m);
+        e = __builtin_amdgcn_readlane(P.idx, L);
+        wgt = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(P.w), L));
+        Q36_TRACE_AT(1);
     } else {
         wgt = 1.0f / (1.0f + expf(-A.shg[t]));
     }
@@ -675,8 +758,10 @@ __global__ __launch_bounds__(256) void k_direct_gateup(DirectArgs A) {
     const int sau = *reinterpret_cast<const int *>(Wu + so);
 
     quant8_lane(xv, lane, sx + wave * 512 + lane * 8, sxs + wave * 16 + (lane >> 2));
+    Q36_TRACE_AT(2);
     if (threadIdx.x < 8) reinterpret_cast<uint32_t *>(sx + kDD)[threadIdx.x] = 0u;
     __syncthreads();
+    Q36_TRACE_AT(3);
 
     // B fragment: column 0 is the token; lanes of other columns read zeros
     const int q = lane >> 4;
@@ -697,6 +782,7 @@ __global__ __launch_bounds__(256) void k_direct_gateup(DirectArgs A) {
         cg = mfma_f4xf8<j>(a0, b, cg, sag, sb);
         cu = mfma_f4xf8<j>(a1, b, cu, sau, sb);
     });
+    Q36_TRACE_AT(4);
     if (col0) {
 #pragma unroll
         for (int r = 0; r < 4; r++) {
@@ -708,8 +794,24 @@ __global__ __launch_bounds__(256) void k_direct_gateup(DirectArgs A) {
     if (wave == 0 && lane < 16) {
         const float g = red[0][0][lane] + red[1][0][lane] + red[2][0][lane] + red[3][0][lane];
         const float u = red[0][1][lane] + red[1][1][lane] + red[2][1][lane] + red[3][1][lane];
-        A.hf[(size_t)i * kDF + ft * 16 + lane] = silu(g) * u;
+        if constexpr (FUSED) {
+            // publish without an L2-wide release fence: the row goes out as a
+            // device-scope store (written through to the coherence point), the
+            // wave waits for its completion, then counts this workgroup in
+            __hip_atomic_store(&A.hf[(size_t)i * kDF + ft * 16 + lane], silu(g) * u,
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __builtin_amdgcn_s_waitcnt(0);
+            // system scope: the add is performed at the coherence point, where
+            // the pollers' device-scope loads look (an agent-scope add sits in
+            // this XCD's L2 and reaches them microseconds later)
+            if (lane == 0)
+                __hip_atomic_fetch_add(&A.arrive[t], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        } else {
+            A.hf[(size_t)i * kDF + ft * 16 + lane] = silu(g) * u;
+        }
     }
+    Q36_TRACE_AT(5);
+    Q36_TRACE_WG(1);
     if (ft == 0) {
         if (threadIdx.x == 0 && routed) {
             A.idx[i] = e;
@@ -724,6 +826,11 @@ __global__ __launch_bounds__(256) void k_direct_gateup(DirectArgs A) {
             if (threadIdx.x < kDD / 32) A.xs[(size_t)t * (kDD / 32) + threadIdx.x] = sxs[threadIdx.x];
         }
     }
+}
+
+__global__ __launch_bounds__(256) void k_direct_gateup(DirectArgs A) {
+    __shared__ DirectGateupLds L_;
+    direct_gateup_body<false>(A, blockIdx.x, blockIdx.y, L_);
 }
 
 // Token t x 16 output rows; wave s handles slot s (wave k: shared expert):
@@ -786,6 +893,143 @@ __global__ __launch_bounds__(576) void k_direct_down(DirectArgs A) {
         const size_t o = (size_t)t * kDD + rt * 16 + lane;
         if (A.out_fmt == Q36MOE_FMT_F32) static_cast<float *>(A.out)[o] = acc;
         else static_cast<uint16_t *>(A.out)[o] = (uint16_t)f32_to_bf16(acc);
+    }
+}
+
+// Single-kernel decode: workgroups [0, n_gateup_wg) are the gate/up role
+// (entry i x 16 rows, as k_direct_gateup); the rest are the down role (token
+// t x 16 output rows).  A down-role workgroup routes its token itself,
+// prefetches its down tiles, then waits until all gate/up workgroups of
+// token t have published their SwiGLU rows (per-token arrival counter,
+// release/acquire at device scope).  Workgroups are dispatched in index
+// order, so every gate/up workgroup is resident or finished before any
+// down-role workgroup waits, and gate/up workgroups never wait; the wait is
+// bounded as a backstop (error flag, then the workgroup goes on).  The last
+// down-role workgroup of a token resets both counters for the next call.
+constexpr uint32_t kSpinLimit = 1u << 22;
+
+__global__ __launch_bounds__(256) void k_decode_fused(DirectArgs A) {
+    __shared__ DirectGateupLds Lg;
+    __shared__ __align__(16) uint8_t sh[4][3][kDF + 32];
+    __shared__ uint8_t shs[4][3][kDF / 32];
+    __shared__ float red[3 * 4][16];
+    const int bid = blockIdx.x;
+    if (bid < A.n_gateup_wg) {
+        direct_gateup_body<true>(A, bid / (kDF / 16), bid % (kDF / 16), Lg);
+        return;
+    }
+    const int d = bid - A.n_gateup_wg;
+    const int t = d / (kDD / 16), rt = d % (kDD / 16);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const bool has_sh = A.sh_down != nullptr;
+    const int nslot = A.k + (has_sh ? 1 : 0);
+    // slots of this wave: wave, wave + 4, wave + 8
+    const Pick P = route_pick(A.logits + (size_t)t * A.ld, A.E, A.k, A.scale, Lg.rlds[wave]);
+    uint4 a[3][4];
+    int sa[3];
+    float wgt[3];
+    const size_t nib = (size_t)kDD * kDF / 2;
+#pragma unroll
+    for (int m = 0; m < 3; m++) {
+        const int sl = wave + 4 * m;
+        wgt[m] = 0.0f;
+        if (sl < nslot) {
+            const uint8_t *W;
+            if (sl < A.k) {
+                const uint64_t b = __ballot(lane < A.k && P.slot == sl);
+                const int L = __builtin_ctzll(b);
+                const int e = __builtin_amdgcn_readlane(P.idx, L);
+                wgt[m] = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(P.w), L));
+                W = A.down + (size_t)e * A.wstride;
+            } else {
+                wgt[m] = 1.0f / (1.0f + expf(-A.shg[t]));
+                W = A.sh_down;
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                a[m][j] = *reinterpret_cast<const uint4 *>(W + ((size_t)rt * 4 + j) * 1024 + (size_t)lane * 16);
+            sa[m] = *reinterpret_cast<const int *>(W + nib + ((size_t)rt * 64 + lane) * 4);
+        }
+    }
+    // wait for the SwiGLU rows of token t: wave 0 polls, the others hold at
+    // the barrier (few pollers keep the counter line uncontended)
+    Q36_TRACE_WG(0);
+    if (wave == 0) {
+        const uint32_t target = (uint32_t)nslot * (kDF / 16);
+        uint32_t spins = 0;
+        while (__hip_atomic_load(&A.arrive[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+            if (++spins > kSpinLimit) {
+                if (lane == 0) atomicOr(A.err, 1u);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(8);
+        }
+    }
+    __syncthreads();
+    Q36_TRACE_WG(1);
+#pragma unroll
+    for (int m = 0; m < 3; m++) {
+        const int sl = wave + 4 * m;
+        if (sl < nslot) {
+            const int i = sl < A.k ? t * A.k + sl : A.T * A.k + t;
+            float hv[8];
+            // device-scope loads: read at the coherence point, not a stale L2 line
+#pragma unroll
+            for (int v = 0; v < 8; v++)
+                hv[v] = __hip_atomic_load(&A.hf[(size_t)i * kDF + lane * 8 + v], __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+            quant8_lane(hv, lane, &sh[wave][m][lane * 8], &shs[wave][m][lane >> 2]);
+            if (lane < 8) reinterpret_cast<uint32_t *>(&sh[wave][m][kDF])[lane] = 0u;
+            if (rt == 0) {   // quantised h (tap)
+                *reinterpret_cast<uint2 *>(A.hq + (size_t)i * kDF + lane * 8) =
+                    *reinterpret_cast<const uint2 *>(&sh[wave][m][lane * 8]);
+                if ((lane & 3) == 0) A.hs[(size_t)i * (kDF / 32) + (lane >> 2)] = shs[wave][m][lane >> 2];
+            }
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int q = lane >> 4;
+    const bool col0 = (lane & 15) == 0;
+#pragma unroll
+    for (int m = 0; m < 3; m++) {
+        const int sl = wave + 4 * m;
+        if (sl < nslot) {
+            v4f c = {0.f, 0.f, 0.f, 0.f};
+            static_for<0, 4>([&](auto J) {
+                constexpr int j = decltype(J)::value;
+                const uint8_t *b0p = col0 ? &sh[wave][m][j * 128 + 16 * q] : &sh[wave][m][kDF];
+                const uint8_t *b1p = col0 ? &sh[wave][m][j * 128 + 64 + 16 * q] : &sh[wave][m][kDF + 16];
+                const uint4 b0 = *reinterpret_cast<const uint4 *>(b0p);
+                const uint4 b1 = *reinterpret_cast<const uint4 *>(b1p);
+                const v8i b = v8i{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w,
+                                  (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+                const int sb = shs[wave][m][j * 4 + q];
+                const v8i av = v8i{(int)a[m][j].x, (int)a[m][j].y, (int)a[m][j].z, (int)a[m][j].w, 0, 0, 0, 0};
+                c = mfma_f4xf8<j>(av, b, c, sa[m], sb);
+            });
+            if (col0) {
+#pragma unroll
+                for (int r = 0; r < 4; r++) red[sl][4 * q + r] = c[r] * wgt[m];
+            }
+        }
+    }
+    __syncthreads();
+    if (wave == 0 && lane < 16) {
+        float acc = 0.0f;
+        for (int sl = 0; sl < nslot; sl++) acc += red[sl][lane];
+        const size_t o = (size_t)t * kDD + rt * 16 + lane;
+        if (A.out_fmt == Q36MOE_FMT_F32) static_cast<float *>(A.out)[o] = acc;
+        else static_cast<uint16_t *>(A.out)[o] = (uint16_t)f32_to_bf16(acc);
+    }
+    if (threadIdx.x == 0) {
+        const uint32_t old =
+            __hip_atomic_fetch_add(&A.depart[t], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        if (old == (uint32_t)(kDD / 16) - 1) {   // last reader of token t
+            __hip_atomic_store(&A.arrive[t], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&A.depart[t], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
 }
 
@@ -903,6 +1147,7 @@ struct q36moe_ctx {
     uint8_t *hq, *hs;
     float *dnw;
     float *hf;                      // direct path: fp32 SwiGLU rows
+    uint32_t *sync;                 // fused decode: arrive[16], depart[16], err
     int path_mode;                  // 0 auto, 1 sorted, 2 direct
     int last_T, last_sh, last_path;
     int timing;
@@ -1075,6 +1320,7 @@ int q36moe_ctx_create(int max_tokens, int n_expert, int d_model, int d_ff, int t
     const size_t o_dnw = take(rows * d_model * 4);
     const size_t direct_rows = (size_t)(max_tokens < kDirectMaxT ? max_tokens : kDirectMaxT) * (top_k + 1);
     const size_t o_hf = take(direct_rows * d_ff * 4);
+    const size_t o_sync = take((2 * kDirectMaxT + 1) * 4);
     if (hipMalloc(&c->base, off) != hipSuccess) {
         delete c;
         return Q36MOE_ENOMEM;
@@ -1096,6 +1342,12 @@ int q36moe_ctx_create(int max_tokens, int n_expert, int d_model, int d_ff, int t
     c->hq = b + o_hq; c->hs = b + o_hs;
     c->dnw = reinterpret_cast<float *>(b + o_dnw);
     c->hf = reinterpret_cast<float *>(b + o_hf);
+    c->sync = reinterpret_cast<uint32_t *>(b + o_sync);
+    if (hipMemset(c->sync, 0, (2 * kDirectMaxT + 1) * 4) != hipSuccess) {
+        (void)hipFree(c->base);
+        delete c;
+        return Q36MOE_EHIP;
+    }
     for (int i = 0; i <= ST_COUNT; i++) {
         if (hipEventCreate(&c->ev[i]) != hipSuccess) {
             for (int j = 0; j < i; j++) (void)hipEventDestroy(c->ev[j]);
@@ -1147,20 +1399,27 @@ int q36moe_forward(q36moe_ctx *c, const q36moe_weights *w, const void *x, int x_
         if (c->timing) (void)hipEventRecord(c->ev[st], s);
     };
 
-    const bool direct = c->path_mode == 2 ? (T <= kDirectMaxT)
+    const bool direct = (c->path_mode == 2 || c->path_mode == 3) ? (T <= kDirectMaxT)
                         : c->path_mode == 1 ? false : (T <= kDirectMaxT);
-    if (c->path_mode == 2 && !direct) return Q36MOE_EINVAL;
+    if ((c->path_mode == 2 || c->path_mode == 3) && !direct) return Q36MOE_EINVAL;
     if (direct) {
+        const int ngu = (n + (has_sh ? T : 0)) * (FF / 16);
         DirectArgs da{logits, ld_logits, T, E, K, scale, x, x_fmt, shg,
-                      w->gate, w->up, w->down, w->sh_gate, w->sh_up, w->sh_down, w->gu_bytes,
-                      c->topk_idx, c->topk_w, c->pos, c->perm, c->xq, c->xs, c->hf, c->hq, c->hs,
-                      out, out_fmt};
+                      w->gate, w->up, w->down, w->sh_gate, w->sh_up, has_sh ? w->sh_down : nullptr,
+                      w->gu_bytes, c->topk_idx, c->topk_w, c->pos, c->perm, c->xq, c->xs, c->hf,
+                      c->hq, c->hs, out, out_fmt, c->sync, c->sync + kDirectMaxT,
+                      c->sync + 2 * kDirectMaxT, ngu};
         mark(ST_ROUTE);
         mark(ST_SCAN);
         mark(ST_GATEUP);
-        hipLaunchKernelGGL(k_direct_gateup, dim3(n + (has_sh ? T : 0), FF / 16), dim3(256), 0, s, da);
-        mark(ST_DOWN);
-        hipLaunchKernelGGL(k_direct_down, dim3(D / 16, T), dim3(64 * (K + has_sh)), 0, s, da);
+        if (c->path_mode != 3) {
+            hipLaunchKernelGGL(k_direct_gateup, dim3(n + (has_sh ? T : 0), FF / 16), dim3(256), 0, s, da);
+            mark(ST_DOWN);
+            hipLaunchKernelGGL(k_direct_down, dim3(D / 16, T), dim3(64 * (K + has_sh)), 0, s, da);
+        } else {
+            hipLaunchKernelGGL(k_decode_fused, dim3(ngu + T * (D / 16)), dim3(256), 0, s, da);
+            mark(ST_DOWN);
+        }
         mark(ST_COMBINE);
         mark(ST_COUNT);
     } else {
@@ -1266,12 +1525,27 @@ int q36moe_ctx_copy_tap(q36moe_ctx *c, int tap, void *dst, size_t bytes, size_t 
 }
 
 int q36moe_ctx_set_path(q36moe_ctx *c, int mode) {
-    if (!c || mode < 0 || mode > 2) return Q36MOE_EINVAL;
+    if (!c || mode < 0 || mode > 3) return Q36MOE_EINVAL;
     c->path_mode = mode;
     return Q36MOE_OK;
 }
 
 int q36moe_ctx_last_path(const q36moe_ctx *c) { return c ? c->last_path : Q36MOE_EINVAL; }
+
+int q36moe_ctx_check(q36moe_ctx *c) {
+    if (!c) return Q36MOE_EINVAL;
+    uint32_t err = 0;
+    if (hipMemcpyAsync(&err, c->sync + 2 * kDirectMaxT, 4, hipMemcpyDeviceToHost, c->stream) != hipSuccess ||
+        hipStreamSynchronize(c->stream) != hipSuccess)
+        return Q36MOE_EHIP;
+    if (err) {
+        // a bounded wait gave up: clear the counters so later calls start clean
+        (void)hipMemsetAsync(c->sync, 0, (2 * kDirectMaxT + 1) * 4, c->stream);
+        (void)hipStreamSynchronize(c->stream);
+        return Q36MOE_EHIP;
+    }
+    return Q36MOE_OK;
+}
 
 int q36moe_ctx_set_timing(q36moe_ctx *c, int on) {
     if (!c) return Q36MOE_EINVAL;

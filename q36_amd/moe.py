@@ -61,6 +61,7 @@ def lib():
     L.q36moe_ctx_copy_tap.argtypes = [vp, i, vp, sz, ctypes.POINTER(sz)]
     L.q36moe_ctx_set_path.argtypes = [vp, i]
     L.q36moe_ctx_last_path.argtypes = [vp]
+    L.q36moe_ctx_check.argtypes = [vp]
     L.q36moe_ctx_set_timing.argtypes = [vp, i]
     L.q36moe_ctx_stage_times.argtypes = [vp, ctypes.POINTER(ctypes.c_double),
                                          ctypes.POINTER(ctypes.c_int), i, i]
@@ -258,16 +259,22 @@ class MoELayer:
               "q36moe_ctx_copy_tap")
         return dst
 
-    PATH_AUTO, PATH_SORTED, PATH_DIRECT = 0, 1, 2
+    PATH_AUTO, PATH_SORTED, PATH_DIRECT, PATH_DIRECT_FUSED = 0, 1, 2, 3
 
     def set_path(self, mode):
-        """0 auto (direct for T <= 16), 1 sorted, 2 direct."""
+        """0 auto (direct for T <= 16), 1 sorted, 2 direct (two kernels),
+        3 direct (one kernel)."""
         check(lib().q36moe_ctx_set_path(self._h, mode), "q36moe_ctx_set_path")
 
     @property
     def last_path(self):
         """0 sorted, 1 direct."""
         return lib().q36moe_ctx_last_path(self._h)
+
+    def check(self):
+        """Synchronise; raise if a bounded wait of the one-kernel direct
+        path gave up since the last check."""
+        check(lib().q36moe_ctx_check(self._h), "q36moe_ctx_check")
 
     def set_timing(self, on):
         check(lib().q36moe_ctx_set_timing(self._h, 1 if on else 0), "q36moe_ctx_set_timing")

@@ -206,6 +206,7 @@ def _run_layer(dev, dw, x, lg, shg, max_tokens=None, x_dtype=torch.float32, path
     st = torch.from_numpy(shg).to(dev) if shg is not None else None
     y32 = layer.forward(dw, xt, lt, st, out_dtype=torch.float32)
     y16 = layer.forward(dw, xt, lt, st, out_dtype=torch.bfloat16)
+    layer.check()
     torch.cuda.synchronize()
     return layer, y32.cpu().numpy(), y16.float().cpu().numpy()
 
@@ -324,7 +325,8 @@ def _check_layer(name, dev, oracle, layer_w, x, lg, shg, sample=None, x_dtype=to
     return layer
 
 
-PATHS = [pytest.param(1, id="sorted"), pytest.param(2, id="direct")]
+PATHS = [pytest.param(1, id="sorted"), pytest.param(2, id="direct"),
+         pytest.param(3, id="direct_fused")]
 
 
 @pytest.mark.parametrize("path", PATHS)
@@ -339,6 +341,29 @@ def test_forward_small_batches(dev, oracle, layer_w, T, path):
     rng = np.random.default_rng(300 + T)
     x, lg = synth.hidden(rng, T), synth.normal_logits(rng, T)
     _check_layer(f"small{T}", dev, oracle, layer_w, x, lg, None, path=path)
+
+
+def test_fused_decode_repeated_calls(dev, layer_w):
+    """The one-kernel direct path over 40 back-to-back calls of varying T
+    (its wait counters must reset themselves) equals the two-kernel direct
+    path bit for bit."""
+    _, dw = layer_w
+    rng = np.random.default_rng(4242)
+    fused, two = moe.MoELayer(16), moe.MoELayer(16)
+    fused.set_path(3)
+    two.set_path(2)
+    xs, ls, ys = [], [], []
+    for c in range(40):
+        T = int(rng.integers(1, 17))
+        x = torch.from_numpy(synth.hidden(rng, T)).to(dev)
+        lg = torch.from_numpy(synth.normal_logits(rng, T)).to(dev)
+        xs.append(x)
+        ls.append(lg)
+        ys.append(fused.forward(dw, x, lg, out_dtype=torch.float32))
+    fused.check()
+    for x, lg, y in zip(xs, ls, ys):
+        assert torch.equal(y, two.forward(dw, x, lg, out_dtype=torch.float32))
+    two.check()
 
 
 def test_forward_small33(dev, oracle, layer_w):
