@@ -35,7 +35,8 @@ __device__ unsigned long long g_q36_trace[64];
 __device__ unsigned long long g_q36_wg[2 * 4096];
 #define Q36_TRACE_WG(n)                                                                  \
     do {                                                                                 \
-        if (threadIdx.x == 0) g_q36_wg[2 * (blockIdx.y * gridDim.x + blockIdx.x) + (n)] = wall_clock64(); \
+        const unsigned wg_ = blockIdx.y * gridDim.x + blockIdx.x;                        \
+        if (threadIdx.x == 0 && wg_ < 4096u) g_q36_wg[2 * wg_ + (n)] = wall_clock64();   \
     } while (0)
 #define Q36_TRACE_AT(n)                                                                  \
     do {                                                                                 \
@@ -51,10 +52,8 @@ namespace {
 
 constexpr int kMaxExperts = 256;
 constexpr int kMaxTopK = 8;
-constexpr int kRouteTPB = 64;      // tokens per k_route workgroup
+constexpr int kRouteTPB = 16;      // tokens per k_route workgroup (one wavefront each)
 constexpr int kRouteThreads = 1024;
-constexpr int kScanThreads = 1024;
-constexpr int kLdsRow = 144;       // LDS row stride of one 128-byte K-step slice
 constexpr int kDirectMaxT = 16;    // largest batch routed to the direct (unsorted) path
 
 // ---------------------------------------------------------------------------
@@ -118,10 +117,19 @@ __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 // scale comes from an LDS byte load.  A VALU-shifted scale register issued
 // two wait states before v_mfma_scale was read stale on gfx950 (inf/NaN
 // from garbage E8M0 bytes).
-template <int SEL>
+template <int SEL, int SELB = 0>
 __device__ __forceinline__ v4f mfma_f4xf8(const v8i &a, const v8i &b, const v4f &c,
                                           int sa, int sb) {
-    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 4, 0, SEL, sa, 0, sb);
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 4, 0, SEL, sa, SELB, sb);
+}
+
+// Workgroup barrier ordering LDS only.  __syncthreads() also waits for
+// every outstanding global load (s_waitcnt vmcnt(0)), which would drain the
+// prefetch rings at each K-step.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 template <int I, int N, typename F>
@@ -337,42 +345,47 @@ __device__ __forceinline__ void quant_block32(const void *__restrict__ x, int x_
 
 struct RouteArgs {
     const float *logits; int ld; int T; int E; int k; float scale;
-    const void *x; int x_fmt; int D;
-    int32_t *idx; float *wt; uint8_t *xq; uint8_t *xs;
+    const void *x; int x_fmt; int D; int nb;
+    int32_t *idx; float *wt; uint8_t *xq; uint8_t *xs; uint8_t *xs2;
     int32_t *blk_cnt; int32_t *rank;
 };
 
+// One wavefront per token, kRouteTPB tokens per workgroup: top-k routing,
+// FP8 quantisation of x, then the block's per-expert counts (expert-major,
+// blk_cnt[e][block]) and each entry's rank among the block's earlier entries
+// of the same expert (the stable order of the sort).
 __global__ __launch_bounds__(kRouteThreads) void k_route(RouteArgs A) {
     __shared__ int ent[kRouteTPB * kMaxTopK];
+    __shared__ int hist[kMaxExperts];
     __shared__ uint32_t rlds[kRouteThreads / 64][2 * kMaxTopK];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int t0 = blockIdx.x * kRouteTPB;
     const int nb32 = A.D / 32;
-    for (int tl = wave; tl < kRouteTPB; tl += kRouteThreads / 64) {
-        const int t = t0 + tl;
-        if (t >= A.T) break;
+    for (int e = threadIdx.x; e < A.E; e += kRouteThreads) hist[e] = 0;
+    const int t = t0 + wave;
+    if (wave < kRouteTPB && t < A.T) {
         route_token(A.logits + (size_t)t * A.ld, A.E, A.k, A.scale, 1,
-                    A.idx + (size_t)t * A.k, A.wt + (size_t)t * A.k, ent + tl * A.k, rlds[wave]);
-        for (int b = lane; b < nb32; b += 64)
+                    A.idx + (size_t)t * A.k, A.wt + (size_t)t * A.k, ent + wave * A.k, rlds[wave]);
+        for (int b = lane; b < nb32; b += 64) {
+            uint8_t *sp = A.xs + (size_t)t * nb32 + b;
             quant_block32(A.x, A.x_fmt, (size_t)t * A.D + (size_t)b * 32,
-                          A.xq + (size_t)t * A.D + (size_t)b * 32, A.xs + (size_t)t * nb32 + b);
+                          A.xq + (size_t)t * A.D + (size_t)b * 32, sp);
+            // lane-group-major copy for the grouped GEMM: [t][b % 4][b / 4]
+            A.xs2[(size_t)t * nb32 + (b & 3) * (nb32 / 4) + (b >> 2)] = *sp;
+        }
     }
     __syncthreads();
-    const int ntok = min(kRouteTPB, A.T - t0);
-    const int nent = ntok * A.k;
-    // in-block rank of each entry among earlier entries of the same expert
+    const int nent = min(kRouteTPB, A.T - t0) * A.k;
     for (int i = threadIdx.x; i < nent; i += kRouteThreads) {
         const int e = ent[i];
         int r = 0;
         for (int j = 0; j < i; j++) r += (ent[j] == e);
         A.rank[(size_t)t0 * A.k + i] = r;
+        atomicAdd(&hist[e], 1);
     }
-    // per-block histogram
-    for (int e = threadIdx.x; e < A.E; e += kRouteThreads) {
-        int c = 0;
-        for (int j = 0; j < nent; j++) c += (ent[j] == e);
-        A.blk_cnt[(size_t)blockIdx.x * A.E + e] = c;
-    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < A.E; e += kRouteThreads)
+        A.blk_cnt[(size_t)e * A.nb + blockIdx.x] = hist[e];
 }
 
 __global__ __launch_bounds__(256) void k_topk(const float *logits, int T, int E, int ld, int k,
@@ -399,71 +412,118 @@ struct ScanArgs {
     const int32_t *blk_cnt; int nb; int E; int T; int k;
     const int32_t *idx; const float *wt; const int32_t *rank; const float *shg;
     int tn;
-    int32_t *blk_off; int32_t *e_off; int32_t *perm; int32_t *pos;
+    int32_t *blk_off; int32_t *tot; int32_t *e_off; int32_t *perm; int32_t *pos;
     int32_t *row_tok; float *row_w; int4 *tiles; int32_t *ntiles;
 };
 
-__global__ __launch_bounds__(kScanThreads) void k_scan(ScanArgs A) {
-    __shared__ int s_cnt[kMaxExperts];
-    __shared__ int s_off[kMaxExperts + 1];
-    __shared__ int s_toff[kMaxExperts + 2];
-    const int tid = threadIdx.x;
-    for (int e = tid; e < A.E; e += kScanThreads) {
+// Column scans: for each expert, the exclusive prefix of its per-block counts
+// (blk_off[e][b]) and its total.  kColExp experts per workgroup, 256 / kColExp
+// threads per expert, each summing a contiguous run of blocks.
+constexpr int kColExp = 8;
+__global__ __launch_bounds__(256) void k_colscan(ScanArgs A) {
+    constexpr int NP = 256 / kColExp;              // partitions per expert
+    __shared__ int part[kColExp][NP + 1];
+    const int el = threadIdx.x / NP, pi = threadIdx.x % NP;
+    const int e = blockIdx.x * kColExp + el;
+    const int chunk = (A.nb + NP - 1) / NP;
+    const int b0 = pi * chunk, b1 = min(A.nb, b0 + chunk);
+    const int32_t *cnt = A.blk_cnt + (size_t)e * A.nb;
+    int sum = 0;
+    if (e < A.E)
+        for (int b = b0; b < b1; b++) sum += cnt[b];
+    part[el][pi] = sum;
+    __syncthreads();
+    if (pi == 0) {
         int run = 0;
-        for (int b = 0; b < A.nb; b++) {
-            const int c = A.blk_cnt[(size_t)b * A.E + e];
-            A.blk_off[(size_t)b * A.E + e] = run;
-            run += c;
+        for (int j = 0; j < NP; j++) {
+            const int v = part[el][j];
+            part[el][j] = run;
+            run += v;
         }
-        s_cnt[e] = run;
+        part[el][NP] = run;
     }
     __syncthreads();
-    if (tid == 0) {
-        int o = 0, to = 0;
-        for (int e = 0; e < A.E; e++) {
-            s_off[e] = o;
-            s_toff[e] = to;
-            o += s_cnt[e];
-            to += (s_cnt[e] + A.tn - 1) / A.tn;
+    if (e < A.E) {
+        int run = part[el][pi];
+        for (int b = b0; b < b1; b++) {
+            const int v = cnt[b];
+            A.blk_off[(size_t)e * A.nb + b] = run;
+            run += v;
         }
-        s_off[A.E] = o;
-        s_toff[A.E] = to;
-        const int nsh = A.shg ? (A.T + A.tn - 1) / A.tn : 0;
-        s_toff[A.E + 1] = to + nsh;
-        *A.ntiles = to + nsh;
+        if (pi == 0) A.tot[e] = part[el][NP];
     }
+}
+
+// Exclusive scan of v[0..n) (n <= 256) by one wavefront into out (LDS).
+__device__ __forceinline__ void wave_scan256(const int *v, int n, int *out, int *total) {
+    const int lane = __lane_id();
+    int a[4], s = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        a[j] = (4 * lane + j < n) ? v[4 * lane + j] : 0;
+        s += a[j];
+    }
+    int inc = s;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(inc, o, 64);
+        if (lane >= o) inc += y;
+    }
+    int run = inc - s;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        if (4 * lane + j < n) out[4 * lane + j] = run;
+        run += a[j];
+    }
+    if (lane == 63 && total) *total = inc;
+}
+
+// Scatter of one route block's entries to their sorted slots: expert offsets
+// from the totals (wave scan in LDS), then p = off[e] + blk_off[e][b] + rank.
+// Block 0 also writes the offsets and the ragged tile list.  This is the
+// deterministic replacement of the reference's atomic bucketing
+// (k_moe_dispatch, q36_engine.cu:3387-3392): entry ids t*k+s ascend inside
+// each expert.
+__global__ __launch_bounds__(256) void k_scatter(ScanArgs A) {
+    __shared__ int tot[kMaxExperts], off[kMaxExperts + 1], ntile[kMaxExperts], toff[kMaxExperts + 1];
+    const int tid = threadIdx.x, b = blockIdx.x;
+    for (int e = tid; e < A.E; e += 256) {
+        tot[e] = A.tot[e];
+        ntile[e] = (tot[e] + A.tn - 1) / A.tn;
+    }
+    __syncthreads();
+    if (tid < 64) wave_scan256(tot, A.E, off, &off[A.E]);
+    else if (tid < 128) wave_scan256(ntile, A.E, toff, &toff[A.E]);
     __syncthreads();
     const int n = A.T * A.k;
-    for (int e = tid; e <= A.E; e += kScanThreads) A.e_off[e] = s_off[e];
-    for (int i = tid; i < n; i += kScanThreads) {
-        const int t = i / A.k;
-        const int b = t / kRouteTPB;
+    const int i0 = b * kRouteTPB * A.k, i1 = min(n, i0 + kRouteTPB * A.k);
+    for (int i = i0 + tid; i < i1; i += 256) {
         const int e = A.idx[i];
-        const int p = s_off[e] + A.blk_off[(size_t)b * A.E + e] + A.rank[i];
+        const int p = off[e] + A.blk_off[(size_t)e * A.nb + b] + A.rank[i];
         A.perm[p] = i;
         A.pos[i] = p;
-        A.row_tok[p] = t;
+        A.row_tok[p] = i / A.k;
         A.row_w[p] = A.wt[i];
     }
     if (A.shg) {
-        for (int t = tid; t < A.T; t += kScanThreads) {
+        for (int t = b * kRouteTPB + tid; t < min(A.T, (b + 1) * kRouteTPB); t += 256) {
             A.row_tok[n + t] = t;
             A.row_w[n + t] = 1.0f / (1.0f + expf(-A.shg[t]));
         }
     }
-    for (int e = tid; e < A.E; e += kScanThreads) {
-        const int c = s_cnt[e];
-        for (int j = 0; j * A.tn < c; j++) {
-            const int p0 = s_off[e] + j * A.tn;
-            A.tiles[s_toff[e] + j] = make_int4(e, p0, min(p0 + A.tn, s_off[e] + c), 0);
-        }
-    }
-    if (A.shg) {
-        const int base = s_toff[A.E];
-        for (int j = tid; j * A.tn < A.T; j += kScanThreads) {
+    if (b == 0) {
+        for (int e = tid; e <= A.E; e += 256) A.e_off[e] = off[e];
+        for (int e = tid; e < A.E; e += 256)
+            for (int j = 0; j < ntile[e]; j++) {
+                const int p0 = off[e] + j * A.tn;
+                A.tiles[toff[e] + j] = make_int4(e, p0, min(p0 + A.tn, off[e] + tot[e]), 0);
+            }
+        const int nsh = A.shg ? (A.T + A.tn - 1) / A.tn : 0;
+        for (int j = tid; j < nsh; j += 256) {
             const int p0 = n + j * A.tn;
-            A.tiles[base + j] = make_int4(A.E, p0, min(p0 + A.tn, n + A.T), 0);
+            A.tiles[toff[A.E] + j] = make_int4(A.E, p0, min(p0 + A.tn, n + A.T), 0);
         }
+        if (tid == 0) *A.ntiles = toff[A.E] + nsh;
     }
 }
 
@@ -478,167 +538,327 @@ struct GemmArgs {
     size_t wstride;           // bytes per expert matrix
     int E, M;                 // routed experts, rows per matrix
     const int4 *tiles; const int32_t *ntiles;
-    const uint8_t *bq, *bs;   // B rows: x by token (GATEUP) / h by sorted slot (DOWN)
+    const uint8_t *bq;        // B rows: x by token (GATEUP) / h by sorted slot (DOWN)
+    const uint8_t *bs2;       // their E8M0 scales, lane-group-major [row][4][K/128]
     const int32_t *row_tok; const float *row_w;
-    uint8_t *hq, *hs;         // GATEUP output rows (sorted slot)
+    uint8_t *hq, *hs, *hs2;   // GATEUP output rows (sorted slot): h, natural and lane-major scales
     float *dnw;               // DOWN output rows (sorted slot), weighted
     int ldo;                  // output row length
 };
 
-// Workgroup = 4 waves arranged WM x WN; each wave owns TM row tiles (per
-// matrix) x TNW token tiles of 16.  Rows per workgroup = WM*TM*16, tokens =
-// WN*TNW*16.  KD = reduction length (d_model for gate/up, d_ff for down).
-template <int MODE, int WM, int WN, int TM, int TNW, int KD>
-__global__ __launch_bounds__(256) void k_expert_gemm(GemmArgs A) {
-    static_assert(WM * WN == 4, "four waves");
-    static_assert(MODE != MODE_GATEUP || TM == 2, "gate/up waves own one 32-row h block");
-    constexpr int NMAT = MODE == MODE_GATEUP ? 2 : 1;
-    constexpr int TN = WN * TNW * 16;
-    constexpr int ROWS = WM * TM * 16;
-    constexpr int NKT = KD / 128;
-    constexpr int NSD = NKT / 4;
-    static_assert(KD % 512 == 0, "K multiple of 512");
+constexpr int kTileTok = 256;
 
-    __shared__ __align__(16) uint8_t sB[TN * kLdsRow];
-    __shared__ uint32_t sS[TN];      // 4 E8M0 bytes (K blocks of this K-step) per row
-    __shared__ int sRow[TN];
+// tile shapes of the grouped GEMMs: row tiles of 16 per workgroup (per
+// matrix) and the depth of the register ring for B (K-steps)
+#ifndef Q36_GU_RT
+#define Q36_GU_RT 4
+#endif
+#ifndef Q36_GU_BR
+#define Q36_GU_BR 4
+#endif
+#ifndef Q36_DN_RT
+#define Q36_DN_RT 8
+#endif
+#ifndef Q36_DN_BR
+#define Q36_DN_BR 4
+#endif
+constexpr int kGuRT = Q36_GU_RT, kGuBR = Q36_GU_BR;
+constexpr int kDnRT = Q36_DN_RT, kDnBR = Q36_DN_BR;
 
-    const int ti = blockIdx.x;
-    if (ti >= *A.ntiles) return;
-    const int4 tile = A.tiles[ti];
-    const int e = tile.x, p0 = tile.y, p1 = tile.z;
+// op_sel byte of both scale dwords (A and B hold 4 K-steps each), fixed once
+// the K loop is unrolled
+__device__ __forceinline__ v4f mfma_sel(int sel, const v8i &a, const v8i &b, const v4f &c, int sa, int sb) {
+    switch (sel & 3) {
+        case 0: return mfma_f4xf8<0, 0>(a, b, c, sa, sb);
+        case 1: return mfma_f4xf8<1, 1>(a, b, c, sa, sb);
+        case 2: return mfma_f4xf8<2, 2>(a, b, c, sa, sb);
+        default: return mfma_f4xf8<3, 3>(a, b, c, sa, sb);
+    }
+}
+
+constexpr int kGW = 8;                 // waves per grouped-GEMM workgroup
+constexpr int kGT = 64 * kGW;          // threads
+
+template <int MODE, int RT, int KD>
+struct GroupedLds {
+    static constexpr int NMAT = MODE == MODE_GATEUP ? 2 : 1;
+    static constexpr int NAT = NMAT * RT;
+    static constexpr int NKT = KD / 128;
+    __align__(16) uint8_t a[2][NAT * 1024];
+    __align__(16) uint32_t sc[NAT][64][NKT / 4];
+    int row[kTileTok];
+};
+
+constexpr int kRA = 4;   // depth of the register ring that carries A from HBM to LDS
+
+// NJ = number of 16-token tiles this wave owns (tiles wave, wave+kGW).
+// Pipeline per K-step kt (all rings indexed by compile-time slots: the K
+// loop is a runtime loop over groups of 4 steps, unrolled inside):
+//   1. issue B rows of step kt+BR-1 into the B register ring (and, on the
+//      first step of a group, the B scale dwords of the next group);
+//   2. issue A of step kt+kRA into the A register ring;
+//   3. MFMAs of step kt: A from LDS slot kt%2, B from the ring;
+//   4. write A of step kt+1 (loaded kRA-1 steps ago) into LDS slot (kt+1)%2;
+//   5. barrier.
+// B loads are issued before A loads in every step, so the in-order vmcnt
+// wait for the B of the current step leaves the later A loads in flight;
+// A gets kRA-1 steps of compute to arrive.  Prefetch indices are clamped to
+// the last step (redundant in-bounds loads), so the body has no branches.
+// Both scale operands come straight from loads, the byte chosen by op_sel.
+template <int MODE, int RT, int KD, int BR, int NJ>
+__device__ __forceinline__ void grouped_body(const GemmArgs &A, GroupedLds<MODE, RT, KD> &L,
+                                             const uint8_t *W0, const uint8_t *W1, int mt0, int p0,
+                                             int p1) {
+    using LT = GroupedLds<MODE, RT, KD>;
+    constexpr int NAT = LT::NAT, NKT = LT::NKT;
+    constexpr int APT = NAT * 1024 / kGT / 16;   // 16-byte A chunks per thread per K-step
+    constexpr int NJ1 = NJ > 0 ? NJ : 1;
+    constexpr int NG = NKT / 4;                  // groups of 4 K-steps
+    static_assert(NKT % 4 == 0 && BR >= 2 && kRA == 4, "rings");
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave % WM, wn = wave / WM;
-    const int rb = blockIdx.y * ROWS;
+    const int q = lane >> 4;
 
-    const uint8_t *W[NMAT];
-    W[0] = e < A.E ? A.wa + (size_t)e * A.wstride : A.sa;
-    if constexpr (NMAT == 2) W[1] = e < A.E ? A.wb + (size_t)e * A.wstride : A.sb;
-    const size_t nib_bytes = (size_t)A.M * KD / 2;
-
-    for (int i = tid; i < TN; i += 256) {
-        const int p = p0 + i;
-        sRow[i] = p < p1 ? (MODE == MODE_GATEUP ? A.row_tok[p] : p) : -1;
+    const uint8_t *asrc[APT];
+#pragma unroll
+    for (int u = 0; u < APT; u++) {
+        const int c = tid + kGT * u;
+        const int at = c >> 6;
+        const uint8_t *Wm = (LT::NMAT == 2 && at >= RT) ? W1 : W0;
+        asrc[u] = Wm + (size_t)(mt0 + at % RT) * NKT * 1024 + (c & 63) * 16;
+    }
+    // padding columns (r < 0) read row 0: they are computed but never stored,
+    // and nothing mixes columns (the h amax reduces lanes of one column)
+    const uint8_t *brp[NJ1];
+    const uint32_t *bsp[NJ1];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const int r0 = L.row[(wave + kGW * j) * 16 + (lane & 15)];
+        const int r = r0 >= 0 ? r0 : 0;
+        brp[j] = A.bq + (size_t)r * KD + q * 16;
+        bsp[j] = reinterpret_cast<const uint32_t *>(A.bs2 + (size_t)r * (KD / 32) + q * NKT);
     }
 
-    uint32_t sa[NMAT][TM][NSD];
+    v4f acc[NAT][NJ1];
 #pragma unroll
-    for (int m = 0; m < NMAT; m++)
+    for (int a = 0; a < NAT; a++)
 #pragma unroll
-        for (int tm = 0; tm < TM; tm++) {
-            const int mt = (rb >> 4) + wm * TM + tm;
-            const uint32_t *sp =
-                reinterpret_cast<const uint32_t *>(W[m] + nib_bytes + ((size_t)mt * 64 + lane) * NKT);
-#pragma unroll
-            for (int d = 0; d < NSD; d++) sa[m][tm][d] = sp[d];
-        }
+        for (int j = 0; j < NJ; j++) acc[a][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
-    v4f acc[NMAT][TM][TNW];
+    // rings as shift registers (fixed names, no ring indexing):
+    //   B: bq[0] = step kt, ..., bq[BR-2] = step kt+BR-2
+    //   A: ra1/ra2/ra3 = steps kt+1, kt+2, kt+3
+    uint4 bq[BR - 1][NJ1][2];
+    uint32_t bsd[NJ1], bsn[NJ1];   // B scale dwords of this group and the next
+    uint4 ra1[APT], ra2[APT], ra3[APT];
 #pragma unroll
-    for (int m = 0; m < NMAT; m++)
+    for (int r = 0; r < BR - 1; r++)
 #pragma unroll
-        for (int tm = 0; tm < TM; tm++)
+        for (int j = 0; j < NJ; j++) {
+            bq[r][j][0] = *reinterpret_cast<const uint4 *>(brp[j] + r * 128);
+            bq[r][j][1] = *reinterpret_cast<const uint4 *>(brp[j] + r * 128 + 64);
+        }
 #pragma unroll
-            for (int n = 0; n < TNW; n++) acc[m][tm][n] = v4f{0.f, 0.f, 0.f, 0.f};
-    __syncthreads();
+    for (int j = 0; j < NJ; j++) bsd[j] = bsp[j][0];
+#pragma unroll
+    for (int u = 0; u < APT; u++) {
+        ra1[u] = *reinterpret_cast<const uint4 *>(asrc[u] + (size_t)min(1, NKT - 1) * 1024);
+        ra2[u] = *reinterpret_cast<const uint4 *>(asrc[u] + (size_t)min(2, NKT - 1) * 1024);
+        ra3[u] = *reinterpret_cast<const uint4 *>(asrc[u] + (size_t)min(3, NKT - 1) * 1024);
+    }
 
-    const uint8_t *sSb = reinterpret_cast<const uint8_t *>(sS);
-    static_for<0, NKT>([&](auto KT) {
-        constexpr int kt = decltype(KT)::value;
-        for (int c = tid; c < TN * 8; c += 256) {
-            const int r = c >> 3, q = c & 7;
-            const int row = sRow[r];
-            uint4 v = make_uint4(0u, 0u, 0u, 0u);
-            if (row >= 0)
-                v = *reinterpret_cast<const uint4 *>(A.bq + (size_t)row * KD + kt * 128 + q * 16);
-            *reinterpret_cast<uint4 *>(sB + r * kLdsRow + q * 16) = v;
-        }
-        for (int r = tid; r < TN; r += 256) {
-            const int row = sRow[r];
-            sS[r] = row >= 0
-                        ? *reinterpret_cast<const uint32_t *>(A.bs + (size_t)row * (KD / 32) + kt * 4)
-                        : 0x7f7f7f7fu;
-        }
-        v8i a[NMAT][TM];
+#pragma unroll 1
+    for (int kg = 0; kg < NG; kg++) {
 #pragma unroll
-        for (int m = 0; m < NMAT; m++)
+        for (int ks = 0; ks < 4; ks++) {
+            const int kt = kg * 4 + ks;
+            // 1. B of step kt+BR-1 (and the next group's scale dwords)
+            const int kb = min(kt + BR - 1, NKT - 1);
+            uint4 bl[NJ1][2];
 #pragma unroll
-            for (int tm = 0; tm < TM; tm++) {
-                const int mt = (rb >> 4) + wm * TM + tm;
-                const uint4 q = *reinterpret_cast<const uint4 *>(
-                    W[m] + ((size_t)mt * NKT + kt) * 1024 + (size_t)lane * 16);
-                a[m][tm] = v8i{(int)q.x, (int)q.y, (int)q.z, (int)q.w, 0, 0, 0, 0};
+            for (int j = 0; j < NJ; j++) {
+                bl[j][0] = *reinterpret_cast<const uint4 *>(brp[j] + kb * 128);
+                bl[j][1] = *reinterpret_cast<const uint4 *>(brp[j] + kb * 128 + 64);
             }
-        __syncthreads();
+            if (ks == 0) {
 #pragma unroll
-        for (int n = 0; n < TNW; n++) {
-            // e4m3 operand: lane group q carries K 16q..16q+15 in bytes 0-15 and
-            // K 64+16q..64+16q+15 in bytes 16-31; the scale of physical K block
-            // kb (32 values) is read from lane group kb.
-            const int r = (wn * TNW + n) * 16 + (lane & 15);
-            const uint8_t *bp = sB + r * kLdsRow + (lane >> 4) * 16;
-            const uint4 b0 = *reinterpret_cast<const uint4 *>(bp);
-            const uint4 b1 = *reinterpret_cast<const uint4 *>(bp + 64);
-            const v8i b = v8i{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w,
-                              (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
-            const int sbv = sSb[r * 4 + (lane >> 4)];
+                for (int j = 0; j < NJ; j++) bsn[j] = bsp[j][min(kg + 1, NG - 1)];
+            }
+            // 2. A of step kt+4
+            uint4 an[APT];
 #pragma unroll
-            for (int m = 0; m < NMAT; m++)
+            for (int u = 0; u < APT; u++)
+                an[u] = *reinterpret_cast<const uint4 *>(asrc[u] + (size_t)min(kt + kRA, NKT - 1) * 1024);
+            // 3. MFMAs of step kt
+            v8i bv[NJ1];
 #pragma unroll
-                for (int tm = 0; tm < TM; tm++)
-                    acc[m][tm][n] = mfma_f4xf8<kt & 3>(a[m][tm], b, acc[m][tm][n],
-                                                       (int)sa[m][tm][kt >> 2], sbv);
+            for (int j = 0; j < NJ; j++)
+                bv[j] = v8i{(int)bq[0][j][0].x, (int)bq[0][j][0].y, (int)bq[0][j][0].z, (int)bq[0][j][0].w,
+                            (int)bq[0][j][1].x, (int)bq[0][j][1].y, (int)bq[0][j][1].z, (int)bq[0][j][1].w};
+#pragma unroll
+            for (int a = 0; a < NAT; a++) {
+                if (NJ == 0) break;
+                const uint4 av = *reinterpret_cast<const uint4 *>(&L.a[ks & 1][a * 1024 + lane * 16]);
+                const v8i afr = v8i{(int)av.x, (int)av.y, (int)av.z, (int)av.w, 0, 0, 0, 0};
+                const int sav = (int)L.sc[a][lane][kg];
+#pragma unroll
+                for (int j = 0; j < NJ; j++)
+                    acc[a][j] = mfma_sel(ks, afr, bv[j], acc[a][j], sav, (int)bsd[j]);
+            }
+            // pin this step's MFMAs here: without a use they sink to the
+            // epilogue and keep every step's operands live at once
+#pragma unroll
+            for (int a = 0; a < NAT; a++)
+#pragma unroll
+                for (int j = 0; j < NJ; j++) asm volatile("" : "+v"(acc[a][j]));
+            // 4. A of step kt+1 into the other LDS slot
+#pragma unroll
+            for (int u = 0; u < APT; u++)
+                *reinterpret_cast<uint4 *>(&L.a[(ks + 1) & 1][(tid + kGT * u) * 16]) = ra1[u];
+            // 5. shift the rings
+#pragma unroll
+            for (int u = 0; u < APT; u++) {
+                ra1[u] = ra2[u];
+                ra2[u] = ra3[u];
+                ra3[u] = an[u];
+            }
+#pragma unroll
+            for (int r = 0; r + 1 < BR - 1; r++)
+#pragma unroll
+                for (int j = 0; j < NJ; j++) {
+                    bq[r][j][0] = bq[r + 1][j][0];
+                    bq[r][j][1] = bq[r + 1][j][1];
+                }
+#pragma unroll
+            for (int j = 0; j < NJ; j++) {
+                bq[BR - 2][j][0] = bl[j][0];
+                bq[BR - 2][j][1] = bl[j][1];
+            }
+            lds_barrier();
+            __builtin_amdgcn_sched_barrier(0);   // keep the next step's LDS reads after the barrier
         }
-        __syncthreads();
-    });
+#pragma unroll
+        for (int j = 0; j < NJ; j++) bsd[j] = bsn[j];
+    }
 
     if constexpr (MODE == MODE_GATEUP) {
-        const int ffb = rb + wm * 32;   // this wave's 32-row h block
 #pragma unroll
-        for (int n = 0; n < TNW; n++) {
-            float h[2][4];
-            float amax = 0.0f;
+        for (int j = 0; j < NJ; j++) {
+            const int p = p0 + (wave + kGW * j) * 16 + (lane & 15);
 #pragma unroll
-            for (int tm = 0; tm < 2; tm++)
+            for (int hb = 0; hb < RT / 2; hb++) {
+                float h[2][4];
+                float amax = 0.0f;
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    h[tm][i] = silu(acc[0][tm][n][i]) * acc[1][tm][n][i];
-                    amax = fmaxf(amax, fabsf(h[tm][i]));
+                for (int r = 0; r < 2; r++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        h[r][i] = silu(acc[2 * hb + r][j][i]) * acc[RT + 2 * hb + r][j][i];
+                        amax = fmaxf(amax, fabsf(h[r][i]));
+                    }
+                amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+                amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+                const int e2 = quant_exp(amax);
+                const float mul = inv_scale(e2);
+                const int ffb = (mt0 + 2 * hb) * 16;
+                if (p < p1) {
+#pragma unroll
+                    for (int r = 0; r < 2; r++) {
+                        const uint32_t w = e4m3_encode(h[r][0] * mul) | (e4m3_encode(h[r][1] * mul) << 8) |
+                                           (e4m3_encode(h[r][2] * mul) << 16) |
+                                           (e4m3_encode(h[r][3] * mul) << 24);
+                        *reinterpret_cast<uint32_t *>(A.hq + (size_t)p * A.ldo + ffb + r * 16 + 4 * q) = w;
+                    }
+                    if (lane < 16) {
+                        const int b = ffb / 32, nb = A.ldo / 32;
+                        A.hs[(size_t)p * nb + b] = (uint8_t)(127 + e2);
+                        A.hs2[(size_t)p * nb + (b & 3) * (nb / 4) + (b >> 2)] = (uint8_t)(127 + e2);
+                    }
                 }
-            amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
-            amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
-            const int e2 = quant_exp(amax);
-            const float mul = inv_scale(e2);
-            const int p = p0 + (wn * TNW + n) * 16 + (lane & 15);
-            if (p < p1) {
-#pragma unroll
-                for (int tm = 0; tm < 2; tm++) {
-                    const uint32_t w = e4m3_encode(h[tm][0] * mul) |
-                                       (e4m3_encode(h[tm][1] * mul) << 8) |
-                                       (e4m3_encode(h[tm][2] * mul) << 16) |
-                                       (e4m3_encode(h[tm][3] * mul) << 24);
-                    *reinterpret_cast<uint32_t *>(A.hq + (size_t)p * A.ldo + ffb + tm * 16 +
-                                                  4 * (lane >> 4)) = w;
-                }
-                if (lane < 16) A.hs[(size_t)p * (A.ldo / 32) + ffb / 32] = (uint8_t)(127 + e2);
             }
         }
     } else {
 #pragma unroll
-        for (int n = 0; n < TNW; n++) {
-            const int p = p0 + (wn * TNW + n) * 16 + (lane & 15);
-            if (p < p1) {
-                const float w = A.row_w[p];
+        for (int j = 0; j < NJ; j++) {
+            const int p = p0 + (wave + kGW * j) * 16 + (lane & 15);
+            if (p >= p1) continue;
+            const float w = A.row_w[p];
 #pragma unroll
-                for (int tm = 0; tm < TM; tm++) {
-                    const int row = rb + (wm * TM + tm) * 16 + 4 * (lane >> 4);
-                    const v4f c = acc[0][tm][n];
-                    *reinterpret_cast<float4 *>(A.dnw + (size_t)p * A.ldo + row) =
-                        make_float4(c[0] * w, c[1] * w, c[2] * w, c[3] * w);
-                }
+            for (int a = 0; a < RT; a++) {
+                const int row = (mt0 + a) * 16 + 4 * q;
+                const v4f c = acc[a][j];
+                *reinterpret_cast<float4 *>(A.dnw + (size_t)p * A.ldo + row) =
+                    make_float4(c[0] * w, c[1] * w, c[2] * w, c[3] * w);
             }
         }
     }
+}
+
+// Grouped expert GEMM, one workgroup per (expert tile, row block).  The
+// tile holds every routed row of one expert up to kTileTok (longer experts
+// are split), so an expert's weights leave HBM once per row block.  A
+// (E2M1 fragments of NAT row tiles, NAT KB per K-step of 128) reaches LDS
+// through a register ring; B (e4m3 rows) goes straight to the registers of
+// the wave that owns those 16-token tiles (tiles w and w+8 of wave w); A
+// scales for all K sit in LDS from the start.
+// GATEUP: A tiles 0..RT-1 are gate rows, RT..2RT-1 the same up rows; the
+// epilogue applies SwiGLU and quantises h per 32 rows.  DOWN: RT row tiles
+// of the output, scaled by the routing weight into the staging rows.
+template <int MODE, int RT, int KD, int BR>
+__global__ __launch_bounds__(kGT) void k_grouped(GemmArgs A) {
+    using LT = GroupedLds<MODE, RT, KD>;
+    constexpr int NAT = LT::NAT, NKT = LT::NKT;
+    static_assert((NAT * 1024) % (kGT * 16) == 0, "A stage");
+    static_assert(MODE != MODE_GATEUP || RT % 2 == 0, "h blocks of 32 rows");
+    __shared__ LT L;
+
+    const int ti = blockIdx.x;
+    if (ti >= *A.ntiles) return;
+    Q36_TRACE_WG(0);
+    const int4 tile = A.tiles[ti];
+    const int e = tile.x, p0 = tile.y, p1 = tile.z;
+    const int tid = threadIdx.x, wave = tid >> 6;
+    const int mt0 = blockIdx.y * RT;
+    const size_t nib_bytes = (size_t)A.M * KD / 2;
+    const uint8_t *W0 = e < A.E ? A.wa + (size_t)e * A.wstride : A.sa;
+    const uint8_t *W1 = W0;
+    if constexpr (LT::NMAT == 2) W1 = e < A.E ? A.wb + (size_t)e * A.wstride : A.sb;
+
+    // A scales for all K of this row block (contiguous per matrix)
+    {
+        constexpr int SB = RT * 64 * NKT;
+        for (int c = tid; c < LT::NMAT * SB / 16; c += kGT) {
+            const int m = c / (SB / 16), o = (c % (SB / 16)) * 16;
+            const uint8_t *src = (m == 0 ? W0 : W1) + nib_bytes + (size_t)mt0 * 64 * NKT + o;
+            *reinterpret_cast<uint4 *>(reinterpret_cast<uint8_t *>(&L.sc[m * RT][0][0]) + o) =
+                *reinterpret_cast<const uint4 *>(src);
+        }
+    }
+    for (int i = tid; i < kTileTok; i += kGT) {
+        const int p = p0 + i;
+        L.row[i] = p < p1 ? (MODE == MODE_GATEUP ? A.row_tok[p] : p) : -1;
+    }
+    // A of K-step 0
+    {
+        constexpr int APT = NAT * 1024 / kGT / 16;
+#pragma unroll
+        for (int u = 0; u < APT; u++) {
+            const int c = tid + kGT * u;
+            const int at = c >> 6;
+            const uint8_t *Wm = (LT::NMAT == 2 && at >= RT) ? W1 : W0;
+            *reinterpret_cast<uint4 *>(&L.a[0][c * 16]) = *reinterpret_cast<const uint4 *>(
+                Wm + (size_t)(mt0 + at % RT) * NKT * 1024 + (c & 63) * 16);
+        }
+    }
+    __syncthreads();
+    const int ntt = (p1 - p0 + 15) >> 4;
+    static_assert(kTileTok == 16 * kGW * 2, "two token tiles per wave");
+    const int nj = ntt > wave ? (ntt - wave + kGW - 1) / kGW : 0;
+    switch (nj) {
+        case 0: grouped_body<MODE, RT, KD, BR, 0>(A, L, W0, W1, mt0, p0, p1); break;
+        case 1: grouped_body<MODE, RT, KD, BR, 1>(A, L, W0, W1, mt0, p0, p1); break;
+        default: grouped_body<MODE, RT, KD, BR, 2>(A, L, W0, W1, mt0, p0, p1); break;
+    }
+    Q36_TRACE_WG(1);
 }
 
 // ---------------------------------------------------------------------------
@@ -1140,11 +1360,11 @@ struct q36moe_ctx {
     size_t tile_cap;
     void *base;
     int32_t *topk_idx; float *topk_w; int32_t *rank;
-    uint8_t *xq, *xs;
-    int32_t *blk_cnt, *blk_off, *e_off, *perm, *pos, *row_tok;
+    uint8_t *xq, *xs, *xs2;
+    int32_t *blk_cnt, *blk_off, *tot, *e_off, *perm, *pos, *row_tok;
     float *row_w;
     int4 *tiles; int32_t *ntiles;
-    uint8_t *hq, *hs;
+    uint8_t *hq, *hs, *hs2;
     float *dnw;
     float *hf;                      // direct path: fp32 SwiGLU rows
     uint32_t *sync;                 // fused decode: arrive[16], depart[16], err
@@ -1190,12 +1410,6 @@ int alloc_weights(int E, int D, int FF, int FFsh, q36moe_weights **out) {
     return Q36MOE_OK;
 }
 
-template <int MODE, int WM, int WN, int TM, int TNW, int KD>
-void launch_gemm(const GemmArgs &a, int tiles, int rows, hipStream_t s) {
-    constexpr int ROWS = WM * TM * 16;
-    hipLaunchKernelGGL((k_expert_gemm<MODE, WM, WN, TM, TNW, KD>), dim3(tiles, rows / ROWS),
-                       dim3(256), 0, s, a);
-}
 
 }  // namespace
 
@@ -1312,11 +1526,13 @@ int q36moe_ctx_create(int max_tokens, int n_expert, int d_model, int d_ff, int t
     auto take = [&off](size_t bytes) { size_t o = off; off = align256(off + bytes); return o; };
     const size_t o_idx = take(n * 4), o_w = take(n * 4), o_rank = take(n * 4);
     const size_t o_xq = take((size_t)max_tokens * d_model), o_xs = take((size_t)max_tokens * d_model / 32);
+    const size_t o_xs2 = take((size_t)max_tokens * d_model / 32);
     const size_t o_bc = take((size_t)c->nb_max * n_expert * 4), o_bo = take((size_t)c->nb_max * n_expert * 4);
+    const size_t o_tot = take((size_t)n_expert * 4);
     const size_t o_eo = take((size_t)(n_expert + 1) * 4), o_perm = take(n * 4), o_pos = take(n * 4);
     const size_t o_rt = take(rows * 4), o_rw = take(rows * 4);
     const size_t o_tiles = take(c->tile_cap * 16), o_nt = take(4);
-    const size_t o_hq = take(rows * d_ff), o_hs = take(rows * d_ff / 32);
+    const size_t o_hq = take(rows * d_ff), o_hs = take(rows * d_ff / 32), o_hs2 = take(rows * d_ff / 32);
     const size_t o_dnw = take(rows * d_model * 4);
     const size_t direct_rows = (size_t)(max_tokens < kDirectMaxT ? max_tokens : kDirectMaxT) * (top_k + 1);
     const size_t o_hf = take(direct_rows * d_ff * 4);
@@ -1329,9 +1545,10 @@ int q36moe_ctx_create(int max_tokens, int n_expert, int d_model, int d_ff, int t
     c->topk_idx = reinterpret_cast<int32_t *>(b + o_idx);
     c->topk_w = reinterpret_cast<float *>(b + o_w);
     c->rank = reinterpret_cast<int32_t *>(b + o_rank);
-    c->xq = b + o_xq; c->xs = b + o_xs;
+    c->xq = b + o_xq; c->xs = b + o_xs; c->xs2 = b + o_xs2;
     c->blk_cnt = reinterpret_cast<int32_t *>(b + o_bc);
     c->blk_off = reinterpret_cast<int32_t *>(b + o_bo);
+    c->tot = reinterpret_cast<int32_t *>(b + o_tot);
     c->e_off = reinterpret_cast<int32_t *>(b + o_eo);
     c->perm = reinterpret_cast<int32_t *>(b + o_perm);
     c->pos = reinterpret_cast<int32_t *>(b + o_pos);
@@ -1339,7 +1556,7 @@ int q36moe_ctx_create(int max_tokens, int n_expert, int d_model, int d_ff, int t
     c->row_w = reinterpret_cast<float *>(b + o_rw);
     c->tiles = reinterpret_cast<int4 *>(b + o_tiles);
     c->ntiles = reinterpret_cast<int32_t *>(b + o_nt);
-    c->hq = b + o_hq; c->hs = b + o_hs;
+    c->hq = b + o_hq; c->hs = b + o_hs; c->hs2 = b + o_hs2;
     c->dnw = reinterpret_cast<float *>(b + o_dnw);
     c->hf = reinterpret_cast<float *>(b + o_hf);
     c->sync = reinterpret_cast<uint32_t *>(b + o_sync);
@@ -1390,8 +1607,7 @@ int q36moe_forward(q36moe_ctx *c, const q36moe_weights *w, const void *x, int x_
     const int E = c->E, D = c->D, FF = c->FF, K = c->K;
     const int n = T * K;
     const int nb = (T + kRouteTPB - 1) / kRouteTPB;
-    const bool wide = n >= 2048;
-    const int tn = wide ? 128 : 16;
+    const int tn = kTileTok;
     int tiles = n / tn + (n < E ? n : E) + (has_sh ? (T + tn - 1) / tn : 0);
     tiles = (tiles + 7) & ~7;
     hipStream_t s = c->stream;
@@ -1424,32 +1640,33 @@ int q36moe_forward(q36moe_ctx *c, const q36moe_weights *w, const void *x, int x_
         mark(ST_COUNT);
     } else {
     mark(ST_ROUTE);
-    RouteArgs ra{logits, ld_logits, T, E, K, scale, x, x_fmt, D,
-                 c->topk_idx, c->topk_w, c->xq, c->xs, c->blk_cnt, c->rank};
+    RouteArgs ra{logits, ld_logits, T, E, K, scale, x, x_fmt, D, nb,
+                 c->topk_idx, c->topk_w, c->xq, c->xs, c->xs2, c->blk_cnt, c->rank};
     hipLaunchKernelGGL(k_route, dim3(nb), dim3(kRouteThreads), 0, s, ra);
 
     mark(ST_SCAN);
     ScanArgs sa{c->blk_cnt, nb, E, T, K, c->topk_idx, c->topk_w, c->rank, shg, tn,
-                c->blk_off, c->e_off, c->perm, c->pos, c->row_tok, c->row_w, c->tiles, c->ntiles};
-    hipLaunchKernelGGL(k_scan, dim3(1), dim3(kScanThreads), 0, s, sa);
+                c->blk_off, c->tot, c->e_off, c->perm, c->pos, c->row_tok, c->row_w, c->tiles, c->ntiles};
+    hipLaunchKernelGGL(k_colscan, dim3((E + kColExp - 1) / kColExp), dim3(256), 0, s, sa);
+    hipLaunchKernelGGL(k_scatter, dim3(nb), dim3(256), 0, s, sa);
 
     mark(ST_GATEUP);
     GemmArgs ga{};
     ga.wa = w->gate; ga.wb = w->up; ga.sa = w->sh_gate; ga.sb = w->sh_up;
     ga.wstride = w->gu_bytes; ga.E = E; ga.M = FF;
     ga.tiles = c->tiles; ga.ntiles = c->ntiles;
-    ga.bq = c->xq; ga.bs = c->xs; ga.row_tok = c->row_tok; ga.row_w = c->row_w;
-    ga.hq = c->hq; ga.hs = c->hs; ga.ldo = FF;
+    ga.bq = c->xq; ga.bs2 = c->xs2; ga.row_tok = c->row_tok; ga.row_w = c->row_w;
+    ga.hq = c->hq; ga.hs = c->hs; ga.hs2 = c->hs2; ga.ldo = FF;
     GemmArgs da = ga;
     da.wa = w->down; da.wb = nullptr; da.sa = w->sh_down; da.sb = nullptr;
     da.wstride = w->dn_bytes; da.M = D;
-    da.bq = c->hq; da.bs = c->hs; da.dnw = c->dnw; da.ldo = D;
-    if (wide) launch_gemm<MODE_GATEUP, 2, 2, 2, 4, 2048>(ga, tiles, FF, s);
-    else launch_gemm<MODE_GATEUP, 4, 1, 2, 1, 2048>(ga, tiles, FF, s);
+    da.bq = c->hq; da.bs2 = c->hs2; da.dnw = c->dnw; da.ldo = D;
+    hipLaunchKernelGGL((k_grouped<MODE_GATEUP, kGuRT, 2048, kGuBR>), dim3(tiles, FF / (16 * kGuRT)),
+                       dim3(kGT), 0, s, ga);
 
     mark(ST_DOWN);
-    if (wide) launch_gemm<MODE_DOWN, 2, 2, 4, 4, 512>(da, tiles, D, s);
-    else launch_gemm<MODE_DOWN, 4, 1, 2, 1, 512>(da, tiles, D, s);
+    hipLaunchKernelGGL((k_grouped<MODE_DOWN, kDnRT, 512, kDnBR>), dim3(tiles, D / (16 * kDnRT)),
+                       dim3(kGT), 0, s, da);
 
     mark(ST_COMBINE);
     hipLaunchKernelGGL(k_combine, dim3(T), dim3(256), 0, s, c->dnw, c->pos, T, K, D, has_sh, out,
