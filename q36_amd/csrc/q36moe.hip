@@ -54,6 +54,7 @@ constexpr int kMaxExperts = 256;
 constexpr int kMaxTopK = 8;
 constexpr int kRouteTPB = 16;      // tokens per k_route workgroup (one wavefront each)
 constexpr int kRouteThreads = 1024;
+constexpr int kRouteD = 2048;     // d_model of k_route (the q36 shape, q36.h:78-84)
 constexpr int kDirectMaxT = 16;    // largest batch routed to the direct (unsorted) path
 
 // ---------------------------------------------------------------------------
@@ -75,6 +76,23 @@ __device__ __forceinline__ uint32_t e4m3_encode(float v) {
     const uint32_t rb = (a >> 19) & 1u, sticky = a & 0x7ffffu;
     r += rb & ((sticky != 0u) | (r & 1u));
     return sign | (r > 0x7eu ? 0x7eu : r);
+}
+
+// Four scaled values to e4m3 bytes (first value in the low byte).  The
+// hardware conversion (v_cvt_pk_fp8_f32: OCP E4M3FN, round to nearest even)
+// equals e4m3_encode for every finite |v| <= 448 -- all the per-32
+// quantiser produces from a finite block -- as an exhaustive run over all
+// 2^32 fp32 patterns showed; NaN and infinities, where the hardware neither
+// saturates nor canonicalises NaN, go through e4m3_encode.
+__device__ __forceinline__ uint32_t e4m3x4(float a, float b, float c, float d) {
+    const bool fin = __builtin_isfinite(a) & __builtin_isfinite(b) & __builtin_isfinite(c) &
+                     __builtin_isfinite(d);
+    if (__builtin_expect(fin, 1)) {
+        int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+        w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+        return (uint32_t)w;
+    }
+    return e4m3_encode(a) | (e4m3_encode(b) << 8) | (e4m3_encode(c) << 16) | (e4m3_encode(d) << 24);
 }
 
 // e2 = ceil(log2(amax/448)) from the binary exponent of the fp32 quotient,
@@ -155,23 +173,29 @@ __device__ __forceinline__ uint32_t logit_key(float f) {
 
 __device__ __forceinline__ int popc_ballot(bool p) { return __popcll(__ballot(p)); }
 
-// Top-k routing of one token by one wavefront, without serial cross-lane
-// argmax rounds:
-//   1. the k-th largest key is found by a radix search over the key bits
-//      whose counts are ballots, stopping as soon as exactly k keys clear the
-//      threshold; ties at the threshold take the lowest expert indices;
-//   2. the k picks are written to LDS in ascending index order (mbcnt
-//      prefix) and read back by every lane;
-//   3. lane r < k owns pick r: its slot is its rank under (value desc, index
-//      asc) -- the order of the reference's k rounds of warp argmax with ties
-//      to the lower index (q36_ops.cuh:409-427) -- and its weight is
-//      exp(l_r - max) / sum_q exp(l_q - max) * scale, the reference's
-//      exp(l-m)/sum_all renormalised over the picks (q36_ops.cuh:424-430), in
-//      which the full denominator cancels; the sum runs in index order.
-// `lds` is 2*kMaxTopK words private to the wave.
+// Top-k routing of one token by one wavefront, without k serial rounds of
+// cross-lane argmax:
+//   1. a lower bound B on the k-th largest key: the minimum of the maxima of
+//      eight disjoint 8-lane groups (eight distinct keys are >= B, so at least
+//      k <= 8 keys clear it);
+//   2. the keys >= B (the candidates; about 2k for N(0,1) logits) are packed
+//      into LDS in ascending index order (mbcnt prefix);
+//   3. each candidate's rank under (value desc, index asc) -- the order of
+//      the reference's k rounds of warp argmax with ties to the lower index
+//      (q36_ops.cuh:409-427) -- is counted against the other candidates
+//      (a key below B cannot outrank one at or above it); ranks < k are the
+//      picks and the rank is the slot;
+//   4. lane r < k owns pick r; its weight is exp(l_r - max) / sum_q exp(l_q -
+//      max) * scale, the reference's exp(l-m)/sum_all renormalised over the
+//      picks (q36_ops.cuh:424-430), in which the full denominator cancels;
+//      the sum runs in slot order as the reference's renormalisation does.
+// `lds` is kRouteLds words private to the wave: [0,8) pick keys, [8,16) pick
+// indices, then up to 256 (key, index) candidates.
+constexpr int kRouteLds = 2 * kMaxTopK + 2 * (kMaxExperts + 8);
+
 struct Pick {
     int idx;     // expert index of pick `lane` (lanes < k)
-    int slot;    // its rank in (value desc, index asc) order
+    int slot;    // its rank in (value desc, index asc) order (== lane)
     float w;     // renormalised weight times scale
 };
 
@@ -182,92 +206,84 @@ __device__ __forceinline__ float key_val(uint32_t kk) {
     return __uint_as_float((kk & 0x80000000u) ? (kk & 0x7fffffffu) : ~kk);
 }
 
+// max over each aligned group of 8 lanes, in every lane of the group
+__device__ __forceinline__ uint32_t group8_max(uint32_t v) {
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xf, 0xf, false));   // quad xor 1
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xf, 0xf, false));   // quad xor 2
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xf, 0xf, false));  // half-row mirror
+    return v;
+}
+
 __device__ __forceinline__ Pick route_pick(const float *__restrict__ l, int E, int k, float scale,
                                            uint32_t *lds) {
     const int lane = __lane_id();
     uint32_t key[4];
+    bool ok[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const int e = lane + 64 * j;
         const float v = l[e < E ? e : E - 1];
-        key[j] = e < E ? logit_key(v) : 0u;
+        ok[j] = e < E;
+        key[j] = ok[j] ? logit_key(v) : 0u;
     }
-#ifdef Q36MOE_TRACE
-    if (key[0] == 12345u) key[0] = 0u;
-#endif
     Q36_TRACE_AT(10);
-    // two key bits per step: the three candidate counts are independent
-    uint32_t tau = 0;
-    int cnt_tau = E;
-    for (int bit = 30; bit >= 0 && cnt_tau != k; bit -= 2) {
-        const uint32_t c1 = tau | (1u << bit), c2 = tau | (2u << bit), c3 = tau | (3u << bit);
-        const int n1 = popc_ballot(key[0] >= c1) + popc_ballot(key[1] >= c1) +
-                       popc_ballot(key[2] >= c1) + popc_ballot(key[3] >= c1);
-        const int n2 = popc_ballot(key[0] >= c2) + popc_ballot(key[1] >= c2) +
-                       popc_ballot(key[2] >= c2) + popc_ballot(key[3] >= c2);
-        const int n3 = popc_ballot(key[0] >= c3) + popc_ballot(key[1] >= c3) +
-                       popc_ballot(key[2] >= c3) + popc_ballot(key[3] >= c3);
-        if (n3 >= k) { tau = c3; cnt_tau = n3; }
-        else if (n2 >= k) { tau = c2; cnt_tau = n2; }
-        else if (n1 >= k) { tau = c1; cnt_tau = n1; }
-    }
-    Q36_TRACE_AT(11);
-    int need = k;
+    // 1. bound: min over the 8 group maxima (a group with no valid key gives 0)
+    uint32_t lm = max(max(key[0], key[1]), max(key[2], key[3]));
+    const uint32_t gm = group8_max(lm);
+    uint32_t bnd = __builtin_amdgcn_readlane(gm, 0);
 #pragma unroll
-    for (int j = 0; j < 4; j++) need -= popc_ballot(key[j] > tau);
-    int base = 0;
+    for (int g = 1; g < 8; g++) bnd = min(bnd, (uint32_t)__builtin_amdgcn_readlane(gm, 8 * g));
+    // 2. pack the candidates (index order) as 64-bit order values
+    //    key << 32 | ~index: larger key first, then lower index
+    uint64_t *cand = reinterpret_cast<uint64_t *>(lds + 2 * kMaxTopK);
+    int nc = 0;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-        uint64_t eq = __ballot(key[j] == tau);
-        uint64_t take = 0;
-        while (need > 0 && eq) {
-            take |= eq & (~eq + 1);
-            eq &= eq - 1;
-            need--;
+        const bool c = ok[j] && key[j] >= bnd;
+        const uint64_t sel = __ballot(c);
+        const int pos = nc + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(sel >> 32),
+                                                            __builtin_amdgcn_mbcnt_lo((uint32_t)sel, 0u));
+        if (c) cand[pos] = ((uint64_t)key[j] << 32) | (uint32_t)~(uint32_t)(lane + 64 * j);
+        nc += __popcll(sel);
+    }
+    // padded to a multiple of 8 with 0, which outranks nothing
+    if (lane < 8) cand[nc + lane] = 0ull;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    Q36_TRACE_AT(11);
+    // 3. rank each candidate; ranks below k are the picks
+    for (int c0 = 0; c0 < nc; c0 += 64) {
+        const int ci = c0 + lane;
+        const uint64_t mo = cand[ci < nc ? ci : 0];
+        int r = 0;
+        for (int d = 0; d < nc; d += 8) {
+            uint64_t o[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) o[u] = cand[d + u];
+#pragma unroll
+            for (int u = 0; u < 8; u++) r += o[u] > mo;
         }
-        const uint64_t sel = __ballot(key[j] > tau) | take;
-        const int pos = base + (int)__builtin_amdgcn_mbcnt_hi(
-                                   (uint32_t)(sel >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)sel, 0u));
-        if ((sel >> lane) & 1ull) {
-            lds[pos] = key[j];
-            lds[kMaxTopK + pos] = (uint32_t)(lane + 64 * j);
+        if (ci < nc && r < k) {
+            lds[r] = (uint32_t)(mo >> 32);
+            lds[kMaxTopK + r] = ~(uint32_t)mo;
         }
-        base += __popcll(sel);
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     Q36_TRACE_AT(12);
-    uint32_t gk[kMaxTopK];
-    int gi[kMaxTopK];
-#pragma unroll
-    for (int q = 0; q < kMaxTopK; q++) {
-        gk[q] = q < k ? lds[q] : 0u;
-        gi[q] = q < k ? (int)lds[kMaxTopK + q] : 0x7fffffff;
-    }
+    // 4. weights
     const int me = lane < k ? lane : 0;
-    const uint32_t mk = lds[me];
-    const int mi = (int)lds[kMaxTopK + me];
-    uint32_t kmax = gk[0];
-#pragma unroll
-    for (int q = 1; q < kMaxTopK; q++) kmax = gk[q] > kmax ? gk[q] : kmax;
-    const float vmax = key_val(kmax);
+    const float vmax = key_val(lds[0]);
     float wsum = 0.0f;
-    int rank = 0;
 #pragma unroll
-    for (int q = 0; q < kMaxTopK; q++) {
-        if (q < k) {
-            wsum += fast_exp(key_val(gk[q]) - vmax);
-            rank += (gk[q] > mk || (gk[q] == mk && gi[q] < mi)) ? 1 : 0;
-        }
-    }
+    for (int q = 0; q < kMaxTopK; q++)
+        if (q < k) wsum += fast_exp(key_val(lds[q]) - vmax);
     Pick P;
-    P.idx = mi;
-    P.slot = rank;
-    P.w = fast_exp(key_val(mk) - vmax) * __builtin_amdgcn_rcpf(wsum) * scale;
-#ifdef Q36MOE_TRACE
-    if (P.w == 12345.f) P.slot = 0;
-#endif
+    P.idx = (int)lds[kMaxTopK + me];
+    P.slot = me;
+    P.w = fast_exp(key_val(lds[me]) - vmax) * __builtin_amdgcn_rcpf(wsum) * scale;
     Q36_TRACE_AT(13);
     return P;
 }
@@ -335,12 +351,45 @@ __device__ __forceinline__ void quant_block32(const void *__restrict__ x, int x_
     uint32_t w[8];
 #pragma unroll
     for (int i = 0; i < 8; i++)
-        w[i] = e4m3_encode(v[4 * i] * mul) | (e4m3_encode(v[4 * i + 1] * mul) << 8) |
-               (e4m3_encode(v[4 * i + 2] * mul) << 16) | (e4m3_encode(v[4 * i + 3] * mul) << 24);
+        w[i] = e4m3x4(v[4 * i] * mul, v[4 * i + 1] * mul, v[4 * i + 2] * mul, v[4 * i + 3] * mul);
     uint4 *qo = reinterpret_cast<uint4 *>(q);
     qo[0] = make_uint4(w[0], w[1], w[2], w[3]);
     qo[1] = make_uint4(w[4], w[5], w[6], w[7]);
     *s = (uint8_t)(127 + e2);
+}
+
+// Quantise 8 consecutive values held by one lane; lanes 4j..4j+3 form one
+// 32-value block (amax via two xor-shuffles).  Writes 8 e4m3 bytes and,
+// from the first lane of the block, the E8M0 byte.
+__device__ __forceinline__ uint8_t quant8_lane(const float (&v)[8], int lane, uint8_t *q, uint8_t *sc) {
+    float a = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) a = fmaxf(a, fabsf(v[i]));
+    a = fmaxf(a, __shfl_xor(a, 1, 64));
+    a = fmaxf(a, __shfl_xor(a, 2, 64));
+    const int e2 = quant_exp(a);
+    const float mul = inv_scale(e2);
+    const uint32_t w0 = e4m3x4(v[0] * mul, v[1] * mul, v[2] * mul, v[3] * mul);
+    const uint32_t w1 = e4m3x4(v[4] * mul, v[5] * mul, v[6] * mul, v[7] * mul);
+    *reinterpret_cast<uint2 *>(q) = make_uint2(w0, w1);
+    if ((lane & 3) == 0) *sc = (uint8_t)(127 + e2);
+    return (uint8_t)(127 + e2);
+}
+
+__device__ __forceinline__ void load8(const void *x, int fmt, size_t off, float (&v)[8]) {
+    if (fmt == Q36MOE_FMT_F32) {
+        const float4 *p = reinterpret_cast<const float4 *>(static_cast<const float *>(x) + off);
+        const float4 a = p[0], b = p[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+        const uint4 t = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(x) + off);
+        const uint32_t w[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            v[2 * j] = __uint_as_float(w[j] << 16);
+            v[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+        }
+    }
 }
 
 struct RouteArgs {
@@ -351,46 +400,62 @@ struct RouteArgs {
 };
 
 // One wavefront per token, kRouteTPB tokens per workgroup: top-k routing,
-// FP8 quantisation of x, then the block's per-expert counts (expert-major,
-// blk_cnt[e][block]) and each entry's rank among the block's earlier entries
-// of the same expert (the stable order of the sort).
+// FP8 quantisation of x (8 values per lane, 4 lanes per 32-block), then the
+// block's per-expert counts (expert-major, blk_cnt[e][block]) and each
+// entry's rank among the block's earlier entries of the same expert (the
+// stable order of the sort), from a per-expert mask of the block's tokens.
 __global__ __launch_bounds__(kRouteThreads) void k_route(RouteArgs A) {
+    __shared__ uint32_t tmask[kMaxExperts];
     __shared__ int ent[kRouteTPB * kMaxTopK];
-    __shared__ int hist[kMaxExperts];
-    __shared__ uint32_t rlds[kRouteThreads / 64][2 * kMaxTopK];
+    __shared__ uint32_t rlds[kRouteThreads / 64][kRouteLds];
+    static_assert(kRouteTPB <= 32, "token mask");
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int t0 = blockIdx.x * kRouteTPB;
     const int nb32 = A.D / 32;
-    for (int e = threadIdx.x; e < A.E; e += kRouteThreads) hist[e] = 0;
+    for (int e = threadIdx.x; e < A.E; e += kRouteThreads) tmask[e] = 0u;
+    __syncthreads();
     const int t = t0 + wave;
+    Q36_TRACE_AT(20);
     if (wave < kRouteTPB && t < A.T) {
-        route_token(A.logits + (size_t)t * A.ld, A.E, A.k, A.scale, 1,
-                    A.idx + (size_t)t * A.k, A.wt + (size_t)t * A.k, ent + wave * A.k, rlds[wave]);
-        for (int b = lane; b < nb32; b += 64) {
-            uint8_t *sp = A.xs + (size_t)t * nb32 + b;
-            quant_block32(A.x, A.x_fmt, (size_t)t * A.D + (size_t)b * 32,
-                          A.xq + (size_t)t * A.D + (size_t)b * 32, sp);
+        // x of the token (kRouteD values, 8 per lane per pass) is loaded
+        // before routing so both latencies overlap
+        float v[kRouteD / 512][8];
+#pragma unroll
+        for (int c = 0; c < kRouteD / 512; c++) load8(A.x, A.x_fmt, (size_t)t * A.D + c * 512 + lane * 8, v[c]);
+        const Pick P = route_pick(A.logits + (size_t)t * A.ld, A.E, A.k, A.scale, rlds[wave]);
+        if (lane < A.k) {
+            A.idx[(size_t)t * A.k + lane] = P.idx;
+            A.wt[(size_t)t * A.k + lane] = P.w;
+            ent[wave * A.k + lane] = P.idx;
+            atomicOr(&tmask[P.idx], 1u << wave);
+        }
+        Q36_TRACE_AT(21);
+#pragma unroll
+        for (int c = 0; c < kRouteD / 512; c++) {
+            const size_t o = (size_t)t * A.D + c * 512 + lane * 8;
+            const int b = c * 16 + (lane >> 2);
+            const uint8_t sb = quant8_lane(v[c], lane, A.xq + o, A.xs + (size_t)t * nb32 + b);
             // lane-group-major copy for the grouped GEMM: [t][b % 4][b / 4]
-            A.xs2[(size_t)t * nb32 + (b & 3) * (nb32 / 4) + (b >> 2)] = *sp;
+            if ((lane & 3) == 0) A.xs2[(size_t)t * nb32 + (b & 3) * (nb32 / 4) + (b >> 2)] = sb;
         }
     }
+    Q36_TRACE_AT(22);
     __syncthreads();
-    const int nent = min(kRouteTPB, A.T - t0) * A.k;
-    for (int i = threadIdx.x; i < nent; i += kRouteThreads) {
-        const int e = ent[i];
-        int r = 0;
-        for (int j = 0; j < i; j++) r += (ent[j] == e);
-        A.rank[(size_t)t0 * A.k + i] = r;
-        atomicAdd(&hist[e], 1);
+    Q36_TRACE_AT(23);
+    const int ntok = min(kRouteTPB, A.T - t0);
+    if (threadIdx.x < ntok * A.k) {
+        const int tl = threadIdx.x / A.k;
+        const int e = ent[threadIdx.x];
+        A.rank[(size_t)t0 * A.k + threadIdx.x] = __popc(tmask[e] & ((1u << tl) - 1u));
     }
-    __syncthreads();
+    Q36_TRACE_AT(24);
     for (int e = threadIdx.x; e < A.E; e += kRouteThreads)
-        A.blk_cnt[(size_t)e * A.nb + blockIdx.x] = hist[e];
+        A.blk_cnt[(size_t)e * A.nb + blockIdx.x] = __popc(tmask[e]);
 }
 
 __global__ __launch_bounds__(256) void k_topk(const float *logits, int T, int E, int ld, int k,
                                              float scale, int renorm, int32_t *idx, float *wt) {
-    __shared__ uint32_t rlds[4][2 * kMaxTopK];
+    __shared__ uint32_t rlds[4][kRouteLds];
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= T) return;
     route_token(logits + (size_t)t * ld, E, k, scale, renorm, idx + (size_t)t * k, wt + (size_t)t * k,
@@ -666,7 +731,7 @@ __device__ __forceinline__ void grouped_body(const GemmArgs &A, GroupedLds<MODE,
         ra3[u] = *reinterpret_cast<const uint4 *>(asrc[u] + (size_t)min(3, NKT - 1) * 1024);
     }
 
-#pragma unroll 1
+#pragma unroll
     for (int kg = 0; kg < NG; kg++) {
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
@@ -763,9 +828,8 @@ __device__ __forceinline__ void grouped_body(const GemmArgs &A, GroupedLds<MODE,
                 if (p < p1) {
 #pragma unroll
                     for (int r = 0; r < 2; r++) {
-                        const uint32_t w = e4m3_encode(h[r][0] * mul) | (e4m3_encode(h[r][1] * mul) << 8) |
-                                           (e4m3_encode(h[r][2] * mul) << 16) |
-                                           (e4m3_encode(h[r][3] * mul) << 24);
+                        const uint32_t w = e4m3x4(h[r][0] * mul, h[r][1] * mul, h[r][2] * mul,
+                                                  h[r][3] * mul);
                         *reinterpret_cast<uint32_t *>(A.hq + (size_t)p * A.ldo + ffb + r * 16 + 4 * q) = w;
                     }
                     if (lane < 16) {
@@ -885,41 +949,6 @@ struct DirectArgs {
 constexpr int kDD = 2048;   // d_model of the instantiated kernels
 constexpr int kDF = 512;    // d_ff
 
-// Quantise 8 consecutive values held by one lane; lanes 4j..4j+3 form one
-// 32-value block (amax via two xor-shuffles).  Writes 8 e4m3 bytes and,
-// from the first lane of the block, the E8M0 byte.
-__device__ __forceinline__ void quant8_lane(const float (&v)[8], int lane, uint8_t *q, uint8_t *sc) {
-    float a = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; i++) a = fmaxf(a, fabsf(v[i]));
-    a = fmaxf(a, __shfl_xor(a, 1, 64));
-    a = fmaxf(a, __shfl_xor(a, 2, 64));
-    const int e2 = quant_exp(a);
-    const float mul = inv_scale(e2);
-    const uint32_t w0 = e4m3_encode(v[0] * mul) | (e4m3_encode(v[1] * mul) << 8) |
-                        (e4m3_encode(v[2] * mul) << 16) | (e4m3_encode(v[3] * mul) << 24);
-    const uint32_t w1 = e4m3_encode(v[4] * mul) | (e4m3_encode(v[5] * mul) << 8) |
-                        (e4m3_encode(v[6] * mul) << 16) | (e4m3_encode(v[7] * mul) << 24);
-    *reinterpret_cast<uint2 *>(q) = make_uint2(w0, w1);
-    if ((lane & 3) == 0) *sc = (uint8_t)(127 + e2);
-}
-
-__device__ __forceinline__ void load8(const void *x, int fmt, size_t off, float (&v)[8]) {
-    if (fmt == Q36MOE_FMT_F32) {
-        const float4 *p = reinterpret_cast<const float4 *>(static_cast<const float *>(x) + off);
-        const float4 a = p[0], b = p[1];
-        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-    } else {
-        const uint4 t = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(x) + off);
-        const uint32_t w[4] = {t.x, t.y, t.z, t.w};
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            v[2 * j] = __uint_as_float(w[j] << 16);
-            v[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
-        }
-    }
-}
-
 // Entry i (token t, slot s; or the shared expert of token t for i >= T*k)
 // x 16 rows of gate and up.  Wave w reduces K range [512w, 512w+512): it
 // quantises exactly that range of x into LDS, so no cross-wave exchange is
@@ -928,7 +957,7 @@ struct DirectGateupLds {
     __align__(16) uint8_t sx[kDD + 32];   // + 32 zero bytes
     uint8_t sxs[kDD / 32];
     float red[4][2][16];
-    uint32_t rlds[4][2 * kMaxTopK];
+    uint32_t rlds[4][kRouteLds];
 };
 
 template <bool FUSED>
