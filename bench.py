@@ -54,6 +54,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="only run a plain device copy of this many MiB (counter calibration)")
     return ap.parse_args()
 
 
@@ -100,6 +102,23 @@ def kernel_flops(stage, T, shared):
     return P * (2 * D * 2 * FF if stage == "gateup" else 2 * FF * D)
 
 
+def measured_traffic(config, stage):
+    """HBM bytes per launch of a stage's kernel from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (profiles/hbm_traffic.md), each counter
+    scaled by its reading on a plain copy of known size; None when absent."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) >= 5 and cells[0] == config and cells[1] == stage:
+            try:
+                return float(cells[4])
+            except ValueError:
+                return None
+    return None
+
+
 def cpu_baseline(cfg_name, T, seconds, shared):
     """The C oracle's fp32 layer forward on host cores over a bounded sample
     of tokens of the same configuration."""
@@ -135,6 +154,18 @@ def main():
     import torch
     from q36_amd import moe
 
+    if args.copy_mib:
+        # a plain copy of known size: the reference point that scales the
+        # FETCH_SIZE / WRITE_SIZE counters of the layer kernels
+        n = args.copy_mib << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(4):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": n, "launches": 4}))
+        return
+
     cfg = CONFIGS[args.config]
     T, shared = cfg["T"], cfg["shared"]
     steps = args.steps if args.steps is not None else cfg["steps"]
@@ -169,18 +200,31 @@ def main():
     torch.cuda.synchronize()
     ms = ev0.elapsed_time(ev1) / steps
 
-    # per-stage pass: HIP events around each kernel on the context stream
-    layer.set_timing(True)
-    layer.stage_times(reset=True)
-    U_sum = 0
-    n_stage = min(steps, 200)
-    for i in range(n_stage):
-        step(i)
-        U_sum += distinct_experts(layer, moe)
-    stages = layer.stage_times(reset=True)
-    layer.set_timing(False)
-    U = U_sum / n_stage
-    st_us = {k: 1e3 * v[0] / max(v[1], 1) for k, v in stages.items()}
+    # per-kernel durations: one more forward fixes the stage inputs, then
+    # each stage's kernels are launched again `reps` times back to back over
+    # the rotating weight sets, bracketed by two HIP events on the layer's
+    # stream (the stream the kernels run on)
+    step(0)
+    torch.cuda.synchronize()
+    U = distinct_experts(layer, moe)
+    reps = max(50, min(2000, int(2e5 / max(ms * 1e3, 1.0))))
+    st_us = {}
+    for st in moe.MoELayer.STAGES:
+        for i in range(5):
+            layer.replay(layers[i % args.layers], st)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(reps):
+            layer.replay(layers[i % args.layers], st)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        st_us[st] = 1e3 * e0.elapsed_time(e1) / reps
+    # stages without kernels on this path time as the empty-launch floor;
+    # report them as 0
+    path = layer.last_path
+    if path != 0:
+        for st in ("route", "scan", "combine"):
+            st_us[st] = 0.0
     dom = "gateup" if st_us["gateup"] >= st_us["down"] else "down"
     prefill = T >= 256
     if prefill:
@@ -196,6 +240,10 @@ def main():
         roof = {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": ach / HBM_PEAK_GBS, "traffic": None, "kernel": dom,
                 "kernel_us": st_us[dom], "bytes_per_launch": by}
+    roof["traffic"] = measured_traffic(args.config, dom)
+    # the forward once more, so `out` holds a real result again
+    step(0)
+    torch.cuda.synchronize()
 
     layer_bytes = (U + (1 if shared else 0)) * EXPERT_BYTES + T * (D * 4 + E * 4 + D * 2)
     res = {
@@ -216,7 +264,7 @@ def main():
                    "top_k": K, "d_ff": FF, "shared_expert": shared,
                    "weight_layers_rotated": args.layers},
         "layer_hbm_fraction": layer_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
-        "distinct_experts_avg": U,
+        "distinct_experts": U,
         "stage_us": st_us,
         "roofline": roof,
     }

@@ -153,6 +153,14 @@ int q36moe_ctx_stage_times(q36moe_ctx *c, double *ms, int *calls, int n_stages, 
 const char *q36moe_stage_name(int stage);
 int q36moe_num_stages(void);
 
+/* Launch again, on the context stream and without synchronising, the
+ * kernels of one stage of the last forward (same inputs, tokens and path)
+ * with the weights w.  Bracketing many replays over rotating weight sets
+ * with two events gives a kernel's average duration without per-launch
+ * event overhead.  The stage's outputs are rewritten; call forward again
+ * before reading results.  No counterpart in the reference (profiling aid). */
+int q36moe_ctx_replay(q36moe_ctx *c, const q36moe_weights *w, int stage);
+
 /* One v_mfma_scale_f32_16x16x128_f8f6f4 on caller-packed operands:
  * a, b: 64 lanes x 32 bytes; sa, sb: 64 lane scale dwords (byte 0 used);
  * fmt_a / fmt_b: 0 e4m3, 1 e5m2, 2 e2m3, 3 e3m2, 4 e2m1; c: 64 x 4 floats. */

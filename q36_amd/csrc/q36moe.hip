@@ -875,13 +875,19 @@ __global__ __launch_bounds__(kGT) void k_grouped(GemmArgs A) {
     static_assert(MODE != MODE_GATEUP || RT % 2 == 0, "h blocks of 32 rows");
     __shared__ LT L;
 
-    const int ti = blockIdx.x;
+    // XCD-major order: workgroups are dealt to the 8 XCDs round-robin
+    // (linear id % 8), so the j-th workgroup of XCD x takes row block
+    // j % NRB of tile 8 * (j / NRB) + x: the row blocks of one tile run
+    // back to back on one XCD and share its L2 copy of the tile's B rows.
+    constexpr int NRB = (MODE == MODE_GATEUP ? 512 : 2048) / (16 * RT);
+    const int xcd = blockIdx.x & 7, jx = blockIdx.x >> 3;
+    const int ti = 8 * (jx / NRB) + xcd;
+    const int mt0 = (jx % NRB) * RT;
     if (ti >= *A.ntiles) return;
     Q36_TRACE_WG(0);
     const int4 tile = A.tiles[ti];
     const int e = tile.x, p0 = tile.y, p1 = tile.z;
     const int tid = threadIdx.x, wave = tid >> 6;
-    const int mt0 = blockIdx.y * RT;
     const size_t nib_bytes = (size_t)A.M * KD / 2;
     const uint8_t *W0 = e < A.E ? A.wa + (size_t)e * A.wstride : A.sa;
     const uint8_t *W1 = W0;
@@ -1381,6 +1387,17 @@ struct q36moe_weights {
     void *base;                      // single device allocation
 };
 
+// Kernel arguments of the last forward; the weights are bound per launch so
+// a stage can be replayed over other weight sets (q36moe_ctx_replay).
+struct Plan {
+    int T, has_sh, direct, mode3, tiles, nb;
+    RouteArgs ra;
+    ScanArgs sa;
+    GemmArgs ga, da;
+    DirectArgs di;
+    const void *out; int out_fmt;
+};
+
 struct q36moe_ctx {
     int dev;
     hipStream_t stream;
@@ -1400,9 +1417,11 @@ struct q36moe_ctx {
     int path_mode;                  // 0 auto, 1 sorted, 2 direct
     int last_T, last_sh, last_path;
     int timing;
+    Plan *plan;                     // kernel arguments of the last forward
     hipEvent_t ev[ST_COUNT + 1];
     double ms[ST_COUNT];
     int calls[ST_COUNT];
+    ~q36moe_ctx() { delete plan; }
 };
 
 namespace {
@@ -1541,6 +1560,11 @@ int q36moe_ctx_create(int max_tokens, int n_expert, int d_model, int d_ff, int t
         return Q36MOE_EINVAL;
     q36moe_ctx *c = new (std::nothrow) q36moe_ctx();
     if (!c) return Q36MOE_ENOMEM;
+    c->plan = new (std::nothrow) Plan();
+    if (!c->plan) {
+        delete c;
+        return Q36MOE_ENOMEM;
+    }
     if (hipGetDevice(&c->dev) != hipSuccess) {
         delete c;
         return Q36MOE_EHIP;
@@ -1619,6 +1643,68 @@ void q36moe_ctx_free(q36moe_ctx *c) {
     delete c;
 }
 
+static void bind_weights(Plan &P, const q36moe_weights *w) {
+    P.ga.wa = w->gate; P.ga.wb = w->up; P.ga.sa = w->sh_gate; P.ga.sb = w->sh_up;
+    P.ga.wstride = w->gu_bytes;
+    P.da.wa = w->down; P.da.wb = nullptr; P.da.sa = w->sh_down; P.da.sb = nullptr;
+    P.da.wstride = w->dn_bytes;
+    P.di.gate = w->gate; P.di.up = w->up; P.di.down = w->down;
+    P.di.sh_gate = w->sh_gate; P.di.sh_up = w->sh_up; P.di.sh_down = P.has_sh ? w->sh_down : nullptr;
+    P.di.wstride = w->gu_bytes;
+}
+
+// Launches the kernels of one stage (direct path: ST_GATEUP is the routing +
+// gate/up kernel, ST_DOWN the down + combine kernel; its other stages are
+// empty).
+static void launch_stage(const q36moe_ctx *c, const Plan &P, int st, hipStream_t s) {
+    const int T = P.T, K = c->K, D = c->D, FF = c->FF;
+    if (P.direct) {
+        const int n = T * K + (P.has_sh ? T : 0);
+        if (P.mode3) {
+            if (st == ST_GATEUP)
+                hipLaunchKernelGGL(k_decode_fused, dim3(P.di.n_gateup_wg + T * (D / 16)), dim3(256), 0, s, P.di);
+        } else if (st == ST_GATEUP) {
+            hipLaunchKernelGGL(k_direct_gateup, dim3(n, FF / 16), dim3(256), 0, s, P.di);
+        } else if (st == ST_DOWN) {
+            hipLaunchKernelGGL(k_direct_down, dim3(D / 16, T), dim3(64 * (K + P.has_sh)), 0, s, P.di);
+        }
+        return;
+    }
+    switch (st) {
+        case ST_ROUTE:
+            hipLaunchKernelGGL(k_route, dim3(P.nb), dim3(kRouteThreads), 0, s, P.ra);
+            break;
+        case ST_SCAN:
+            hipLaunchKernelGGL(k_colscan, dim3((c->E + kColExp - 1) / kColExp), dim3(256), 0, s, P.sa);
+            hipLaunchKernelGGL(k_scatter, dim3(P.nb), dim3(256), 0, s, P.sa);
+            break;
+        case ST_GATEUP:
+            hipLaunchKernelGGL((k_grouped<MODE_GATEUP, kGuRT, 2048, kGuBR>),
+                               dim3(P.tiles * (FF / (16 * kGuRT))), dim3(kGT), 0, s, P.ga);
+            break;
+        case ST_DOWN:
+            hipLaunchKernelGGL((k_grouped<MODE_DOWN, kDnRT, 512, kDnBR>),
+                               dim3(P.tiles * (D / (16 * kDnRT))), dim3(kGT), 0, s, P.da);
+            break;
+        case ST_COMBINE:
+            hipLaunchKernelGGL(k_combine, dim3(T), dim3(256), 0, s, c->dnw, c->pos, T, K, D, P.has_sh,
+                               const_cast<void *>(P.out), P.out_fmt);
+            break;
+        default: break;
+    }
+}
+
+int q36moe_ctx_replay(q36moe_ctx *c, const q36moe_weights *w, int stage) {
+    if (!c || !w || stage < 0 || stage >= ST_COUNT) return Q36MOE_EINVAL;
+    if (c->last_T <= 0) return Q36MOE_EINVAL;
+    if (w->E != c->E || w->D != c->D || w->FF != c->FF) return Q36MOE_EINVAL;
+    if (c->plan->has_sh && !w->sh_gate) return Q36MOE_EINVAL;
+    Plan P = *c->plan;
+    bind_weights(P, w);
+    launch_stage(c, P, stage, c->stream);
+    return hipGetLastError() == hipSuccess ? Q36MOE_OK : Q36MOE_EHIP;
+}
+
 int q36moe_forward(q36moe_ctx *c, const q36moe_weights *w, const void *x, int x_fmt,
                    const float *logits, int ld_logits, const float *shg, int T, float scale,
                    void *out, int out_fmt) {
@@ -1638,70 +1724,46 @@ int q36moe_forward(q36moe_ctx *c, const q36moe_weights *w, const void *x, int x_
     const int nb = (T + kRouteTPB - 1) / kRouteTPB;
     const int tn = kTileTok;
     int tiles = n / tn + (n < E ? n : E) + (has_sh ? (T + tn - 1) / tn : 0);
-    tiles = (tiles + 7) & ~7;
+    tiles = (tiles + 7) & ~7;   // whole groups of 8 for the XCD-major tile order
     hipStream_t s = c->stream;
-    auto mark = [&](int st) {
-        if (c->timing) (void)hipEventRecord(c->ev[st], s);
-    };
 
     const bool direct = (c->path_mode == 2 || c->path_mode == 3) ? (T <= kDirectMaxT)
                         : c->path_mode == 1 ? false : (T <= kDirectMaxT);
     if ((c->path_mode == 2 || c->path_mode == 3) && !direct) return Q36MOE_EINVAL;
+
+    Plan &P = *c->plan;
+    P = Plan{};
+    P.T = T; P.has_sh = has_sh; P.direct = direct; P.mode3 = c->path_mode == 3;
+    P.tiles = tiles; P.nb = nb; P.out = out; P.out_fmt = out_fmt;
     if (direct) {
         const int ngu = (n + (has_sh ? T : 0)) * (FF / 16);
-        DirectArgs da{logits, ld_logits, T, E, K, scale, x, x_fmt, shg,
-                      w->gate, w->up, w->down, w->sh_gate, w->sh_up, has_sh ? w->sh_down : nullptr,
-                      w->gu_bytes, c->topk_idx, c->topk_w, c->pos, c->perm, c->xq, c->xs, c->hf,
-                      c->hq, c->hs, out, out_fmt, c->sync, c->sync + kDirectMaxT,
-                      c->sync + 2 * kDirectMaxT, ngu};
-        mark(ST_ROUTE);
-        mark(ST_SCAN);
-        mark(ST_GATEUP);
-        if (c->path_mode != 3) {
-            hipLaunchKernelGGL(k_direct_gateup, dim3(n + (has_sh ? T : 0), FF / 16), dim3(256), 0, s, da);
-            mark(ST_DOWN);
-            hipLaunchKernelGGL(k_direct_down, dim3(D / 16, T), dim3(64 * (K + has_sh)), 0, s, da);
-        } else {
-            hipLaunchKernelGGL(k_decode_fused, dim3(ngu + T * (D / 16)), dim3(256), 0, s, da);
-            mark(ST_DOWN);
-        }
-        mark(ST_COMBINE);
-        mark(ST_COUNT);
+        P.di = DirectArgs{logits, ld_logits, T, E, K, scale, x, x_fmt, shg,
+                          nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0,
+                          c->topk_idx, c->topk_w, c->pos, c->perm, c->xq, c->xs, c->hf,
+                          c->hq, c->hs, out, out_fmt, c->sync, c->sync + kDirectMaxT,
+                          c->sync + 2 * kDirectMaxT, ngu};
     } else {
-    mark(ST_ROUTE);
-    RouteArgs ra{logits, ld_logits, T, E, K, scale, x, x_fmt, D, nb,
-                 c->topk_idx, c->topk_w, c->xq, c->xs, c->xs2, c->blk_cnt, c->rank};
-    hipLaunchKernelGGL(k_route, dim3(nb), dim3(kRouteThreads), 0, s, ra);
-
-    mark(ST_SCAN);
-    ScanArgs sa{c->blk_cnt, nb, E, T, K, c->topk_idx, c->topk_w, c->rank, shg, tn,
-                c->blk_off, c->tot, c->e_off, c->perm, c->pos, c->row_tok, c->row_w, c->tiles, c->ntiles};
-    hipLaunchKernelGGL(k_colscan, dim3((E + kColExp - 1) / kColExp), dim3(256), 0, s, sa);
-    hipLaunchKernelGGL(k_scatter, dim3(nb), dim3(256), 0, s, sa);
-
-    mark(ST_GATEUP);
-    GemmArgs ga{};
-    ga.wa = w->gate; ga.wb = w->up; ga.sa = w->sh_gate; ga.sb = w->sh_up;
-    ga.wstride = w->gu_bytes; ga.E = E; ga.M = FF;
-    ga.tiles = c->tiles; ga.ntiles = c->ntiles;
-    ga.bq = c->xq; ga.bs2 = c->xs2; ga.row_tok = c->row_tok; ga.row_w = c->row_w;
-    ga.hq = c->hq; ga.hs = c->hs; ga.hs2 = c->hs2; ga.ldo = FF;
-    GemmArgs da = ga;
-    da.wa = w->down; da.wb = nullptr; da.sa = w->sh_down; da.sb = nullptr;
-    da.wstride = w->dn_bytes; da.M = D;
-    da.bq = c->hq; da.bs2 = c->hs2; da.dnw = c->dnw; da.ldo = D;
-    hipLaunchKernelGGL((k_grouped<MODE_GATEUP, kGuRT, 2048, kGuBR>), dim3(tiles, FF / (16 * kGuRT)),
-                       dim3(kGT), 0, s, ga);
-
-    mark(ST_DOWN);
-    hipLaunchKernelGGL((k_grouped<MODE_DOWN, kDnRT, 512, kDnBR>), dim3(tiles, D / (16 * kDnRT)),
-                       dim3(kGT), 0, s, da);
-
-    mark(ST_COMBINE);
-    hipLaunchKernelGGL(k_combine, dim3(T), dim3(256), 0, s, c->dnw, c->pos, T, K, D, has_sh, out,
-                       out_fmt);
-    mark(ST_COUNT);
+        P.ra = RouteArgs{logits, ld_logits, T, E, K, scale, x, x_fmt, D, nb,
+                         c->topk_idx, c->topk_w, c->xq, c->xs, c->xs2, c->blk_cnt, c->rank};
+        P.sa = ScanArgs{c->blk_cnt, nb, E, T, K, c->topk_idx, c->topk_w, c->rank, shg, tn,
+                        c->blk_off, c->tot, c->e_off, c->perm, c->pos, c->row_tok, c->row_w, c->tiles,
+                        c->ntiles};
+        GemmArgs &ga = P.ga;
+        ga.E = E; ga.M = FF;
+        ga.tiles = c->tiles; ga.ntiles = c->ntiles;
+        ga.bq = c->xq; ga.bs2 = c->xs2; ga.row_tok = c->row_tok; ga.row_w = c->row_w;
+        ga.hq = c->hq; ga.hs = c->hs; ga.hs2 = c->hs2; ga.ldo = FF;
+        GemmArgs &da = P.da;
+        da = ga;
+        da.M = D;
+        da.bq = c->hq; da.bs2 = c->hs2; da.dnw = c->dnw; da.ldo = D;
     }
+    bind_weights(P, w);
+    for (int st = 0; st < ST_COUNT; st++) {
+        if (c->timing) (void)hipEventRecord(c->ev[st], s);
+        launch_stage(c, P, st, s);
+    }
+    if (c->timing) (void)hipEventRecord(c->ev[ST_COUNT], s);
     c->last_T = T;
     c->last_sh = has_sh;
     c->last_path = direct ? 1 : 0;

@@ -69,6 +69,7 @@ def lib():
     L.q36moe_stage_name.restype = ctypes.c_char_p
     L.q36moe_num_stages.argtypes = []
     L.q36moe_probe_mfma.argtypes = [vp, vp, vp, vp, i, i, vp, vp]
+    L.q36moe_ctx_replay.argtypes = [vp, vp, i]
     _lib = L
     return L
 
@@ -287,6 +288,14 @@ class MoELayer:
         check(lib().q36moe_ctx_stage_times(self._h, ms, calls, n, 1 if reset else 0),
               "q36moe_ctx_stage_times")
         return {lib().q36moe_stage_name(i).decode(): (ms[i], calls[i]) for i in range(n)}
+
+    STAGES = ("route", "scan", "gateup", "down", "combine")
+
+    def replay(self, weights, stage):
+        """Launch the kernels of one stage of the last forward again with
+        `weights` (asynchronous, on the layer's stream)."""
+        st = self.STAGES.index(stage) if isinstance(stage, str) else int(stage)
+        check(lib().q36moe_ctx_replay(self._h, weights._h, st), "q36moe_ctx_replay")
 
     def free(self):
         if self._h:
