@@ -222,7 +222,7 @@ def main():
     # stages without kernels on this path time as the empty-launch floor;
     # report them as 0
     path = layer.last_path
-    if path != 0:
+    if path == 1:
         for st in ("route", "scan", "combine"):
             st_us[st] = 0.0
     dom = "gateup" if st_us["gateup"] >= st_us["down"] else "down"

@@ -123,15 +123,19 @@ int q36moe_quant_e4m3(const void *x, int x_fmt, int T, int K,
                       uint8_t *xq, uint8_t *xs, void *stream);
 
 /* Execution path of q36moe_forward.  The sorted path (route + sort + grouped
- * expert GEMMs + combine) serves any T; the direct path (no sort, slots
- * combined in registers) serves T <= 16 as two kernels (gate/up, then down),
- * or as one kernel whose down-role workgroups wait on per-token counters
- * (mode 3; measured slower on MI355X: each device-scope poll is a memory
- * round trip).  mode 0 picks the two-kernel direct path for T <= 16, 1
- * forces sorted, 2 forces direct, 3 forces the one-kernel direct path
- * (EINVAL from forward when T > 16 in modes 2/3).  last_path: 0 sorted, 1
- * direct.  With the direct path the PERM/POS taps are the identity (rows in
- * entry order) and the EOFF/DNW taps are unavailable. */
+ * expert GEMMs + combine) serves any T, with fat tiles (up to 256 rows per
+ * expert tile, weights staged through LDS) or skinny tiles (up to 32 rows,
+ * weights streamed straight into registers); the direct path (no sort,
+ * slots combined in registers) serves T <= 16 as two kernels (gate/up, then
+ * down), or as one kernel whose down-role workgroups wait on per-token
+ * counters (mode 3; measured slower on MI355X: each device-scope poll is a
+ * memory round trip).  mode 0 picks the two-kernel direct path for T <= 16,
+ * skinny tiles while T*k <= 8*n_expert and fat tiles above; 1 forces sorted
+ * with fat tiles, 4 sorted with skinny tiles, 2 direct, 3 the one-kernel
+ * direct path (EINVAL from forward when T > 16 in modes 2/3).  last_path:
+ * 0 sorted (fat), 1 direct, 2 sorted (skinny).  With the direct path the
+ * PERM/POS taps are the identity (rows in entry order) and the EOFF/DNW taps
+ * are unavailable. */
 int q36moe_ctx_set_path(q36moe_ctx *c, int mode);
 int q36moe_ctx_last_path(const q36moe_ctx *c);
 

@@ -29,6 +29,7 @@
 #include "q36moe.h"
 
 typedef int v8i __attribute__((ext_vector_type(8)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 #ifdef Q36MOE_TRACE
 __device__ unsigned long long g_q36_trace[64];
@@ -118,7 +119,11 @@ __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
     return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
 }
 
-__device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
+// g * sigmoid(g) on the hardware exp2 and reciprocal (about 2 ulp; h is
+// quantised to e4m3 right after, whose step is 2^-3 relative)
+__device__ __forceinline__ float silu(float g) {
+    return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * 1.44269504088896341f));
+}
 
 // v_mfma_scale_f32_16x16x128_f8f6f4, A = E2M1 (cbsz 4), B = E4M3 (blgp 0).
 // Operand layout on gfx950 (measured with q36moe_probe_mfma):
@@ -611,7 +616,10 @@ struct GemmArgs {
     int ldo;                  // output row length
 };
 
-constexpr int kTileTok = 256;
+#ifndef Q36_TILE_TOK
+#define Q36_TILE_TOK 256
+#endif
+constexpr int kTileTok = Q36_TILE_TOK;
 
 // tile shapes of the grouped GEMMs: row tiles of 16 per workgroup (per
 // matrix) and the depth of the register ring for B (K-steps)
@@ -641,7 +649,10 @@ __device__ __forceinline__ v4f mfma_sel(int sel, const v8i &a, const v8i &b, con
     }
 }
 
-constexpr int kGW = 8;                 // waves per grouped-GEMM workgroup
+#ifndef Q36_GW
+#define Q36_GW 8
+#endif
+constexpr int kGW = Q36_GW;            // waves per grouped-GEMM workgroup
 constexpr int kGT = 64 * kGW;          // threads
 
 template <int MODE, int RT, int KD>
@@ -650,11 +661,14 @@ struct GroupedLds {
     static constexpr int NAT = NMAT * RT;
     static constexpr int NKT = KD / 128;
     __align__(16) uint8_t a[2][NAT * 1024];
-    __align__(16) uint32_t sc[NAT][64][NKT / 4];
+    __align__(16) uint32_t sc[NAT][NKT / 4][64];   // lane-contiguous: conflict-free reads
     int row[kTileTok];
 };
 
-constexpr int kRA = 4;   // depth of the register ring that carries A from HBM to LDS
+#ifndef Q36_RA
+#define Q36_RA 4
+#endif
+constexpr int kRA = Q36_RA;   // depth of the register ring that carries A from HBM to LDS
 
 // NJ = number of 16-token tiles this wave owns (tiles wave, wave+kGW).
 // Pipeline per K-step kt (all rings indexed by compile-time slots: the K
@@ -679,7 +693,7 @@ __device__ __forceinline__ void grouped_body(const GemmArgs &A, GroupedLds<MODE,
     constexpr int APT = NAT * 1024 / kGT / 16;   // 16-byte A chunks per thread per K-step
     constexpr int NJ1 = NJ > 0 ? NJ : 1;
     constexpr int NG = NKT / 4;                  // groups of 4 K-steps
-    static_assert(NKT % 4 == 0 && BR >= 2 && kRA == 4, "rings");
+    static_assert(NKT % 4 == 0 && BR >= 2 && kRA >= 2, "rings");
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int q = lane >> 4;
 
@@ -709,101 +723,124 @@ __device__ __forceinline__ void grouped_body(const GemmArgs &A, GroupedLds<MODE,
 #pragma unroll
         for (int j = 0; j < NJ; j++) acc[a][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
-    // rings as shift registers (fixed names, no ring indexing):
-    //   B: bq[0] = step kt, ..., bq[BR-2] = step kt+BR-2
-    //   A: ra1/ra2/ra3 = steps kt+1, kt+2, kt+3
-    uint4 bq[BR - 1][NJ1][2];
-    uint32_t bsd[NJ1], bsn[NJ1];   // B scale dwords of this group and the next
-    uint4 ra1[APT], ra2[APT], ra3[APT];
+    // Rings indexed by the (compile-time) K-step, so no register is copied
+    // between steps: a VALU write into a register that an in-flight MFMA
+    // still reads (operand or scale) stalls the wave until that MFMA is done.
+    //   B rows of step k:      bq[k % NB]     (loaded NB-1 steps ahead)
+    //   A slices of step k:    ra[k % NR]     (loaded NR-1 steps ahead, then
+    //                                          written to LDS one step ahead)
+    //   A fragments of step k: fx[k & 1]      (read from LDS one step ahead)
+    //   scale dwords:          all groups held from the start
+    constexpr int NB = BR - 1 + 1, NR = kRA;
+    u32x4 bq[NB][NJ1][2];
+    u32x4 ra[NR][APT];
+    u32x4 fx[2][NAT];
+    uint32_t scA[NG][NAT];     // A scale dwords per group of 4 K-steps
+    uint32_t scB[NG][NJ1];     // B scale dwords per group
 #pragma unroll
-    for (int r = 0; r < BR - 1; r++)
+    for (int g = 0; g < NG; g++) {
+#pragma unroll
+        for (int a = 0; a < NAT; a++) scA[g][a] = L.sc[a][g][lane];
+#pragma unroll
+        for (int j = 0; j < NJ; j++) scB[g][j] = bsp[j][g];
+    }
+    static_for<0, NB - 1>([&](auto R) {
+        constexpr int r = decltype(R)::value;
 #pragma unroll
         for (int j = 0; j < NJ; j++) {
-            bq[r][j][0] = *reinterpret_cast<const uint4 *>(brp[j] + r * 128);
-            bq[r][j][1] = *reinterpret_cast<const uint4 *>(brp[j] + r * 128 + 64);
+            bq[r][j][0] = *reinterpret_cast<const u32x4 *>(brp[j] + min(r, NKT - 1) * 128);
+            bq[r][j][1] = *reinterpret_cast<const u32x4 *>(brp[j] + min(r, NKT - 1) * 128 + 64);
         }
+    });
+    static_for<1, NR>([&](auto R) {
+        constexpr int r = decltype(R)::value;
 #pragma unroll
-    for (int j = 0; j < NJ; j++) bsd[j] = bsp[j][0];
+        for (int u = 0; u < APT; u++)
+            ra[r][u] = *reinterpret_cast<const u32x4 *>(asrc[u] + (size_t)min(r, NKT - 1) * 1024);
+    });
 #pragma unroll
-    for (int u = 0; u < APT; u++) {
-        ra1[u] = *reinterpret_cast<const uint4 *>(asrc[u] + (size_t)min(1, NKT - 1) * 1024);
-        ra2[u] = *reinterpret_cast<const uint4 *>(asrc[u] + (size_t)min(2, NKT - 1) * 1024);
-        ra3[u] = *reinterpret_cast<const uint4 *>(asrc[u] + (size_t)min(3, NKT - 1) * 1024);
-    }
+    for (int a = 0; a < NAT; a++) fx[0][a] = *reinterpret_cast<const u32x4 *>(&L.a[0][a * 1024 + lane * 16]);
 
-#pragma unroll
-    for (int kg = 0; kg < NG; kg++) {
-#pragma unroll
-        for (int ks = 0; ks < 4; ks++) {
-            const int kt = kg * 4 + ks;
-            // 1. B of step kt+BR-1 (and the next group's scale dwords)
-            const int kb = min(kt + BR - 1, NKT - 1);
-            uint4 bl[NJ1][2];
+    // the K loop is instantiated per step (static_for), so every ring index
+    // is a constant when the arrays are scalarised
+    static_for<0, NKT>([&](auto KT) {
+        constexpr int kt = decltype(KT)::value;
+        constexpr int ks = kt & 3, kg = kt >> 2;
+        if (MODE == MODE_GATEUP && wave == 0) Q36_TRACE_AT(30 + kt);
+        // 1. B rows of step kt+NB-1
+        if constexpr (kt + NB - 1 < NKT) {
 #pragma unroll
             for (int j = 0; j < NJ; j++) {
-                bl[j][0] = *reinterpret_cast<const uint4 *>(brp[j] + kb * 128);
-                bl[j][1] = *reinterpret_cast<const uint4 *>(brp[j] + kb * 128 + 64);
+#ifdef Q36_EXP_NOB
+                bq[(kt + NB - 1) % NB][j][0] = bq[kt % NB][j][1];
+                bq[(kt + NB - 1) % NB][j][1] = bq[kt % NB][j][0];
+#else
+                bq[(kt + NB - 1) % NB][j][0] = *reinterpret_cast<const u32x4 *>(brp[j] + (kt + NB - 1) * 128);
+                bq[(kt + NB - 1) % NB][j][1] = *reinterpret_cast<const u32x4 *>(brp[j] + (kt + NB - 1) * 128 + 64);
+#endif
             }
-            if (ks == 0) {
-#pragma unroll
-                for (int j = 0; j < NJ; j++) bsn[j] = bsp[j][min(kg + 1, NG - 1)];
-            }
-            // 2. A of step kt+4
-            uint4 an[APT];
+        }
+        // 2. A slices of step kt+NR
+        if constexpr (kt + NR < NKT) {
 #pragma unroll
             for (int u = 0; u < APT; u++)
-                an[u] = *reinterpret_cast<const uint4 *>(asrc[u] + (size_t)min(kt + kRA, NKT - 1) * 1024);
-            // 3. MFMAs of step kt
-            v8i bv[NJ1];
+#ifdef Q36_EXP_NOA
+                ra[(kt + NR) % NR][u] = ra[(kt + 1) % NR][u];
+#else
+                ra[(kt + NR) % NR][u] = *reinterpret_cast<const u32x4 *>(asrc[u] + (size_t)(kt + NR) * 1024);
+#endif
+        }
+        // 3. A of step kt+1 into the other LDS slot (its last readers,
+        //    the fragment loads of step kt-1, finished before barrier kt-1)
+        if constexpr (kt + 1 < NKT) {
 #pragma unroll
-            for (int j = 0; j < NJ; j++)
-                bv[j] = v8i{(int)bq[0][j][0].x, (int)bq[0][j][0].y, (int)bq[0][j][0].z, (int)bq[0][j][0].w,
-                            (int)bq[0][j][1].x, (int)bq[0][j][1].y, (int)bq[0][j][1].z, (int)bq[0][j][1].w};
-#pragma unroll
-            for (int a = 0; a < NAT; a++) {
-                if (NJ == 0) break;
-                const uint4 av = *reinterpret_cast<const uint4 *>(&L.a[ks & 1][a * 1024 + lane * 16]);
-                const v8i afr = v8i{(int)av.x, (int)av.y, (int)av.z, (int)av.w, 0, 0, 0, 0};
-                const int sav = (int)L.sc[a][lane][kg];
-#pragma unroll
-                for (int j = 0; j < NJ; j++)
-                    acc[a][j] = mfma_sel(ks, afr, bv[j], acc[a][j], sav, (int)bsd[j]);
-            }
-            // pin this step's MFMAs here: without a use they sink to the
-            // epilogue and keep every step's operands live at once
+            for (int u = 0; u < APT; u++)
+                *reinterpret_cast<u32x4 *>(&L.a[(kt + 1) & 1][(tid + kGT * u) * 16]) = ra[(kt + 1) % NR][u];
+        }
+        // pin the previous step's MFMAs here: without a use they sink to the
+        // epilogue and keep every step's operands live at once; pinning one
+        // step late lets them overlap this step's loads and LDS write
+#ifndef Q36_NO_PIN
+        if constexpr (kt > 0) {
 #pragma unroll
             for (int a = 0; a < NAT; a++)
 #pragma unroll
                 for (int j = 0; j < NJ; j++) asm volatile("" : "+v"(acc[a][j]));
-            // 4. A of step kt+1 into the other LDS slot
-#pragma unroll
-            for (int u = 0; u < APT; u++)
-                *reinterpret_cast<uint4 *>(&L.a[(ks + 1) & 1][(tid + kGT * u) * 16]) = ra1[u];
-            // 5. shift the rings
-#pragma unroll
-            for (int u = 0; u < APT; u++) {
-                ra1[u] = ra2[u];
-                ra2[u] = ra3[u];
-                ra3[u] = an[u];
-            }
-#pragma unroll
-            for (int r = 0; r + 1 < BR - 1; r++)
-#pragma unroll
-                for (int j = 0; j < NJ; j++) {
-                    bq[r][j][0] = bq[r + 1][j][0];
-                    bq[r][j][1] = bq[r + 1][j][1];
-                }
-#pragma unroll
-            for (int j = 0; j < NJ; j++) {
-                bq[BR - 2][j][0] = bl[j][0];
-                bq[BR - 2][j][1] = bl[j][1];
-            }
-            lds_barrier();
-            __builtin_amdgcn_sched_barrier(0);   // keep the next step's LDS reads after the barrier
         }
+#endif
+        // 4. MFMAs of step kt, first half
+        v8i bv[NJ1];
 #pragma unroll
-        for (int j = 0; j < NJ; j++) bsd[j] = bsn[j];
-    }
+        for (int j = 0; j < NJ; j++) {
+            const u32x4 b0 = bq[kt % NB][j][0], b1 = bq[kt % NB][j][1];
+            bv[j] = v8i{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
+        }
+        auto mfmas = [&](int a0, int a1) {
+#pragma unroll
+            for (int a = a0; a < a1; a++) {
+                const u32x4 f = fx[kt & 1][a];
+                const v8i afr = v8i{(int)f[0], (int)f[1], (int)f[2], (int)f[3], 0, 0, 0, 0};
+#pragma unroll
+                for (int j = 0; j < NJ; j++)
+                    acc[a][j] = mfma_sel(ks, afr, bv[j], acc[a][j], (int)scA[kg][a], (int)scB[kg][j]);
+            }
+        };
+        mfmas(0, NAT / 2);
+        // 5. barrier: step kt+1's A slot is complete
+        if constexpr (kt + 1 < NKT) {
+#ifndef Q36_EXP_NOBAR
+            lds_barrier();
+#endif
+            __builtin_amdgcn_sched_barrier(0);
+            // 6. step kt+1's A fragments
+#pragma unroll
+            for (int a = 0; a < NAT; a++)
+                fx[(kt + 1) & 1][a] = *reinterpret_cast<const u32x4 *>(&L.a[(kt + 1) & 1][a * 1024 + lane * 16]);
+            __builtin_amdgcn_sched_barrier(0);   // issue those reads before the second half
+        }
+        // 7. second half
+        mfmas(NAT / 2, NAT);
+    });
 
     if constexpr (MODE == MODE_GATEUP) {
 #pragma unroll
@@ -885,6 +922,7 @@ __global__ __launch_bounds__(kGT) void k_grouped(GemmArgs A) {
     const int mt0 = (jx % NRB) * RT;
     if (ti >= *A.ntiles) return;
     Q36_TRACE_WG(0);
+    if (MODE == MODE_GATEUP) Q36_TRACE_AT(28);
     const int4 tile = A.tiles[ti];
     const int e = tile.x, p0 = tile.y, p1 = tile.z;
     const int tid = threadIdx.x, wave = tid >> 6;
@@ -893,14 +931,21 @@ __global__ __launch_bounds__(kGT) void k_grouped(GemmArgs A) {
     const uint8_t *W1 = W0;
     if constexpr (LT::NMAT == 2) W1 = e < A.E ? A.wb + (size_t)e * A.wstride : A.sb;
 
-    // A scales for all K of this row block (contiguous per matrix)
+    // A scales for all K of this row block: per matrix a contiguous
+    // [row tile][lane][K/128] byte block, stored transposed as
+    // sc[tile][group of 4 K-steps][lane]
     {
-        constexpr int SB = RT * 64 * NKT;
-        for (int c = tid; c < LT::NMAT * SB / 16; c += kGT) {
-            const int m = c / (SB / 16), o = (c % (SB / 16)) * 16;
-            const uint8_t *src = (m == 0 ? W0 : W1) + nib_bytes + (size_t)mt0 * 64 * NKT + o;
-            *reinterpret_cast<uint4 *>(reinterpret_cast<uint8_t *>(&L.sc[m * RT][0][0]) + o) =
-                *reinterpret_cast<const uint4 *>(src);
+        constexpr int G = NKT / 4, SBD = RT * 64 * G;   // dwords per matrix
+        for (int c = tid; c < LT::NMAT * SBD / 4; c += kGT) {
+            const int m = c / (SBD / 4), d0 = (c % (SBD / 4)) * 4;
+            const uint4 v = *reinterpret_cast<const uint4 *>((m == 0 ? W0 : W1) + nib_bytes +
+                                                             (size_t)mt0 * 64 * NKT + (size_t)d0 * 4);
+            const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int d = d0 + u, at = d / (64 * G), ln = (d / G) % 64, g = d % G;
+                L.sc[m * RT + at][g][ln] = vv[u];
+            }
         }
     }
     for (int i = tid; i < kTileTok; i += kGT) {
@@ -920,15 +965,212 @@ __global__ __launch_bounds__(kGT) void k_grouped(GemmArgs A) {
         }
     }
     __syncthreads();
+    if (MODE == MODE_GATEUP) Q36_TRACE_AT(29);
     const int ntt = (p1 - p0 + 15) >> 4;
-    static_assert(kTileTok == 16 * kGW * 2, "two token tiles per wave");
+    static_assert(kTileTok % (16 * kGW) == 0 && kTileTok <= 4 * 16 * kGW, "1..4 token tiles per wave");
     const int nj = ntt > wave ? (ntt - wave + kGW - 1) / kGW : 0;
+    constexpr int NJMAX = kTileTok / (16 * kGW);
     switch (nj) {
         case 0: grouped_body<MODE, RT, KD, BR, 0>(A, L, W0, W1, mt0, p0, p1); break;
         case 1: grouped_body<MODE, RT, KD, BR, 1>(A, L, W0, W1, mt0, p0, p1); break;
-        default: grouped_body<MODE, RT, KD, BR, 2>(A, L, W0, W1, mt0, p0, p1); break;
+        case 2:
+            if constexpr (NJMAX >= 2) grouped_body<MODE, RT, KD, BR, 2>(A, L, W0, W1, mt0, p0, p1);
+            break;
+        case 3:
+            if constexpr (NJMAX >= 3) grouped_body<MODE, RT, KD, BR, 3>(A, L, W0, W1, mt0, p0, p1);
+            break;
+        default:
+            if constexpr (NJMAX >= 4) grouped_body<MODE, RT, KD, BR, 4>(A, L, W0, W1, mt0, p0, p1);
+            break;
     }
+    if (MODE == MODE_GATEUP) Q36_TRACE_AT(46);
     Q36_TRACE_WG(1);
+}
+
+// ---------------------------------------------------------------------------
+// skinny grouped GEMMs: tiles of at most 32 rows (few rows per expert)
+// ---------------------------------------------------------------------------
+// With a handful of rows per expert the grouped GEMM is a weight stream.
+// These kernels keep every wave's A (E2M1 fragments) in its own registers,
+// loaded all at once straight from HBM: no LDS staging of A and, for down, no
+// barrier at all.  B rows (e4m3) come from L2 into registers.
+//   GATEUP: workgroup = (tile, 32-row block of gate and up); the 8 waves split
+//           K into 8 x 256, partial sums meet in LDS in wave order, then
+//           SwiGLU and the per-32 quantisation of h (one block per row).
+//   DOWN:   workgroup = (tile, 128 output rows); wave w owns row tile w with
+//           all of K = 512, scales by the routing weight into the staging.
+constexpr int kSkTok = 32;     // rows per skinny tile (two 16-row column tiles)
+constexpr int kSkinnyRows = 8; // auto mode: skinny while T*k <= kSkinnyRows * n_expert
+constexpr int kSkW = 8;        // waves per workgroup
+
+template <int NJ>
+__device__ __forceinline__ void skinny_gateup(const GemmArgs &A, const uint8_t *Wg, const uint8_t *Wu,
+                                              int mt0, int p0, int p1, float (*red)[4][2][64][4]) {
+    constexpr int KD = 2048, NKT = KD / 128;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q = lane >> 4;
+    const size_t nib = (size_t)512 * KD / 2;
+    // this wave's K-steps: 2w and 2w+1 (one scale dword group, op_sel 2w%4 and +1)
+    const int kt0 = 2 * wave, g = kt0 >> 2;
+    u32x4 af[4][2];
+    uint32_t sa[4];
+#pragma unroll
+    for (int a = 0; a < 4; a++) {
+        const uint8_t *W = a < 2 ? Wg : Wu;
+        const int mt = mt0 + (a & 1);
+#pragma unroll
+        for (int s2 = 0; s2 < 2; s2++)
+            af[a][s2] = *reinterpret_cast<const u32x4 *>(W + ((size_t)mt * NKT + kt0 + s2) * 1024 + lane * 16);
+        sa[a] = *reinterpret_cast<const uint32_t *>(W + nib + ((size_t)mt * 64 + lane) * NKT + 4 * g);
+    }
+    u32x4 bf[NJ][2][2];
+    uint32_t sb[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const int p = p0 + j * 16 + (lane & 15);
+        const int r = A.row_tok[p < p1 ? p : p0];
+        const uint8_t *bp = A.bq + (size_t)r * KD + q * 16;
+#pragma unroll
+        for (int s2 = 0; s2 < 2; s2++) {
+            bf[j][s2][0] = *reinterpret_cast<const u32x4 *>(bp + (kt0 + s2) * 128);
+            bf[j][s2][1] = *reinterpret_cast<const u32x4 *>(bp + (kt0 + s2) * 128 + 64);
+        }
+        sb[j] = *reinterpret_cast<const uint32_t *>(A.bs2 + (size_t)r * (KD / 32) + q * NKT + 4 * g);
+    }
+    v4f acc[4][NJ];
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int j = 0; j < NJ; j++) acc[a][j] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s2 = 0; s2 < 2; s2++)
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            const u32x4 b0 = bf[j][s2][0], b1 = bf[j][s2][1];
+            const v8i bv = v8i{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
+#pragma unroll
+            for (int a = 0; a < 4; a++) {
+                const u32x4 f = af[a][s2];
+                const v8i av = v8i{(int)f[0], (int)f[1], (int)f[2], (int)f[3], 0, 0, 0, 0};
+                acc[a][j] = mfma_sel((kt0 + s2) & 3, av, bv, acc[a][j], (int)sa[a], (int)sb[j]);
+            }
+        }
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+            *reinterpret_cast<v4f *>(&red[wave][a][j][lane][0]) = acc[a][j];
+    __syncthreads();
+    if (wave >= NJ) return;
+    // wave j finishes column tile j: sums over the 8 K-slices in wave order
+    const int j = wave;
+    const int p = p0 + j * 16 + (lane & 15);
+    float h[2][4];
+    float amax = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        v4f gs = *reinterpret_cast<const v4f *>(&red[0][r][j][lane][0]);
+        v4f us = *reinterpret_cast<const v4f *>(&red[0][2 + r][j][lane][0]);
+#pragma unroll
+        for (int w = 1; w < kSkW; w++) {
+            gs += *reinterpret_cast<const v4f *>(&red[w][r][j][lane][0]);
+            us += *reinterpret_cast<const v4f *>(&red[w][2 + r][j][lane][0]);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            h[r][i] = silu(gs[i]) * us[i];
+            amax = fmaxf(amax, fabsf(h[r][i]));
+        }
+    }
+    amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+    const int e2 = quant_exp(amax);
+    const float mul = inv_scale(e2);
+    if (p < p1) {
+        const int ffb = mt0 * 16;
+#pragma unroll
+        for (int r = 0; r < 2; r++)
+            *reinterpret_cast<uint32_t *>(A.hq + (size_t)p * A.ldo + ffb + r * 16 + 4 * q) =
+                e4m3x4(h[r][0] * mul, h[r][1] * mul, h[r][2] * mul, h[r][3] * mul);
+        if (lane < 16) {
+            const int b = ffb / 32, nb = A.ldo / 32;
+            A.hs[(size_t)p * nb + b] = (uint8_t)(127 + e2);
+            A.hs2[(size_t)p * nb + (b & 3) * (nb / 4) + (b >> 2)] = (uint8_t)(127 + e2);
+        }
+    }
+}
+
+template <int NJ>
+__device__ __forceinline__ void skinny_down(const GemmArgs &A, const uint8_t *W, int mt0, int p0, int p1) {
+    constexpr int KD = 512, NKT = KD / 128;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q = lane >> 4;
+    const size_t nib = (size_t)2048 * KD / 2;
+    const int mt = mt0 + wave;
+    u32x4 af[NKT];
+#pragma unroll
+    for (int kt = 0; kt < NKT; kt++)
+        af[kt] = *reinterpret_cast<const u32x4 *>(W + ((size_t)mt * NKT + kt) * 1024 + lane * 16);
+    const uint32_t sa = *reinterpret_cast<const uint32_t *>(W + nib + ((size_t)mt * 64 + lane) * NKT);
+    u32x4 bf[NJ][NKT][2];
+    uint32_t sb[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const int p = p0 + j * 16 + (lane & 15);
+        const int r = p < p1 ? p : p0;
+        const uint8_t *bp = A.bq + (size_t)r * KD + q * 16;
+#pragma unroll
+        for (int kt = 0; kt < NKT; kt++) {
+            bf[j][kt][0] = *reinterpret_cast<const u32x4 *>(bp + kt * 128);
+            bf[j][kt][1] = *reinterpret_cast<const u32x4 *>(bp + kt * 128 + 64);
+        }
+        sb[j] = *reinterpret_cast<const uint32_t *>(A.bs2 + (size_t)r * (KD / 32) + q * NKT);
+    }
+    v4f acc[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) acc[j] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kt = 0; kt < NKT; kt++) {
+        const u32x4 f = af[kt];
+        const v8i av = v8i{(int)f[0], (int)f[1], (int)f[2], (int)f[3], 0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            const u32x4 b0 = bf[j][kt][0], b1 = bf[j][kt][1];
+            const v8i bv = v8i{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
+            acc[j] = mfma_sel(kt, av, bv, acc[j], (int)sa, (int)sb[j]);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const int p = p0 + j * 16 + (lane & 15);
+        if (p >= p1) continue;
+        const float w = A.row_w[p];
+        const v4f c = acc[j];
+        *reinterpret_cast<float4 *>(A.dnw + (size_t)p * A.ldo + mt * 16 + 4 * q) =
+            make_float4(c[0] * w, c[1] * w, c[2] * w, c[3] * w);
+    }
+}
+
+// XCD-major order as in k_grouped: the 16 row blocks of one tile run back to
+// back on one XCD.
+template <int MODE>
+__global__ __launch_bounds__(64 * kSkW) void k_skinny(GemmArgs A) {
+    constexpr int NRB = 16;
+    const int xcd = blockIdx.x & 7, jx = blockIdx.x >> 3;
+    const int ti = 8 * (jx / NRB) + xcd, rb = jx % NRB;
+    if (ti >= *A.ntiles) return;
+    const int4 tile = A.tiles[ti];
+    const int e = tile.x, p0 = tile.y, p1 = tile.z;
+    const int nj = (p1 - p0 + 15) >> 4;
+    if constexpr (MODE == MODE_GATEUP) {
+        __shared__ __align__(16) float red[kSkW][4][2][64][4];
+        const uint8_t *Wg = e < A.E ? A.wa + (size_t)e * A.wstride : A.sa;
+        const uint8_t *Wu = e < A.E ? A.wb + (size_t)e * A.wstride : A.sb;
+        if (nj <= 1) skinny_gateup<1>(A, Wg, Wu, rb * 2, p0, p1, red);
+        else skinny_gateup<2>(A, Wg, Wu, rb * 2, p0, p1, red);
+    } else {
+        const uint8_t *W = e < A.E ? A.wa + (size_t)e * A.wstride : A.sa;
+        if (nj <= 1) skinny_down<1>(A, W, rb * 8, p0, p1);
+        else skinny_down<2>(A, W, rb * 8, p0, p1);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1390,7 +1632,7 @@ struct q36moe_weights {
 // Kernel arguments of the last forward; the weights are bound per launch so
 // a stage can be replayed over other weight sets (q36moe_ctx_replay).
 struct Plan {
-    int T, has_sh, direct, mode3, tiles, nb;
+    int T, has_sh, direct, mode3, skinny, tiles, nb;
     RouteArgs ra;
     ScanArgs sa;
     GemmArgs ga, da;
@@ -1414,7 +1656,7 @@ struct q36moe_ctx {
     float *dnw;
     float *hf;                      // direct path: fp32 SwiGLU rows
     uint32_t *sync;                 // fused decode: arrive[16], depart[16], err
-    int path_mode;                  // 0 auto, 1 sorted, 2 direct
+    int path_mode;                  // 0 auto, 1 sorted (fat tiles), 2 direct, 3 one-kernel direct, 4 sorted (skinny tiles)
     int last_T, last_sh, last_path;
     int timing;
     Plan *plan;                     // kernel arguments of the last forward
@@ -1679,12 +1921,18 @@ static void launch_stage(const q36moe_ctx *c, const Plan &P, int st, hipStream_t
             hipLaunchKernelGGL(k_scatter, dim3(P.nb), dim3(256), 0, s, P.sa);
             break;
         case ST_GATEUP:
-            hipLaunchKernelGGL((k_grouped<MODE_GATEUP, kGuRT, 2048, kGuBR>),
-                               dim3(P.tiles * (FF / (16 * kGuRT))), dim3(kGT), 0, s, P.ga);
+            if (P.skinny)
+                hipLaunchKernelGGL(k_skinny<MODE_GATEUP>, dim3(P.tiles * 16), dim3(64 * kSkW), 0, s, P.ga);
+            else
+                hipLaunchKernelGGL((k_grouped<MODE_GATEUP, kGuRT, 2048, kGuBR>),
+                                   dim3(P.tiles * (FF / (16 * kGuRT))), dim3(kGT), 0, s, P.ga);
             break;
         case ST_DOWN:
-            hipLaunchKernelGGL((k_grouped<MODE_DOWN, kDnRT, 512, kDnBR>),
-                               dim3(P.tiles * (D / (16 * kDnRT))), dim3(kGT), 0, s, P.da);
+            if (P.skinny)
+                hipLaunchKernelGGL(k_skinny<MODE_DOWN>, dim3(P.tiles * 16), dim3(64 * kSkW), 0, s, P.da);
+            else
+                hipLaunchKernelGGL((k_grouped<MODE_DOWN, kDnRT, 512, kDnBR>),
+                                   dim3(P.tiles * (D / (16 * kDnRT))), dim3(kGT), 0, s, P.da);
             break;
         case ST_COMBINE:
             hipLaunchKernelGGL(k_combine, dim3(T), dim3(256), 0, s, c->dnw, c->pos, T, K, D, P.has_sh,
@@ -1722,18 +1970,22 @@ int q36moe_forward(q36moe_ctx *c, const q36moe_weights *w, const void *x, int x_
     const int E = c->E, D = c->D, FF = c->FF, K = c->K;
     const int n = T * K;
     const int nb = (T + kRouteTPB - 1) / kRouteTPB;
-    const int tn = kTileTok;
-    int tiles = n / tn + (n < E ? n : E) + (has_sh ? (T + tn - 1) / tn : 0);
-    tiles = (tiles + 7) & ~7;   // whole groups of 8 for the XCD-major tile order
     hipStream_t s = c->stream;
 
-    const bool direct = (c->path_mode == 2 || c->path_mode == 3) ? (T <= kDirectMaxT)
-                        : c->path_mode == 1 ? false : (T <= kDirectMaxT);
-    if ((c->path_mode == 2 || c->path_mode == 3) && !direct) return Q36MOE_EINVAL;
+    const int pm = c->path_mode;
+    const bool direct = (pm == 2 || pm == 3) ? (T <= kDirectMaxT) : (pm == 1 || pm == 4) ? false
+                                                                                      : (T <= kDirectMaxT);
+    if ((pm == 2 || pm == 3) && !direct) return Q36MOE_EINVAL;
+    // sorted path: skinny tiles (<= 32 rows) while the average expert has at
+    // most kSkinnyRows rows, else fat tiles of up to kTileTok rows
+    const bool skinny = pm == 4 || (pm == 0 && (size_t)n <= (size_t)kSkinnyRows * E);
+    const int tn = skinny ? kSkTok : kTileTok;
+    int tiles = n / tn + (n < E ? n : E) + (has_sh ? (T + tn - 1) / tn : 0);
+    tiles = (tiles + 7) & ~7;   // whole groups of 8 for the XCD-major tile order
 
     Plan &P = *c->plan;
     P = Plan{};
-    P.T = T; P.has_sh = has_sh; P.direct = direct; P.mode3 = c->path_mode == 3;
+    P.T = T; P.has_sh = has_sh; P.direct = direct; P.mode3 = pm == 3; P.skinny = skinny;
     P.tiles = tiles; P.nb = nb; P.out = out; P.out_fmt = out_fmt;
     if (direct) {
         const int ngu = (n + (has_sh ? T : 0)) * (FF / 16);
@@ -1766,7 +2018,7 @@ int q36moe_forward(q36moe_ctx *c, const q36moe_weights *w, const void *x, int x_
     if (c->timing) (void)hipEventRecord(c->ev[ST_COUNT], s);
     c->last_T = T;
     c->last_sh = has_sh;
-    c->last_path = direct ? 1 : 0;
+    c->last_path = direct ? 1 : skinny ? 2 : 0;
     if (hipGetLastError() != hipSuccess) return Q36MOE_EHIP;
     if (c->timing) {
         if (hipEventSynchronize(c->ev[ST_COUNT]) != hipSuccess) return Q36MOE_EHIP;
@@ -1833,7 +2085,7 @@ int q36moe_ctx_copy_tap(q36moe_ctx *c, int tap, void *dst, size_t bytes, size_t 
 }
 
 int q36moe_ctx_set_path(q36moe_ctx *c, int mode) {
-    if (!c || mode < 0 || mode > 3) return Q36MOE_EINVAL;
+    if (!c || mode < 0 || mode > 4) return Q36MOE_EINVAL;
     c->path_mode = mode;
     return Q36MOE_OK;
 }

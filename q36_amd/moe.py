@@ -260,16 +260,17 @@ class MoELayer:
               "q36moe_ctx_copy_tap")
         return dst
 
-    PATH_AUTO, PATH_SORTED, PATH_DIRECT, PATH_DIRECT_FUSED = 0, 1, 2, 3
+    PATH_AUTO, PATH_SORTED, PATH_DIRECT, PATH_DIRECT_FUSED, PATH_SORTED_SKINNY = 0, 1, 2, 3, 4
 
     def set_path(self, mode):
-        """0 auto (direct for T <= 16), 1 sorted, 2 direct (two kernels),
-        3 direct (one kernel)."""
+        """0 auto (direct for T <= 16, skinny tiles while T*k <= 8*n_expert),
+        1 sorted (fat tiles), 2 direct (two kernels), 3 direct (one kernel),
+        4 sorted (skinny tiles)."""
         check(lib().q36moe_ctx_set_path(self._h, mode), "q36moe_ctx_set_path")
 
     @property
     def last_path(self):
-        """0 sorted, 1 direct."""
+        """0 sorted (fat tiles), 1 direct, 2 sorted (skinny tiles)."""
         return lib().q36moe_ctx_last_path(self._h)
 
     def check(self):

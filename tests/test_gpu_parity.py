@@ -217,7 +217,7 @@ def _check_routing(layer, oracle, lg, E=256, k=8):
     np.testing.assert_array_equal(gi, oi)
     gw = layer.tap(moe.TAP_TOPK_W).cpu().double().numpy()
     assert np.abs(gw - ow).max() <= 2e-6
-    if layer.last_path == 0:        # sorted path: offsets and permutation bit-exact
+    if layer.last_path in (0, 2):   # sorted paths: offsets and permutation bit-exact
         off, perm, pos = oracle.sort_entries(gi, E)
         np.testing.assert_array_equal(layer.tap(moe.TAP_EOFF).cpu().numpy(), off)
         np.testing.assert_array_equal(layer.tap(moe.TAP_PERM).cpu().numpy(), perm)
@@ -279,7 +279,7 @@ def _check_layer(name, dev, oracle, layer_w, x, lg, shg, sample=None, x_dtype=to
     w, dw = layer_w
     T = x.shape[0]
     layer, y32, y16 = _run_layer(dev, dw, x, lg, shg, x_dtype=x_dtype, path=path)
-    name = f"{name}/{'direct' if layer.last_path == 1 else 'sorted'}"
+    name = f"{name}/{({1: 'direct', 2: 'sorted_skinny'}).get(layer.last_path, 'sorted')}"
     gi = _check_routing(layer, oracle, lg)
     oq, os_ = oracle.quant_e4m3(x)
     np.testing.assert_array_equal(layer.tap(moe.TAP_XQ).cpu().numpy(), oq)
@@ -325,8 +325,8 @@ def _check_layer(name, dev, oracle, layer_w, x, lg, shg, sample=None, x_dtype=to
     return layer
 
 
-PATHS = [pytest.param(1, id="sorted"), pytest.param(2, id="direct"),
-         pytest.param(3, id="direct_fused")]
+PATHS = [pytest.param(1, id="sorted"), pytest.param(4, id="sorted_skinny"),
+         pytest.param(2, id="direct"), pytest.param(3, id="direct_fused")]
 
 
 @pytest.mark.parametrize("path", PATHS)
@@ -366,10 +366,11 @@ def test_fused_decode_repeated_calls(dev, layer_w):
     two.check()
 
 
-def test_forward_small33(dev, oracle, layer_w):
+@pytest.mark.parametrize("path", [pytest.param(0, id="auto"), pytest.param(1, id="sorted")])
+def test_forward_small33(dev, oracle, layer_w, path):
     rng = np.random.default_rng(333)
     x, lg = synth.hidden(rng, 33), synth.normal_logits(rng, 33)
-    _check_layer("small33", dev, oracle, layer_w, x, lg, None)
+    _check_layer("small33", dev, oracle, layer_w, x, lg, None, path=path)
 
 
 @pytest.mark.parametrize("T", [1, 5, 16])
@@ -380,20 +381,23 @@ def test_direct_equals_sorted_inputs(dev, layer_w, T):
     rng = np.random.default_rng(900 + T)
     x, lg = synth.hidden(rng, T), synth.normal_logits(rng, T)
     outs, taps = [], []
-    for path in (1, 2):
+    for path in (1, 2, 4):
         layer, y32, _ = _run_layer(dev, dw, x, lg, None, path=path)
         outs.append(y32)
         taps.append([layer.tap(m).cpu().numpy() for m in (moe.TAP_TOPK_IDX, moe.TAP_TOPK_W,
                                                           moe.TAP_XQ, moe.TAP_XS)])
-    for a, b in zip(*taps):
-        np.testing.assert_array_equal(a, b)
-    _, normwise = _row_err(outs[1], outs[0].astype(np.float64))
-    assert normwise <= TOL
+    for other in taps[1:]:
+        for a, b in zip(taps[0], other):
+            np.testing.assert_array_equal(a, b)
+    for o in outs[1:]:
+        _, normwise = _row_err(o, outs[0].astype(np.float64))
+        assert normwise <= TOL
 
 
-def test_forward_ragged64_zipf(dev, oracle, layer_w):
+@pytest.mark.parametrize("path", [pytest.param(0, id="auto_skinny"), pytest.param(1, id="sorted")])
+def test_forward_ragged64_zipf(dev, oracle, layer_w, path):
     x, lg, _ = synth.config_inputs("ragged64", 2)
-    _check_layer("ragged64", dev, oracle, layer_w, x, lg, None)
+    _check_layer("ragged64", dev, oracle, layer_w, x, lg, None, path=path)
 
 
 def test_forward_prefill4096(dev, oracle, layer_w):
