@@ -1174,6 +1174,98 @@ __global__ __launch_bounds__(64 * kSkW) void k_skinny(GemmArgs A) {
 }
 
 // ---------------------------------------------------------------------------
+// down projection for fat tiles: B (h rows) staged once in LDS, A in registers
+// ---------------------------------------------------------------------------
+// K = d_ff = 512 is short, so the whole B operand of up to 128 rows fits in
+// LDS (128 x 512 B) and every wave keeps its A -- 4 row tiles x all of K --
+// in registers for the workgroup's lifetime.  One barrier after staging;
+// then each wave walks the 16-row column tiles, reading each B fragment once
+// for 4 MFMAs, and stores the finished column tile (x routing weight) before
+// the next: no accumulator outlives its column tile.
+//   workgroup = (tile, 256 output rows), 4 waves; tiles longer than 128 rows
+//   are staged in chunks of 128.
+constexpr int kDlW = 4;                  // waves
+constexpr int kDlRows = 128;             // B rows staged per chunk
+constexpr int kDlStride = 512 + 16;      // LDS row stride: conflict-free fragment reads
+
+__global__ __launch_bounds__(64 * kDlW) void k_down_lds(GemmArgs A) {
+    constexpr int KD = 512, NKT = KD / 128, NRB = 2048 / 256;
+    __shared__ __align__(16) uint8_t sb[kDlRows * kDlStride];
+    __shared__ uint32_t ss[kDlRows][4];       // B scale dwords: [row][lane group]
+    __shared__ float ws[kDlRows];             // routing weight of each row
+    const int xcd = blockIdx.x & 7, jx = blockIdx.x >> 3;
+    const int ti = 8 * (jx / NRB) + xcd, rb = jx % NRB;
+    if (ti >= *A.ntiles) return;
+    const int4 tile = A.tiles[ti];
+    const int e = tile.x, p0 = tile.y, p1 = tile.z;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q = lane >> 4, n = lane & 15;
+    const uint8_t *W = e < A.E ? A.wa + (size_t)e * A.wstride : A.sa;
+    const size_t nib = (size_t)2048 * KD / 2;
+    // this wave's A: row tiles rb*16 + 4*wave + i, all 4 K-steps
+    const int mt0 = rb * 16 + 4 * wave;
+    u32x4 af[4][NKT];
+    uint32_t sa[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+#pragma unroll
+        for (int kt = 0; kt < NKT; kt++)
+            af[i][kt] = *reinterpret_cast<const u32x4 *>(W + ((size_t)(mt0 + i) * NKT + kt) * 1024 + lane * 16);
+        sa[i] = *reinterpret_cast<const uint32_t *>(W + nib + ((size_t)(mt0 + i) * 64 + lane) * NKT);
+    }
+    for (int c0 = p0; c0 < p1; c0 += kDlRows) {
+        const int nr = min(kDlRows, p1 - c0);
+        if (c0 != p0) __syncthreads();   // previous chunk fully read
+        // stage rows c0 .. c0+nr of h (contiguous in sorted order), their
+        // lane-group-major scale dwords and routing weights
+        for (int c = tid; c < nr * (KD / 16); c += 64 * kDlW) {
+            const int r = c / (KD / 16), o = (c % (KD / 16)) * 16;
+            *reinterpret_cast<u32x4 *>(&sb[r * kDlStride + o]) =
+                *reinterpret_cast<const u32x4 *>(A.bq + (size_t)(c0 + r) * KD + o);
+        }
+        for (int c = tid; c < nr; c += 64 * kDlW) {
+            *reinterpret_cast<u32x4 *>(&ss[c][0]) = *reinterpret_cast<const u32x4 *>(A.bs2 + (size_t)(c0 + c) * 16);
+            ws[c] = A.row_w[c0 + c];
+        }
+        __syncthreads();
+        const int ntt = (nr + 15) >> 4;
+        for (int j = 0; j < ntt; j++) {
+            // padding columns read row 0 of the chunk; never stored
+            const int r = j * 16 + n < nr ? j * 16 + n : 0;
+            const uint8_t *bp = &sb[r * kDlStride + q * 16];
+            v8i bv[NKT];
+#pragma unroll
+            for (int kt = 0; kt < NKT; kt++) {
+                const u32x4 b0 = *reinterpret_cast<const u32x4 *>(bp + kt * 128);
+                const u32x4 b1 = *reinterpret_cast<const u32x4 *>(bp + kt * 128 + 64);
+                bv[kt] = v8i{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
+            }
+            const uint32_t sbw = ss[r][q];
+            v4f acc[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[i] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kt = 0; kt < NKT; kt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const u32x4 f = af[i][kt];
+                    const v8i av = v8i{(int)f[0], (int)f[1], (int)f[2], (int)f[3], 0, 0, 0, 0};
+                    acc[i] = mfma_sel(kt, av, bv[kt], acc[i], (int)sa[i], (int)sbw);
+                }
+            if (j * 16 + n < nr) {
+                const int p = c0 + j * 16 + n;
+                const float w = ws[j * 16 + n];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const v4f c = acc[i];
+                    *reinterpret_cast<float4 *>(A.dnw + (size_t)p * A.ldo + (mt0 + i) * 16 + 4 * q) =
+                        make_float4(c[0] * w, c[1] * w, c[2] * w, c[3] * w);
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // direct path for small batches (decode): no sort, two kernels
 // ---------------------------------------------------------------------------
 struct DirectArgs {
@@ -1931,8 +2023,7 @@ static void launch_stage(const q36moe_ctx *c, const Plan &P, int st, hipStream_t
             if (P.skinny)
                 hipLaunchKernelGGL(k_skinny<MODE_DOWN>, dim3(P.tiles * 16), dim3(64 * kSkW), 0, s, P.da);
             else
-                hipLaunchKernelGGL((k_grouped<MODE_DOWN, kDnRT, 512, kDnBR>),
-                                   dim3(P.tiles * (D / (16 * kDnRT))), dim3(kGT), 0, s, P.da);
+                hipLaunchKernelGGL(k_down_lds, dim3(P.tiles * (D / 256)), dim3(64 * kDlW), 0, s, P.da);
             break;
         case ST_COMBINE:
             hipLaunchKernelGGL(k_combine, dim3(T), dim3(256), 0, s, c->dnw, c->pos, T, K, D, P.has_sh,
