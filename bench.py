@@ -54,6 +54,7 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--path", type=int, default=0, help="q36moe_ctx_set_path mode (0 auto)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (counter calibration)")
     return ap.parse_args()
@@ -181,6 +182,7 @@ def main():
         layers.append(w)
     xs, ls, ss = make_inputs(args.config, T, args.inputs, args.seed, dev)
     layer = moe.MoELayer(T, stream=stream)
+    layer.set_path(args.path)
     out = torch.empty((T, D), dtype=torch.bfloat16, device=dev)
     torch.cuda.synchronize()
 

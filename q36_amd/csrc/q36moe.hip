@@ -172,8 +172,8 @@ __device__ __forceinline__ void static_for(F &&f) {
 // a NaN either).
 __device__ __forceinline__ uint32_t logit_key(float f) {
     const uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return 0u;
-    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    const uint32_t k = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return (u & 0x7fffffffu) > 0x7f800000u ? 0u : k;   // selects, no branch
 }
 
 __device__ __forceinline__ int popc_ballot(bool p) { return __popcll(__ballot(p)); }
@@ -222,14 +222,19 @@ __device__ __forceinline__ uint32_t group8_max(uint32_t v) {
 __device__ __forceinline__ Pick route_pick(const float *__restrict__ l, int E, int k, float scale,
                                            uint32_t *lds) {
     const int lane = __lane_id();
+    // the four loads are unconditional and independent (a guarded load
+    // would be sunk into a branch and waited on one at a time)
+    float lv[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) lv[j] = l[min(lane + 64 * j, E - 1)];
     uint32_t key[4];
     bool ok[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-        const int e = lane + 64 * j;
-        const float v = l[e < E ? e : E - 1];
-        ok[j] = e < E;
-        key[j] = ok[j] ? logit_key(v) : 0u;
+        ok[j] = lane + 64 * j < E;
+        // an index past E reads as NaN (key 0); selecting the input rather
+        // than the key keeps the load outside any branch
+        key[j] = logit_key(ok[j] ? lv[j] : __uint_as_float(0x7fffffffu));
     }
     Q36_TRACE_AT(10);
     // 1. bound: min over the 8 group maxima (a group with no valid key gives 0)
@@ -381,20 +386,40 @@ __device__ __forceinline__ uint8_t quant8_lane(const float (&v)[8], int lane, ui
     return (uint8_t)(127 + e2);
 }
 
-__device__ __forceinline__ void load8(const void *x, int fmt, size_t off, float (&v)[8]) {
+// 8 activations as raw bits, then widened to float: split so the load can be
+// issued early (before routing) without the conversion waiting on it there.
+struct X8 {
+    u32x4 a, b;
+};
+__device__ __forceinline__ X8 load8_raw(const void *x, int fmt, size_t off) {
+    X8 r;
     if (fmt == Q36MOE_FMT_F32) {
-        const float4 *p = reinterpret_cast<const float4 *>(static_cast<const float *>(x) + off);
-        const float4 a = p[0], b = p[1];
-        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+        const u32x4 *p = reinterpret_cast<const u32x4 *>(static_cast<const float *>(x) + off);
+        r.a = p[0];
+        r.b = p[1];
     } else {
-        const uint4 t = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(x) + off);
-        const uint32_t w[4] = {t.x, t.y, t.z, t.w};
+        r.a = *reinterpret_cast<const u32x4 *>(static_cast<const uint16_t *>(x) + off);
+        r.b = u32x4{0u, 0u, 0u, 0u};   // unused (no copy of r.a: that would wait on the load)
+    }
+    return r;
+}
+__device__ __forceinline__ void cvt8(const X8 &r, int fmt, float (&v)[8]) {
+    if (fmt == Q36MOE_FMT_F32) {
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            v[2 * j] = __uint_as_float(w[j] << 16);
-            v[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+            v[j] = __uint_as_float(r.a[j]);
+            v[4 + j] = __uint_as_float(r.b[j]);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            v[2 * j] = __uint_as_float(r.a[j] << 16);
+            v[2 * j + 1] = __uint_as_float(r.a[j] & 0xffff0000u);
         }
     }
+}
+__device__ __forceinline__ void load8(const void *x, int fmt, size_t off, float (&v)[8]) {
+    cvt8(load8_raw(x, fmt, off), fmt, v);
 }
 
 struct RouteArgs {
@@ -424,9 +449,9 @@ __global__ __launch_bounds__(kRouteThreads) void k_route(RouteArgs A) {
     if (wave < kRouteTPB && t < A.T) {
         // x of the token (kRouteD values, 8 per lane per pass) is loaded
         // before routing so both latencies overlap
-        float v[kRouteD / 512][8];
+        X8 xr[kRouteD / 512];
 #pragma unroll
-        for (int c = 0; c < kRouteD / 512; c++) load8(A.x, A.x_fmt, (size_t)t * A.D + c * 512 + lane * 8, v[c]);
+        for (int c = 0; c < kRouteD / 512; c++) xr[c] = load8_raw(A.x, A.x_fmt, (size_t)t * A.D + c * 512 + lane * 8);
         const Pick P = route_pick(A.logits + (size_t)t * A.ld, A.E, A.k, A.scale, rlds[wave]);
         if (lane < A.k) {
             A.idx[(size_t)t * A.k + lane] = P.idx;
@@ -439,7 +464,9 @@ __global__ __launch_bounds__(kRouteThreads) void k_route(RouteArgs A) {
         for (int c = 0; c < kRouteD / 512; c++) {
             const size_t o = (size_t)t * A.D + c * 512 + lane * 8;
             const int b = c * 16 + (lane >> 2);
-            const uint8_t sb = quant8_lane(v[c], lane, A.xq + o, A.xs + (size_t)t * nb32 + b);
+            float v[8];
+            cvt8(xr[c], A.x_fmt, v);
+            const uint8_t sb = quant8_lane(v, lane, A.xq + o, A.xs + (size_t)t * nb32 + b);
             // lane-group-major copy for the grouped GEMM: [t][b % 4][b / 4]
             if ((lane & 3) == 0) A.xs2[(size_t)t * nb32 + (b & 3) * (nb32 / 4) + (b >> 2)] = sb;
         }
@@ -1316,8 +1343,7 @@ __device__ __forceinline__ void direct_gateup_body(const DirectArgs &A, int i, i
     Q36_TRACE_AT(0);
     Q36_TRACE_WG(0);
     // issue this wave's x loads first (512 values, 8 per lane)
-    float xv[8];
-    load8(A.x, A.x_fmt, (size_t)t * kDD + wave * 512 + lane * 8, xv);
+    const X8 xr = load8_raw(A.x, A.x_fmt, (size_t)t * kDD + wave * 512 + lane * 8);
 
     int e = A.E;
     float wgt = 0.0f;
@@ -1346,6 +1372,8 @@ __device__ __forceinline__ void direct_gateup_body(const DirectArgs &A, int i, i
     const int sag = *reinterpret_cast<const int *>(Wg + so);
     const int sau = *reinterpret_cast<const int *>(Wu + so);
 
+    float xv[8];
+    cvt8(xr, A.x_fmt, xv);
     quant8_lane(xv, lane, sx + wave * 512 + lane * 8, sxs + wave * 16 + (lane >> 2));
     Q36_TRACE_AT(2);
     if (threadIdx.x < 8) reinterpret_cast<uint32_t *>(sx + kDD)[threadIdx.x] = 0u;
