@@ -654,7 +654,7 @@ constexpr int kTileTok = Q36_TILE_TOK;
 #define Q36_GU_RT 4
 #endif
 #ifndef Q36_GU_BR
-#define Q36_GU_BR 4
+#define Q36_GU_BR 3
 #endif
 #ifndef Q36_DN_RT
 #define Q36_DN_RT 8
@@ -798,24 +798,15 @@ __device__ __forceinline__ void grouped_body(const GemmArgs &A, GroupedLds<MODE,
         if constexpr (kt + NB - 1 < NKT) {
 #pragma unroll
             for (int j = 0; j < NJ; j++) {
-#ifdef Q36_EXP_NOB
-                bq[(kt + NB - 1) % NB][j][0] = bq[kt % NB][j][1];
-                bq[(kt + NB - 1) % NB][j][1] = bq[kt % NB][j][0];
-#else
                 bq[(kt + NB - 1) % NB][j][0] = *reinterpret_cast<const u32x4 *>(brp[j] + (kt + NB - 1) * 128);
                 bq[(kt + NB - 1) % NB][j][1] = *reinterpret_cast<const u32x4 *>(brp[j] + (kt + NB - 1) * 128 + 64);
-#endif
             }
         }
         // 2. A slices of step kt+NR
         if constexpr (kt + NR < NKT) {
 #pragma unroll
             for (int u = 0; u < APT; u++)
-#ifdef Q36_EXP_NOA
-                ra[(kt + NR) % NR][u] = ra[(kt + 1) % NR][u];
-#else
                 ra[(kt + NR) % NR][u] = *reinterpret_cast<const u32x4 *>(asrc[u] + (size_t)(kt + NR) * 1024);
-#endif
         }
         // 3. A of step kt+1 into the other LDS slot (its last readers,
         //    the fragment loads of step kt-1, finished before barrier kt-1)
@@ -827,14 +818,12 @@ __device__ __forceinline__ void grouped_body(const GemmArgs &A, GroupedLds<MODE,
         // pin the previous step's MFMAs here: without a use they sink to the
         // epilogue and keep every step's operands live at once; pinning one
         // step late lets them overlap this step's loads and LDS write
-#ifndef Q36_NO_PIN
         if constexpr (kt > 0) {
 #pragma unroll
             for (int a = 0; a < NAT; a++)
 #pragma unroll
                 for (int j = 0; j < NJ; j++) asm volatile("" : "+v"(acc[a][j]));
         }
-#endif
         // 4. MFMAs of step kt, first half
         v8i bv[NJ1];
 #pragma unroll
@@ -855,9 +844,7 @@ __device__ __forceinline__ void grouped_body(const GemmArgs &A, GroupedLds<MODE,
         mfmas(0, NAT / 2);
         // 5. barrier: step kt+1's A slot is complete
         if constexpr (kt + 1 < NKT) {
-#ifndef Q36_EXP_NOBAR
             lds_barrier();
-#endif
             __builtin_amdgcn_sched_barrier(0);
             // 6. step kt+1's A fragments
 #pragma unroll
