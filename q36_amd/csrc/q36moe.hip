@@ -53,8 +53,9 @@ namespace {
 
 constexpr int kMaxExperts = 256;
 constexpr int kMaxTopK = 8;
-constexpr int kRouteTPB = 16;      // tokens per k_route workgroup (one wavefront each)
-constexpr int kRouteThreads = 1024;
+constexpr int kRouteTPB = 16;      // most tokens per k_route workgroup (one wavefront each)
+constexpr int kRouteTPBSmall = 4;  // tokens per workgroup for small batches (T <= kRouteSmallT)
+constexpr int kRouteSmallT = 512;
 constexpr int kRouteD = 2048;     // d_model of k_route (the q36 shape, q36.h:78-84)
 constexpr int kDirectMaxT = 16;    // largest batch routed to the direct (unsorted) path
 
@@ -429,24 +430,27 @@ struct RouteArgs {
     int32_t *blk_cnt; int32_t *rank;
 };
 
-// One wavefront per token, kRouteTPB tokens per workgroup: top-k routing,
+// One wavefront per token, TPB tokens per workgroup: top-k routing,
 // FP8 quantisation of x (8 values per lane, 4 lanes per 32-block), then the
 // block's per-expert counts (expert-major, blk_cnt[e][block]) and each
 // entry's rank among the block's earlier entries of the same expert (the
 // stable order of the sort), from a per-expert mask of the block's tokens.
-__global__ __launch_bounds__(kRouteThreads) void k_route(RouteArgs A) {
+// Small batches use 4 tokens per workgroup to spread the quantisation over
+// more CUs; large ones 16, which keeps the per-block count table short.
+template <int TPB>
+__global__ __launch_bounds__(64 * TPB) void k_route(RouteArgs A) {
     __shared__ uint32_t tmask[kMaxExperts];
-    __shared__ int ent[kRouteTPB * kMaxTopK];
-    __shared__ uint32_t rlds[kRouteThreads / 64][kRouteLds];
-    static_assert(kRouteTPB <= 32, "token mask");
+    __shared__ int ent[TPB * kMaxTopK];
+    __shared__ uint32_t rlds[TPB][kRouteLds];
+    static_assert(TPB <= 32, "token mask");
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int t0 = blockIdx.x * kRouteTPB;
+    const int t0 = blockIdx.x * TPB;
     const int nb32 = A.D / 32;
-    for (int e = threadIdx.x; e < A.E; e += kRouteThreads) tmask[e] = 0u;
+    for (int e = threadIdx.x; e < A.E; e += 64 * TPB) tmask[e] = 0u;
     __syncthreads();
     const int t = t0 + wave;
     Q36_TRACE_AT(20);
-    if (wave < kRouteTPB && t < A.T) {
+    if (t < A.T) {
         // x of the token (kRouteD values, 8 per lane per pass) is loaded
         // before routing so both latencies overlap
         X8 xr[kRouteD / 512];
@@ -474,14 +478,14 @@ __global__ __launch_bounds__(kRouteThreads) void k_route(RouteArgs A) {
     Q36_TRACE_AT(22);
     __syncthreads();
     Q36_TRACE_AT(23);
-    const int ntok = min(kRouteTPB, A.T - t0);
+    const int ntok = min(TPB, A.T - t0);
     if (threadIdx.x < ntok * A.k) {
         const int tl = threadIdx.x / A.k;
         const int e = ent[threadIdx.x];
         A.rank[(size_t)t0 * A.k + threadIdx.x] = __popc(tmask[e] & ((1u << tl) - 1u));
     }
     Q36_TRACE_AT(24);
-    for (int e = threadIdx.x; e < A.E; e += kRouteThreads)
+    for (int e = threadIdx.x; e < A.E; e += 64 * TPB)
         A.blk_cnt[(size_t)e * A.nb + blockIdx.x] = __popc(tmask[e]);
 }
 
@@ -506,7 +510,7 @@ __global__ __launch_bounds__(256) void k_quant(const void *x, int x_fmt, int T, 
 // sort: offsets, stable scatter, tile list
 // ---------------------------------------------------------------------------
 struct ScanArgs {
-    const int32_t *blk_cnt; int nb; int E; int T; int k;
+    const int32_t *blk_cnt; int nb; int tpb; int E; int T; int k;
     const int32_t *idx; const float *wt; const int32_t *rank; const float *shg;
     int tn;
     int32_t *blk_off; int32_t *tot; int32_t *e_off; int32_t *perm; int32_t *pos;
@@ -593,7 +597,7 @@ __global__ __launch_bounds__(256) void k_scatter(ScanArgs A) {
     else if (tid < 128) wave_scan256(ntile, A.E, toff, &toff[A.E]);
     __syncthreads();
     const int n = A.T * A.k;
-    const int i0 = b * kRouteTPB * A.k, i1 = min(n, i0 + kRouteTPB * A.k);
+    const int i0 = b * A.tpb * A.k, i1 = min(n, i0 + A.tpb * A.k);
     for (int i = i0 + tid; i < i1; i += 256) {
         const int e = A.idx[i];
         const int p = off[e] + A.blk_off[(size_t)e * A.nb + b] + A.rank[i];
@@ -603,7 +607,7 @@ __global__ __launch_bounds__(256) void k_scatter(ScanArgs A) {
         A.row_w[p] = A.wt[i];
     }
     if (A.shg) {
-        for (int t = b * kRouteTPB + tid; t < min(A.T, (b + 1) * kRouteTPB); t += 256) {
+        for (int t = b * A.tpb + tid; t < min(A.T, (b + 1) * A.tpb); t += 256) {
             A.row_tok[n + t] = t;
             A.row_w[n + t] = 1.0f / (1.0f + expf(-A.shg[t]));
         }
@@ -1920,7 +1924,7 @@ int q36moe_ctx_create(int max_tokens, int n_expert, int d_model, int d_ff, int t
     }
     c->stream = static_cast<hipStream_t>(stream);
     c->max_T = max_tokens; c->E = n_expert; c->D = d_model; c->FF = d_ff; c->K = top_k;
-    c->nb_max = (max_tokens + kRouteTPB - 1) / kRouteTPB;
+    c->nb_max = (max_tokens + kRouteTPBSmall - 1) / kRouteTPBSmall;
     const size_t n = (size_t)max_tokens * top_k;
     const size_t rows = n + max_tokens;            // routed entries + shared rows
     c->tile_cap = n / 16 + (size_t)(n < (size_t)n_expert ? n : n_expert) + (max_tokens + 15) / 16 + 16;
@@ -2021,7 +2025,10 @@ static void launch_stage(const q36moe_ctx *c, const Plan &P, int st, hipStream_t
     }
     switch (st) {
         case ST_ROUTE:
-            hipLaunchKernelGGL(k_route, dim3(P.nb), dim3(kRouteThreads), 0, s, P.ra);
+            if (P.sa.tpb == kRouteTPB)
+                hipLaunchKernelGGL(k_route<kRouteTPB>, dim3(P.nb), dim3(64 * kRouteTPB), 0, s, P.ra);
+            else
+                hipLaunchKernelGGL(k_route<kRouteTPBSmall>, dim3(P.nb), dim3(64 * kRouteTPBSmall), 0, s, P.ra);
             break;
         case ST_SCAN:
             hipLaunchKernelGGL(k_colscan, dim3((c->E + kColExp - 1) / kColExp), dim3(256), 0, s, P.sa);
@@ -2075,7 +2082,8 @@ int q36moe_forward(q36moe_ctx *c, const q36moe_weights *w, const void *x, int x_
     const int has_sh = shg != nullptr;
     const int E = c->E, D = c->D, FF = c->FF, K = c->K;
     const int n = T * K;
-    const int nb = (T + kRouteTPB - 1) / kRouteTPB;
+    const int tpb = T <= kRouteSmallT ? kRouteTPBSmall : kRouteTPB;
+    const int nb = (T + tpb - 1) / tpb;
     hipStream_t s = c->stream;
 
     const int pm = c->path_mode;
@@ -2103,7 +2111,7 @@ int q36moe_forward(q36moe_ctx *c, const q36moe_weights *w, const void *x, int x_
     } else {
         P.ra = RouteArgs{logits, ld_logits, T, E, K, scale, x, x_fmt, D, nb,
                          c->topk_idx, c->topk_w, c->xq, c->xs, c->xs2, c->blk_cnt, c->rank};
-        P.sa = ScanArgs{c->blk_cnt, nb, E, T, K, c->topk_idx, c->topk_w, c->rank, shg, tn,
+        P.sa = ScanArgs{c->blk_cnt, nb, tpb, E, T, K, c->topk_idx, c->topk_w, c->rank, shg, tn,
                         c->blk_off, c->tot, c->e_off, c->perm, c->pos, c->row_tok, c->row_w, c->tiles,
                         c->ntiles};
         GemmArgs &ga = P.ga;
