@@ -55,6 +55,9 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--path", type=int, default=0, help="q36moe_ctx_set_path mode (0 auto)")
+    ap.add_argument("--graph", type=int, default=1,
+                    help="1: time a HIP graph of one forward per weight layer (how a model's "
+                         "layer loop runs when captured); 0: eager launches only")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (counter calibration)")
     return ap.parse_args()
@@ -200,7 +203,35 @@ def main():
         step(warmup + i)
     ev1.record(stream)
     torch.cuda.synchronize()
-    ms = ev0.elapsed_time(ev1) / steps
+    ms_eager = ev0.elapsed_time(ev1) / steps
+    ms = ms_eager
+    graph_layers = 0
+    if args.graph:
+        # one forward per weight layer (inputs cycling) captured once, then
+        # replayed: the host issues one launch per args.layers layers
+        graph_layers = args.layers
+        cap = torch.cuda.Stream()
+        layer.set_stream(cap)
+        with torch.cuda.stream(cap):
+            for i in range(graph_layers):
+                step(i)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=cap):
+            for i in range(graph_layers):
+                step(i)
+        torch.cuda.synchronize()
+        layer.set_stream(stream)
+        reps = max(1, steps // graph_layers)
+        g.replay()
+        torch.cuda.synchronize()
+        ev0.record(stream)
+        for _ in range(reps):
+            g.replay()
+        ev1.record(stream)
+        torch.cuda.synchronize()
+        ms = ev0.elapsed_time(ev1) / (reps * graph_layers)
+        steps = reps * graph_layers
 
     # per-kernel durations: one more forward fixes the stage inputs, then
     # each stage's kernels are launched again `reps` times back to back over
@@ -257,6 +288,7 @@ def main():
         "warmup": warmup,
         "ms_per_step": ms,
         "us_per_layer": ms * 1e3,
+        "us_per_layer_eager": ms_eager * 1e3,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -264,7 +296,9 @@ def main():
         "data": "synthetic (seeded MXFP4 weights filled on device, N(0,1) x and logits)",
         "config": {"workload": args.config, "tokens": T, "d_model": D, "n_expert": E,
                    "top_k": K, "d_ff": FF, "shared_expert": shared,
-                   "weight_layers_rotated": args.layers},
+                   "weight_layers_rotated": args.layers,
+                   "launch": (f"HIP graph of {graph_layers} layer forwards, replayed"
+                              if graph_layers else "eager stream launches")},
         "layer_hbm_fraction": layer_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "distinct_experts": U,
         "stage_us": st_us,
