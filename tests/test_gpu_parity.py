@@ -459,3 +459,38 @@ def test_forward_empty_and_errors(dev, layer_w):
         layer.forward(dw, torch.zeros((5, 2048), device=dev), torch.zeros((5, 256), device=dev))
     with pytest.raises(moe.Q36MoEError):
         moe.MoELayer(4).forward(dw, torch.zeros((1, 2048)), torch.zeros((1, 256)))
+
+
+@pytest.mark.parametrize("T", [1, 64, 600])
+def test_forward_in_hip_graph(dev, layer_w, T):
+    """forward captured in a HIP graph (as a model's layer loop runs it):
+    every replay, with eager forwards of other inputs and synchronisations
+    in between, equals the eager result bit for bit (covers the direct,
+    skinny and fat sorted paths)."""
+    _, dw = layer_w
+    rng = np.random.default_rng(1000 + T)
+    x = torch.from_numpy(synth.hidden(rng, T)).to(dev)
+    lg = torch.from_numpy(synth.normal_logits(rng, T)).to(dev)
+    x2 = torch.from_numpy(synth.hidden(rng, T)).to(dev)
+    lg2 = torch.from_numpy(synth.normal_logits(rng, T)).to(dev)
+    layer = moe.MoELayer(T)
+    out = torch.empty((T, 2048), dtype=torch.float32, device=dev)
+    ref = layer.forward(dw, x, lg, out_dtype=torch.float32).clone()
+    cap = torch.cuda.Stream()
+    layer.set_stream(cap)
+    with torch.cuda.stream(cap):
+        layer.forward(dw, x, lg, out=out)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=cap):
+        layer.forward(dw, x, lg, out=out)
+    torch.cuda.synchronize()
+    layer.set_stream(torch.cuda.current_stream())
+    for rep in range(4):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"replay {rep}"
+        other = layer.forward(dw, x2, lg2, out_dtype=torch.float32)   # eager work between
+        torch.cuda.synchronize()
+        assert not torch.equal(other, ref)
