@@ -1023,7 +1023,7 @@ constexpr int kSkW = 8;        // waves per workgroup
 
 template <int NJ>
 __device__ __forceinline__ void skinny_gateup(const GemmArgs &A, const uint8_t *Wg, const uint8_t *Wu,
-                                              int mt0, int p0, int p1, float (*red)[4][2][64][4]) {
+                                              int mt0, int p0, int p1, float (*red)[4][64][4]) {
     constexpr int KD = 2048, NKT = KD / 128;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q = lane >> 4;
     const size_t nib = (size_t)512 * KD / 2;
@@ -1072,47 +1072,49 @@ __device__ __forceinline__ void skinny_gateup(const GemmArgs &A, const uint8_t *
                 acc[a][j] = mfma_sel((kt0 + s2) & 3, av, bv, acc[a][j], (int)sa[a], (int)sb[j]);
             }
         }
+    // column tiles one at a time through one 32 KiB LDS slab (more
+    // workgroups per CU than a slab per column tile would allow)
 #pragma unroll
-    for (int a = 0; a < 4; a++)
+    for (int j = 0; j < NJ; j++) {
+        if (j > 0) __syncthreads();      // wave 0 has read column tile j-1
 #pragma unroll
-        for (int j = 0; j < NJ; j++)
-            *reinterpret_cast<v4f *>(&red[wave][a][j][lane][0]) = acc[a][j];
-    __syncthreads();
-    if (wave >= NJ) return;
-    // wave j finishes column tile j: sums over the 8 K-slices in wave order
-    const int j = wave;
-    const int p = p0 + j * 16 + (lane & 15);
-    float h[2][4];
-    float amax = 0.0f;
+        for (int a = 0; a < 4; a++) *reinterpret_cast<v4f *>(&red[wave][a][lane][0]) = acc[a][j];
+        __syncthreads();
+        if (wave != 0) continue;
+        // wave 0 finishes column tile j: sums over the 8 K-slices in wave order
+        const int p = p0 + j * 16 + (lane & 15);
+        float h[2][4];
+        float amax = 0.0f;
 #pragma unroll
-    for (int r = 0; r < 2; r++) {
-        v4f gs = *reinterpret_cast<const v4f *>(&red[0][r][j][lane][0]);
-        v4f us = *reinterpret_cast<const v4f *>(&red[0][2 + r][j][lane][0]);
+        for (int r = 0; r < 2; r++) {
+            v4f gs = *reinterpret_cast<const v4f *>(&red[0][r][lane][0]);
+            v4f us = *reinterpret_cast<const v4f *>(&red[0][2 + r][lane][0]);
 #pragma unroll
-        for (int w = 1; w < kSkW; w++) {
-            gs += *reinterpret_cast<const v4f *>(&red[w][r][j][lane][0]);
-            us += *reinterpret_cast<const v4f *>(&red[w][2 + r][j][lane][0]);
+            for (int w = 1; w < kSkW; w++) {
+                gs += *reinterpret_cast<const v4f *>(&red[w][r][lane][0]);
+                us += *reinterpret_cast<const v4f *>(&red[w][2 + r][lane][0]);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                h[r][i] = silu(gs[i]) * us[i];
+                amax = fmaxf(amax, fabsf(h[r][i]));
+            }
         }
+        amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+        amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+        const int e2 = quant_exp(amax);
+        const float mul = inv_scale(e2);
+        if (p < p1) {
+            const int ffb = mt0 * 16;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            h[r][i] = silu(gs[i]) * us[i];
-            amax = fmaxf(amax, fabsf(h[r][i]));
-        }
-    }
-    amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
-    const int e2 = quant_exp(amax);
-    const float mul = inv_scale(e2);
-    if (p < p1) {
-        const int ffb = mt0 * 16;
-#pragma unroll
-        for (int r = 0; r < 2; r++)
-            *reinterpret_cast<uint32_t *>(A.hq + (size_t)p * A.ldo + ffb + r * 16 + 4 * q) =
-                e4m3x4(h[r][0] * mul, h[r][1] * mul, h[r][2] * mul, h[r][3] * mul);
-        if (lane < 16) {
-            const int b = ffb / 32, nb = A.ldo / 32;
-            A.hs[(size_t)p * nb + b] = (uint8_t)(127 + e2);
-            A.hs2[(size_t)p * nb + (b & 3) * (nb / 4) + (b >> 2)] = (uint8_t)(127 + e2);
+            for (int r = 0; r < 2; r++)
+                *reinterpret_cast<uint32_t *>(A.hq + (size_t)p * A.ldo + ffb + r * 16 + 4 * q) =
+                    e4m3x4(h[r][0] * mul, h[r][1] * mul, h[r][2] * mul, h[r][3] * mul);
+            if (lane < 16) {
+                const int b = ffb / 32, nb = A.ldo / 32;
+                A.hs[(size_t)p * nb + b] = (uint8_t)(127 + e2);
+                A.hs2[(size_t)p * nb + (b & 3) * (nb / 4) + (b >> 2)] = (uint8_t)(127 + e2);
+            }
         }
     }
 }
@@ -1179,7 +1181,7 @@ __global__ __launch_bounds__(64 * kSkW) void k_skinny(GemmArgs A) {
     const int e = tile.x, p0 = tile.y, p1 = tile.z;
     const int nj = (p1 - p0 + 15) >> 4;
     if constexpr (MODE == MODE_GATEUP) {
-        __shared__ __align__(16) float red[kSkW][4][2][64][4];
+        __shared__ __align__(16) float red[kSkW][4][64][4];
         const uint8_t *Wg = e < A.E ? A.wa + (size_t)e * A.wstride : A.sa;
         const uint8_t *Wu = e < A.E ? A.wb + (size_t)e * A.wstride : A.sb;
         if (nj <= 1) skinny_gateup<1>(A, Wg, Wu, rb * 2, p0, p1, red);
