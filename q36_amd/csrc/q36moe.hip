@@ -510,7 +510,7 @@ __global__ __launch_bounds__(256) void k_quant(const void *x, int x_fmt, int T, 
 // sort: offsets, stable scatter, tile list
 // ---------------------------------------------------------------------------
 struct ScanArgs {
-    const int32_t *blk_cnt; int nb; int tpb; int E; int T; int k;
+    const int32_t *blk_cnt; int nb; int tpb; int inline_cols; int E; int T; int k;
     const int32_t *idx; const float *wt; const int32_t *rank; const float *shg;
     int tn;
     int32_t *blk_off; int32_t *tot; int32_t *e_off; int32_t *perm; int32_t *pos;
@@ -521,6 +521,7 @@ struct ScanArgs {
 // (blk_off[e][b]) and its total.  kColExp experts per workgroup, 256 / kColExp
 // threads per expert, each summing a contiguous run of blocks.
 constexpr int kColExp = 8;
+constexpr int kScanInlineBlocks = 64;   // k_scatter does the column scan itself up to this many blocks
 __global__ __launch_bounds__(256) void k_colscan(ScanArgs A) {
     constexpr int NP = 256 / kColExp;              // partitions per expert
     __shared__ int part[kColExp][NP + 1];
@@ -585,11 +586,27 @@ __device__ __forceinline__ void wave_scan256(const int *v, int n, int *out, int 
 // deterministic replacement of the reference's atomic bucketing
 // (k_moe_dispatch, q36_engine.cu:3387-3392): entry ids t*k+s ascend inside
 // each expert.
+// With few routing blocks (inline_cols) each workgroup also does the column
+// scan itself -- every expert's counts over all blocks, a few KiB -- and
+// k_colscan is not launched.
 __global__ __launch_bounds__(256) void k_scatter(ScanArgs A) {
     __shared__ int tot[kMaxExperts], off[kMaxExperts + 1], ntile[kMaxExperts], toff[kMaxExperts + 1];
+    __shared__ int boff[kMaxExperts];
     const int tid = threadIdx.x, b = blockIdx.x;
     for (int e = tid; e < A.E; e += 256) {
-        tot[e] = A.tot[e];
+        if (A.inline_cols) {
+            const int32_t *cnt = A.blk_cnt + (size_t)e * A.nb;
+            int run = 0, mine = 0;
+            for (int bb = 0; bb < A.nb; bb++) {
+                if (bb == b) mine = run;
+                run += cnt[bb];
+            }
+            tot[e] = run;
+            boff[e] = mine;
+        } else {
+            tot[e] = A.tot[e];
+            boff[e] = A.blk_off[(size_t)e * A.nb + b];
+        }
         ntile[e] = (tot[e] + A.tn - 1) / A.tn;
     }
     __syncthreads();
@@ -600,7 +617,7 @@ __global__ __launch_bounds__(256) void k_scatter(ScanArgs A) {
     const int i0 = b * A.tpb * A.k, i1 = min(n, i0 + A.tpb * A.k);
     for (int i = i0 + tid; i < i1; i += 256) {
         const int e = A.idx[i];
-        const int p = off[e] + A.blk_off[(size_t)e * A.nb + b] + A.rank[i];
+        const int p = off[e] + boff[e] + A.rank[i];
         A.perm[p] = i;
         A.pos[i] = p;
         A.row_tok[p] = i / A.k;
@@ -2033,7 +2050,8 @@ static void launch_stage(const q36moe_ctx *c, const Plan &P, int st, hipStream_t
                 hipLaunchKernelGGL(k_route<kRouteTPBSmall>, dim3(P.nb), dim3(64 * kRouteTPBSmall), 0, s, P.ra);
             break;
         case ST_SCAN:
-            hipLaunchKernelGGL(k_colscan, dim3((c->E + kColExp - 1) / kColExp), dim3(256), 0, s, P.sa);
+            if (!P.sa.inline_cols)
+                hipLaunchKernelGGL(k_colscan, dim3((c->E + kColExp - 1) / kColExp), dim3(256), 0, s, P.sa);
             hipLaunchKernelGGL(k_scatter, dim3(P.nb), dim3(256), 0, s, P.sa);
             break;
         case ST_GATEUP:
@@ -2113,7 +2131,7 @@ int q36moe_forward(q36moe_ctx *c, const q36moe_weights *w, const void *x, int x_
     } else {
         P.ra = RouteArgs{logits, ld_logits, T, E, K, scale, x, x_fmt, D, nb,
                          c->topk_idx, c->topk_w, c->xq, c->xs, c->xs2, c->blk_cnt, c->rank};
-        P.sa = ScanArgs{c->blk_cnt, nb, tpb, E, T, K, c->topk_idx, c->topk_w, c->rank, shg, tn,
+        P.sa = ScanArgs{c->blk_cnt, nb, tpb, nb <= kScanInlineBlocks ? 1 : 0, E, T, K, c->topk_idx, c->topk_w, c->rank, shg, tn,
                         c->blk_off, c->tot, c->e_off, c->perm, c->pos, c->row_tok, c->row_w, c->tiles,
                         c->ntiles};
         GemmArgs &ga = P.ga;
