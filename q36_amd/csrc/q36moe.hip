@@ -863,8 +863,11 @@ __device__ __forceinline__ void grouped_body(const GemmArgs &A, GroupedLds<MODE,
             }
         };
         mfmas(0, NAT / 2);
-        // 5. barrier: step kt+1's A slot is complete
+        // 5. barrier: step kt+1's A slot is complete (the first half stays
+        //    before it: the scheduler would otherwise sink those MFMAs past
+        //    the barrier, which orders memory only)
         if constexpr (kt + 1 < NKT) {
+            __builtin_amdgcn_sched_barrier(0);
             lds_barrier();
             __builtin_amdgcn_sched_barrier(0);
             // 6. step kt+1's A fragments
@@ -877,6 +880,7 @@ __device__ __forceinline__ void grouped_body(const GemmArgs &A, GroupedLds<MODE,
         mfmas(NAT / 2, NAT);
     });
 
+    if (MODE == MODE_GATEUP && wave == 0) Q36_TRACE_AT(47);
     if constexpr (MODE == MODE_GATEUP) {
 #pragma unroll
         for (int j = 0; j < NJ; j++) {
