@@ -1237,6 +1237,8 @@ __global__ __launch_bounds__(64 * kDlW) void k_down_lds(GemmArgs A) {
     const int xcd = blockIdx.x & 7, jx = blockIdx.x >> 3;
     const int ti = 8 * (jx / NRB) + xcd, rb = jx % NRB;
     if (ti >= *A.ntiles) return;
+    Q36_TRACE_WG(0);
+    Q36_TRACE_AT(48);
     const int4 tile = A.tiles[ti];
     const int e = tile.x, p0 = tile.y, p1 = tile.z;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q = lane >> 4, n = lane & 15;
@@ -1258,16 +1260,30 @@ __global__ __launch_bounds__(64 * kDlW) void k_down_lds(GemmArgs A) {
         if (c0 != p0) __syncthreads();   // previous chunk fully read
         // stage rows c0 .. c0+nr of h (contiguous in sorted order), their
         // lane-group-major scale dwords and routing weights
-        for (int c = tid; c < nr * (KD / 16); c += 64 * kDlW) {
-            const int r = c / (KD / 16), o = (c % (KD / 16)) * 16;
-            *reinterpret_cast<u32x4 *>(&sb[r * kDlStride + o]) =
-                *reinterpret_cast<const u32x4 *>(A.bq + (size_t)(c0 + r) * KD + o);
+        // 16 pieces of 16 B per thread, 8 loads in flight at a time (a
+        // plain loop would wait on each load before the next)
+        constexpr int PT = kDlRows * (KD / 16) / (64 * kDlW);
+#pragma unroll
+        for (int h2 = 0; h2 < PT; h2 += 8) {
+            u32x4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int c = tid + 64 * kDlW * (h2 + u);
+                const int r = min(c / (KD / 16), nr - 1);   // rows past nr: never read
+                v[u] = *reinterpret_cast<const u32x4 *>(A.bq + (size_t)(c0 + r) * KD + (c % (KD / 16)) * 16);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int c = tid + 64 * kDlW * (h2 + u);
+                *reinterpret_cast<u32x4 *>(&sb[(c / (KD / 16)) * kDlStride + (c % (KD / 16)) * 16]) = v[u];
+            }
         }
         for (int c = tid; c < nr; c += 64 * kDlW) {
             *reinterpret_cast<u32x4 *>(&ss[c][0]) = *reinterpret_cast<const u32x4 *>(A.bs2 + (size_t)(c0 + c) * 16);
             ws[c] = A.row_w[c0 + c];
         }
         __syncthreads();
+        Q36_TRACE_AT(49);
         const int ntt = (nr + 15) >> 4;
         for (int j = 0; j < ntt; j++) {
             // padding columns read row 0 of the chunk; never stored
@@ -1304,6 +1320,8 @@ __global__ __launch_bounds__(64 * kDlW) void k_down_lds(GemmArgs A) {
             }
         }
     }
+    Q36_TRACE_AT(50);
+    Q36_TRACE_WG(1);
 }
 
 // ---------------------------------------------------------------------------
