@@ -14,6 +14,11 @@
  *                             pf_moe_block, q36_engine.cu:3423-3472 (prefill),
  *                             starting after the router matvec
  *   q36moe_router_topk     <- k_router_topk, q36_ops.cuh:397-431
+ *   q36moe_router_logits   <- the router matvec at the top of moe_ffn,
+ *                             k_matvec_f32_row (q36_engine.cu:1602,
+ *                             q36_ops.cuh:331-342), and pf_gemm's fp16
+ *                             tensor-core GEMM for prefill (q36_engine.cu:3427,
+ *                             :3403-3414)
  *   q36moe_quant_e4m3      <- k_quant_e4m3, q36_engine.cu:2411-2428
  *   q36moe_ctx_copy_tap    <- the Q36_DEBUG routing dumps, q36_engine.cu:1648-1653
  *   q36moe_probe_mfma      <- the block-scaled MMA calibration harness,
@@ -119,6 +124,15 @@ int q36moe_forward(q36moe_ctx *c, const q36moe_weights *w,
 /* Stage entry points (device pointers, asynchronous on `stream`). */
 int q36moe_router_topk(const float *logits, int T, int n_expert, int ld, int k,
                        float scale, int renorm, int32_t *idx, float *wt, void *stream);
+/* Router logits: logits[t][r] = w[r] . x[t] for r < n_expert (row stride
+ * ld); with n_rows == n_expert + 1 the last row is the shared-expert gate
+ * and goes to shg[t].  w [n_rows][d_model] f32 (device), x [T][d_model]
+ * f32|bf16, d_model == 2048.  mode 1: fp32 products and sums (the decode
+ * matvec); 2: w and x rounded to fp16, fp32 accumulation (the prefill
+ * GEMM); 0: mode 1 for T <= 16, else 2. */
+int q36moe_router_logits(const float *w, int n_rows, int n_expert, const void *x, int x_fmt, int T,
+                         int d_model, int mode, float *logits, int ld, float *shg, void *stream);
+
 int q36moe_quant_e4m3(const void *x, int x_fmt, int T, int K,
                       uint8_t *xq, uint8_t *xs, void *stream);
 

@@ -1027,6 +1027,122 @@ __global__ __launch_bounds__(kGT) void k_grouped(GemmArgs A) {
 }
 
 // ---------------------------------------------------------------------------
+// router logits (the matvec in front of the MoE step)
+// ---------------------------------------------------------------------------
+// logits[t][r] = W[r] . x[t] for r < n_expert; row n_expert (when present)
+// is the shared-expert gate, written to shg[t].  Two numerics, as the
+// reference has two paths:
+//   k_router_f32: fp32 products and sums, one wavefront per row (decode:
+//     k_matvec_f32_row, q36_ops.cuh:331-342); the row stays in registers
+//     while every token's dot product is formed.
+//   k_router_f16: W and x rounded to fp16 (RNE), fp32 accumulation on
+//     v_mfma_f32_16x16x32_f16 (prefill: pf_gemm's fp16 tensor-core path,
+//     q36_engine.cu:3403-3414, 2365-2384).
+constexpr int kRtD = 2048;
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__global__ __launch_bounds__(64) void k_router_f32(const float *__restrict__ W, int n_expert,
+                                                   const void *__restrict__ x, int x_fmt, int T,
+                                                   float *__restrict__ logits, int ld,
+                                                   float *__restrict__ shg) {
+    const int r = blockIdx.x, lane = threadIdx.x;
+    const float *w = W + (size_t)r * kRtD;
+    float4 wv[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) wv[j] = *reinterpret_cast<const float4 *>(w + (j * 64 + lane) * 4);
+    for (int t = 0; t < T; t++) {
+        float xv[32];
+        if (x_fmt == Q36MOE_FMT_F32) {
+            const float *xt = static_cast<const float *>(x) + (size_t)t * kRtD;
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const float4 v = *reinterpret_cast<const float4 *>(xt + (j * 64 + lane) * 4);
+                xv[4 * j] = v.x; xv[4 * j + 1] = v.y; xv[4 * j + 2] = v.z; xv[4 * j + 3] = v.w;
+            }
+        } else {
+            const uint16_t *xt = static_cast<const uint16_t *>(x) + (size_t)t * kRtD;
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const uint2 v = *reinterpret_cast<const uint2 *>(xt + (j * 64 + lane) * 4);
+                xv[4 * j] = __uint_as_float(v.x << 16); xv[4 * j + 1] = __uint_as_float(v.x & 0xffff0000u);
+                xv[4 * j + 2] = __uint_as_float(v.y << 16); xv[4 * j + 3] = __uint_as_float(v.y & 0xffff0000u);
+            }
+        }
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            acc = fmaf(wv[j].x, xv[4 * j], acc);
+            acc = fmaf(wv[j].y, xv[4 * j + 1], acc);
+            acc = fmaf(wv[j].z, xv[4 * j + 2], acc);
+            acc = fmaf(wv[j].w, xv[4 * j + 3], acc);
+        }
+        acc = wave_sum(acc);
+        if (lane == 0) {
+            if (r < n_expert) logits[(size_t)t * ld + r] = acc;
+            else shg[t] = acc;
+        }
+    }
+}
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+// 8 consecutive activations of token row `t` from K offset k, rounded to fp16
+__device__ __forceinline__ f16x8 x8_f16(const void *x, int x_fmt, size_t off) {
+    float v[8];
+    load8(x, x_fmt, off, v);
+    f16x8 h;
+#pragma unroll
+    for (int i = 0; i < 8; i++) h[i] = (_Float16)v[i];
+    return h;
+}
+
+// workgroup = 64 router rows x 64 tokens; wave w owns tokens 16w..16w+15
+// and all 4 row tiles.  v_mfma_f32_16x16x32_f16 operands: lane L holds row
+// (A) or column (B) L%16 and K elements 8(L/16)..8(L/16)+7.
+__global__ __launch_bounds__(256) void k_router_f16(const float *__restrict__ W, int n_rows, int n_expert,
+                                                    const void *__restrict__ x, int x_fmt, int T,
+                                                    float *__restrict__ logits, int ld,
+                                                    float *__restrict__ shg) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, n = lane & 15, g = lane >> 4;
+    const int r0 = blockIdx.x * 64, t0 = blockIdx.y * 64 + wave * 16;
+    const int tok = min(t0 + n, T - 1);                  // padding columns repeat the last token
+    int rows[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) rows[i] = min(r0 + 16 * i + n, n_rows - 1);
+    v4f acc[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) acc[i] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int k0 = 0; k0 < kRtD; k0 += 32) {
+        const f16x8 b = x8_f16(x, x_fmt, (size_t)tok * kRtD + k0 + 8 * g);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float *wr = W + (size_t)rows[i] * kRtD + k0 + 8 * g;
+            const float4 w0 = *reinterpret_cast<const float4 *>(wr);
+            const float4 w1 = *reinterpret_cast<const float4 *>(wr + 4);
+            const f16x8 a = f16x8{(_Float16)w0.x, (_Float16)w0.y, (_Float16)w0.z, (_Float16)w0.w,
+                                  (_Float16)w1.x, (_Float16)w1.y, (_Float16)w1.z, (_Float16)w1.w};
+            acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[i], 0, 0, 0);
+        }
+    }
+    // C: lane L holds rows 4(L/16)+j of token column L%16
+    const int t = t0 + n;
+    if (t >= T) return;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int r = r0 + 16 * i + 4 * g + j;
+            if (r < n_expert) logits[(size_t)t * ld + r] = acc[i][j];
+            else if (r < n_rows) shg[t] = acc[i][j];
+        }
+}
+
+// ---------------------------------------------------------------------------
 // skinny grouped GEMMs: tiles of at most 32 rows (few rows per expert)
 // ---------------------------------------------------------------------------
 // With a handful of rows per expert the grouped GEMM is a weight stream.
@@ -2197,6 +2313,24 @@ int q36moe_router_topk(const float *logits, int T, int n_expert, int ld, int k, 
     if (!logits || !idx || !wt) return Q36MOE_EINVAL;
     hipLaunchKernelGGL(k_topk, dim3((T + 3) / 4), dim3(256), 0, static_cast<hipStream_t>(stream),
                        logits, T, n_expert, ld, k, scale, renorm, idx, wt);
+    return hip_rc(hipGetLastError());
+}
+
+int q36moe_router_logits(const float *w, int n_rows, int n_expert, const void *x, int x_fmt, int T,
+                          int d_model, int mode, float *logits, int ld, float *shg, void *stream) {
+    if (T < 0 || d_model != kRtD || n_expert < 1 || n_rows < n_expert || n_rows > n_expert + 1 ||
+        ld < n_expert || mode < 0 || mode > 2 || (x_fmt != Q36MOE_FMT_F32 && x_fmt != Q36MOE_FMT_BF16))
+        return Q36MOE_EINVAL;
+    if (T == 0) return Q36MOE_OK;
+    if (!w || !x || !logits || (n_rows > n_expert && !shg)) return Q36MOE_EINVAL;
+    const bool f16 = mode == 2 || (mode == 0 && T > kDirectMaxT);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (f16)
+        hipLaunchKernelGGL(k_router_f16, dim3((n_rows + 63) / 64, (T + 63) / 64), dim3(256), 0, s, w, n_rows,
+                           n_expert, x, x_fmt, T, logits, ld, shg);
+    else
+        hipLaunchKernelGGL(k_router_f32, dim3(n_rows), dim3(64), 0, s, w, n_expert, x, x_fmt, T, logits, ld,
+                           shg);
     return hip_rc(hipGetLastError());
 }
 

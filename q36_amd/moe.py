@@ -57,6 +57,7 @@ def lib():
     L.q36moe_ctx_free.restype = None
     L.q36moe_forward.argtypes = [vp, vp, vp, i, vp, i, vp, i, f, vp, i]
     L.q36moe_router_topk.argtypes = [vp, i, i, i, i, f, i, vp, vp, vp]
+    L.q36moe_router_logits.argtypes = [vp, i, i, vp, i, i, i, i, vp, i, vp, vp]
     L.q36moe_quant_e4m3.argtypes = [vp, i, i, i, vp, vp, vp]
     L.q36moe_ctx_copy_tap.argtypes = [vp, i, vp, sz, ctypes.POINTER(sz)]
     L.q36moe_ctx_set_path.argtypes = [vp, i]
@@ -328,6 +329,28 @@ def router_topk(logits, k=8, scale=1.0, renorm=True, n_expert=None):
                                    ctypes.c_void_p(idx.data_ptr()), ctypes.c_void_p(wt.data_ptr()),
                                    _stream()), "q36moe_router_topk")
     return idx, wt
+
+
+ROUTER_AUTO, ROUTER_F32, ROUTER_F16 = 0, 1, 2
+
+
+def router_logits(w, x, n_expert, mode=ROUTER_AUTO):
+    """Router matvec (k_matvec_f32_row / pf_gemm, q36_ops.cuh:331-342,
+    q36_engine.cu:3403-3414): w [n_rows, 2048] f32, x [T, 2048] f32|bf16 ->
+    logits f32 [T, n_expert] and, with n_rows == n_expert + 1, the
+    shared-gate logit f32 [T] (else None)."""
+    T = x.shape[0]
+    n_rows = w.shape[0]
+    logits = torch.empty((T, n_expert), dtype=torch.float32, device=x.device)
+    shg = torch.empty((T,), dtype=torch.float32, device=x.device) if n_rows > n_expert else None
+    fmt = FMT_F32 if x.dtype == torch.float32 else FMT_BF16
+    wp = _dev(w, "w", torch.float32)
+    xp = _dev(x, "x") if T else None
+    check(lib().q36moe_router_logits(wp, n_rows, n_expert, xp, fmt, T, x.shape[1], mode,
+                                     ctypes.c_void_p(logits.data_ptr()), n_expert,
+                                     ctypes.c_void_p(shg.data_ptr()) if shg is not None else None,
+                                     _stream()), "q36moe_router_logits")
+    return logits, shg
 
 
 def quant_e4m3(x):

@@ -95,6 +95,12 @@ def test_entry_points_reject_bad_args_without_gpu(L):
     assert L.q36moe_router_topk(None, 4, 256, 256, 9, ctypes.c_float(1.0), 1, None, None, None) == -22
     assert L.q36moe_router_topk(None, 0, 256, 256, 8, ctypes.c_float(1.0), 1, None, None, None) == 0
     assert L.q36moe_quant_e4m3(None, 0, 4, 100, None, None, None) == -22
+    rl = L.q36moe_router_logits
+    assert rl(None, 257, 256, None, 0, 4, 2000, 0, None, 256, None, None) == -22   # d_model
+    assert rl(None, 258, 256, None, 0, 4, 2048, 0, None, 256, None, None) == -22   # rows > E+1
+    assert rl(None, 256, 256, None, 0, 4, 2048, 3, None, 256, None, None) == -22   # mode
+    assert rl(None, 256, 256, None, 0, 4, 2048, 0, None, 255, None, None) == -22   # ld < E
+    assert rl(None, 257, 256, None, 0, 0, 2048, 0, None, 256, None, None) == 0     # T = 0
     assert L.q36moe_quant_e4m3(None, 2, 4, 128, None, None, None) == -22
     assert L.q36moe_quant_e4m3(None, 0, 0, 128, None, None, None) == 0
     h = ctypes.c_void_p()

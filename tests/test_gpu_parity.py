@@ -494,3 +494,42 @@ def test_forward_in_hip_graph(dev, layer_w, T):
         other = layer.forward(dw, x2, lg2, out_dtype=torch.float32)   # eager work between
         torch.cuda.synchronize()
         assert not torch.equal(other, ref)
+
+
+def _router_ref(w, x, f16):
+    """fp64 dot products of (optionally fp16-rounded, RNE by numpy) inputs,
+    and the sum of |terms| that bounds fp32 accumulation error."""
+    if f16:
+        w = w.astype(np.float16)
+        x = x.astype(np.float16)
+    w64, x64 = w.astype(np.float64), x.astype(np.float64)
+    return x64 @ w64.T, np.abs(x64) @ np.abs(w64).T
+
+
+@pytest.mark.parametrize("T,mode", [(1, 1), (5, 1), (16, 1), (16, 0), (17, 0), (300, 2), (64, 2)])
+def test_router_logits(dev, T, mode):
+    """Router matvec against fp64 (fp32 path) or fp64 over fp16-rounded
+    inputs (fp16 path); error within fp32 accumulation of |terms|."""
+    rng = np.random.default_rng(500 + T)
+    w = (rng.standard_normal((257, 2048)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((T, 2048)).astype(np.float32)
+    lg, shg = moe.router_logits(torch.from_numpy(w).to(dev), torch.from_numpy(x).to(dev), 256, mode)
+    torch.cuda.synchronize()
+    f16 = mode == 2 or (mode == 0 and T > 16)
+    ref, mag = _router_ref(w, x, f16)
+    got = np.concatenate([lg.cpu().numpy(), shg.cpu().numpy()[:, None]], axis=1).astype(np.float64)
+    err = np.abs(got - ref) / mag
+    _metrics("router_logits", T=T, mode=mode, max_rel_to_abs_terms=float(err.max()))
+    assert err.max() <= 2e-6, err.max()
+
+
+def test_router_logits_bf16_input_and_no_shared(dev):
+    rng = np.random.default_rng(77)
+    w = (rng.standard_normal((256, 2048)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((3, 2048)).astype(np.float32)
+    xb = torch.from_numpy(x).to(dev).to(torch.bfloat16)
+    lg, shg = moe.router_logits(torch.from_numpy(w).to(dev), xb, 256, 1)
+    torch.cuda.synchronize()
+    assert shg is None
+    ref, mag = _router_ref(w, xb.float().cpu().numpy(), False)
+    assert (np.abs(lg.cpu().numpy() - ref) / mag).max() <= 2e-6
