@@ -10,6 +10,8 @@ over --layers distinct seeded layers (40 x 428 MB = 17 GB by default) so the
 Workload (configs of the q36 MoE layer, hidden 2048, 256 experts, top-8,
 expert FF 512, MXFP4 weights, e4m3 activations with per-32 E8M0 scales):
   decode1      T=1, N(0,1) router logits (the headline configuration)
+  decode8      T=8, N(0,1) router logits (decode batch)
+  decode32     T=32, N(0,1) router logits (decode batch)
   ragged64     T=64, Zipf(1.1) expert popularity
   prefill4096  T=4096, N(0,1) logits
   mixed        T=4006 (6x1 decode + 3000 + 1000 prefill) + shared expert
@@ -37,6 +39,8 @@ EXPERT_BYTES = 3 * MAT_BYTES                   # gate + up + down, 1,671,168 B
 
 CONFIGS = {
     "decode1": dict(T=1, shared=False, steps=2000, warmup=200),
+    "decode8": dict(T=8, shared=False, steps=2000, warmup=200),
+    "decode32": dict(T=32, shared=False, steps=1000, warmup=100),
     "ragged64": dict(T=64, shared=False, steps=1000, warmup=100),
     "prefill4096": dict(T=4096, shared=False, steps=100, warmup=10),
     "mixed": dict(T=4006, shared=True, steps=100, warmup=10),

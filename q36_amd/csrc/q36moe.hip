@@ -1027,6 +1027,207 @@ __global__ __launch_bounds__(kGT) void k_grouped(GemmArgs A) {
 }
 
 // ---------------------------------------------------------------------------
+// fat gate/up: A and B staged in LDS by direct-to-LDS loads
+// ---------------------------------------------------------------------------
+// Workgroup = (expert tile of up to kGdTok rows, 128 rows of gate and the same
+// 128 rows of up), 8 waves.  Per K-step of 128 the workgroup stages 16 A tiles
+// (16 KiB of E2M1 fragments, contiguous in the packed layout) and the tile's
+// B rows (128 B of each e4m3 x row) with global_load_lds_dwordx4: the data
+// goes from L2 to LDS without passing through VGPRs, 8 lanes cover one
+// 128-byte x row, and three stages keep two K-steps of loads in flight.
+// Waves form a 2 x 4 grid: wave w computes gate and up tiles 4(w&1)..+3
+// (8 A fragments) against column tiles (w>>1) + 4j, so each B row in LDS is
+// read by two waves and each A fragment by four.  B rows sit in LDS as
+// 256-byte lines of two rows with the 16-byte slot index XORed by the line
+// index, so the 16 lanes of a fragment read hit 16 distinct bank groups.
+constexpr int kGdRT = 8;                         // row tiles per matrix per workgroup
+constexpr int kGdTok = 192;                      // rows per fat tile (12 column tiles)
+constexpr int kGdStages = 3;
+constexpr int kGdNJ = kGdTok / 16 / 4;           // column tiles per wave, max
+
+struct GdLds {
+    __align__(16) uint8_t a[kGdStages][2 * kGdRT * 1024];
+    __align__(16) uint8_t b[kGdStages][kGdTok * 128];
+    __align__(16) uint8_t sc[2 * kGdRT * 1024];   // A scales as packed: [tile][lane][16 K-steps]
+};
+
+__device__ __forceinline__ void dma16(const void *g, void *lds) {
+    __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 0);
+}
+
+// s_waitcnt vmcnt(n) for the few counts the pipeline needs (an immediate)
+__device__ __forceinline__ void wait_vm(int n) {
+    switch (n) {
+        case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+        case 2: asm volatile("s_waitcnt vmcnt(2)" ::: "memory"); break;
+        case 3: asm volatile("s_waitcnt vmcnt(3)" ::: "memory"); break;
+        case 4: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
+        default: asm volatile("s_waitcnt vmcnt(5)" ::: "memory"); break;
+    }
+}
+
+// Barrier for the staging pipeline.  A fence-based barrier would make the
+// compiler wait for every outstanding direct-to-LDS load (they count as LDS
+// writes), including the stages still meant to be in flight; here the wait
+// for the stage about to be read is wait_vm's, and this wave's LDS reads of
+// the previous stage are complete before any wave passes the barrier and
+// restages that slot.
+__device__ __forceinline__ void dma_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// byte offset of (row r, 16-byte chunk c) in a B stage
+__device__ __forceinline__ int gd_boff(int r, int c) {
+    const int m = r >> 1;
+    return m * 256 + ((((r & 1) << 3) | c) ^ (m & 7)) * 16;
+}
+
+template <int NJ>
+__device__ __forceinline__ void gateup_dma_body(const GemmArgs &A, GdLds &L, const uint8_t *Wg,
+                                                const uint8_t *Wu, int mt0, int p0, int p1) {
+    constexpr int KD = 2048, NKT = KD / 128;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n = lane & 15, q = lane >> 4;
+    const int wa = wave & 1, wt = wave >> 1;
+    const int ntok = p1 - p0;
+
+    // staging sources: A tiles mt0+wave of gate and of up; B row groups
+    // wave, wave+8, wave+16 (8 rows each) that hold rows of the tile
+    const uint8_t *ag = Wg + (size_t)(mt0 + wave) * NKT * 1024 + lane * 16;
+    const uint8_t *au = Wu + (size_t)(mt0 + wave) * NKT * 1024 + lane * 16;
+    const int nrg = (ntok + 7) >> 3;
+    const int nbw = nrg > wave ? (nrg - wave + 7) >> 3 : 0;
+    const uint8_t *bsrc[3];
+#pragma unroll
+    for (int i = 0; i < 3; i++) {
+        const int m = 4 * (wave + 8 * i) + (lane >> 4);      // 256-byte line
+        const int s = (lane & 15) ^ (m & 7);                  // its logical slot
+        const int r = min(2 * m + (s >> 3), ntok - 1);        // rows past the tile repeat its last
+        bsrc[i] = A.bq + (size_t)A.row_tok[p0 + r] * KD + (s & 7) * 16;
+    }
+    auto issue = [&](int kt, int st) {
+        dma16(ag + kt * 1024, &L.a[st][wave * 1024]);
+        dma16(au + kt * 1024, &L.a[st][(kGdRT + wave) * 1024]);
+#pragma unroll
+        for (int i = 0; i < 3; i++)
+            if (i < nbw) dma16(bsrc[i] + kt * 128, &L.b[st][(wave + 8 * i) * 1024]);
+    };
+    const size_t nib = (size_t)512 * KD / 2;
+    dma16(Wg + nib + ((size_t)(mt0 + wave) * 64 + lane) * 16, &L.sc[wave * 1024]);
+    dma16(Wu + nib + ((size_t)(mt0 + wave) * 64 + lane) * 16, &L.sc[(kGdRT + wave) * 1024]);
+    // B scale dwords of this wave's column tiles, all K (lane-group-major rows)
+    constexpr int NJ1 = NJ > 0 ? NJ : 1;
+    u32x4 sb[NJ1];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const int r = min(16 * (wt + 4 * j) + n, ntok - 1);
+        sb[j] = *reinterpret_cast<const u32x4 *>(A.bs2 + (size_t)A.row_tok[p0 + r] * (KD / 32) + q * 16);
+    }
+    issue(0, 0);
+    issue(1, 1);
+
+    v4f acc[8][NJ1];
+#pragma unroll
+    for (int a = 0; a < 8; a++)
+#pragma unroll
+        for (int j = 0; j < NJ; j++) acc[a][j] = v4f{0.f, 0.f, 0.f, 0.f};
+    uint32_t sa[8];
+    static_for<0, NKT>([&](auto KT) {
+        constexpr int kt = decltype(KT)::value;
+        constexpr int st = kt % kGdStages;
+        wait_vm(kt + 1 < NKT ? 2 + nbw : 0);
+        dma_barrier();
+        if constexpr (kt + 2 < NKT) issue(kt + 2, (kt + 2) % kGdStages);
+        if constexpr (kt % 4 == 0) {
+#pragma unroll
+            for (int a = 0; a < 8; a++) {
+                const int slot = (a < 4 ? 0 : kGdRT) + 4 * wa + (a & 3);
+                sa[a] = *reinterpret_cast<const uint32_t *>(&L.sc[slot * 1024 + lane * 16 + kt]);
+            }
+        }
+        u32x4 af[8];
+#pragma unroll
+        for (int a = 0; a < 8; a++) {
+            const int slot = (a < 4 ? 0 : kGdRT) + 4 * wa + (a & 3);
+            af[a] = *reinterpret_cast<const u32x4 *>(&L.a[st][slot * 1024 + lane * 16]);
+        }
+        v8i bv[NJ1];
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            const int r = 16 * (wt + 4 * j) + n;
+            const u32x4 b0 = *reinterpret_cast<const u32x4 *>(&L.b[st][gd_boff(r, q)]);
+            const u32x4 b1 = *reinterpret_cast<const u32x4 *>(&L.b[st][gd_boff(r, 4 + q)]);
+            bv[j] = v8i{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
+        }
+#pragma unroll
+        for (int a = 0; a < 8; a++) {
+            const v8i av = v8i{(int)af[a][0], (int)af[a][1], (int)af[a][2], (int)af[a][3], 0, 0, 0, 0};
+#pragma unroll
+            for (int j = 0; j < NJ; j++)
+                acc[a][j] = mfma_sel(kt & 3, av, bv[j], acc[a][j], (int)sa[a], (int)sb[j][kt >> 2]);
+        }
+    });
+
+    // SwiGLU of gate tile i and up tile i, per-32-row quantisation of h
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const int p = p0 + 16 * (wt + 4 * j) + n;
+#pragma unroll
+        for (int hb = 0; hb < 2; hb++) {
+            float h[2][4];
+            float amax = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 2; r++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    h[r][i] = silu(acc[2 * hb + r][j][i]) * acc[4 + 2 * hb + r][j][i];
+                    amax = fmaxf(amax, fabsf(h[r][i]));
+                }
+            amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+            amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+            const int e2 = quant_exp(amax);
+            const float mul = inv_scale(e2);
+            const int ffb = (mt0 + 4 * wa + 2 * hb) * 16;
+            if (p < p1) {
+#pragma unroll
+                for (int r = 0; r < 2; r++)
+                    *reinterpret_cast<uint32_t *>(A.hq + (size_t)p * A.ldo + ffb + r * 16 + 4 * q) =
+                        e4m3x4(h[r][0] * mul, h[r][1] * mul, h[r][2] * mul, h[r][3] * mul);
+                if (lane < 16) {
+                    const int b = ffb / 32, nb = A.ldo / 32;
+                    A.hs[(size_t)p * nb + b] = (uint8_t)(127 + e2);
+                    A.hs2[(size_t)p * nb + (b & 3) * (nb / 4) + (b >> 2)] = (uint8_t)(127 + e2);
+                }
+            }
+        }
+    }
+}
+
+// XCD-major order as in k_grouped: the 4 row blocks of one tile run back to
+// back on one XCD and share its L2 copy of the tile's x rows.
+__global__ __launch_bounds__(512) void k_gateup_dma(GemmArgs A) {
+    __shared__ GdLds L;
+    constexpr int NRB = 512 / (16 * kGdRT);
+    const int xcd = blockIdx.x & 7, jx = blockIdx.x >> 3;
+    const int ti = 8 * (jx / NRB) + xcd;
+    const int mt0 = (jx % NRB) * kGdRT;
+    if (ti >= *A.ntiles) return;
+    const int4 tile = A.tiles[ti];
+    const int e = tile.x, p0 = tile.y, p1 = tile.z;
+    const uint8_t *Wg = e < A.E ? A.wa + (size_t)e * A.wstride : A.sa;
+    const uint8_t *Wu = e < A.E ? A.wb + (size_t)e * A.wstride : A.sb;
+    const int ntt = (p1 - p0 + 15) >> 4;
+    const int wt = (threadIdx.x >> 6) >> 1;
+    const int nj = ntt > wt ? (ntt - wt + 3) >> 2 : 0;
+    switch (nj) {
+        case 0: gateup_dma_body<0>(A, L, Wg, Wu, mt0, p0, p1); break;
+        case 1: gateup_dma_body<1>(A, L, Wg, Wu, mt0, p0, p1); break;
+        case 2: gateup_dma_body<2>(A, L, Wg, Wu, mt0, p0, p1); break;
+        default: gateup_dma_body<3>(A, L, Wg, Wu, mt0, p0, p1); break;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // router logits (the matvec in front of the MoE step)
 // ---------------------------------------------------------------------------
 // logits[t][r] = W[r] . x[t] for r < n_expert; row n_expert (when present)
@@ -2196,8 +2397,7 @@ static void launch_stage(const q36moe_ctx *c, const Plan &P, int st, hipStream_t
             if (P.skinny)
                 hipLaunchKernelGGL(k_skinny<MODE_GATEUP>, dim3(P.tiles * 16), dim3(64 * kSkW), 0, s, P.ga);
             else
-                hipLaunchKernelGGL((k_grouped<MODE_GATEUP, kGuRT, 2048, kGuBR>),
-                                   dim3(P.tiles * (FF / (16 * kGuRT))), dim3(kGT), 0, s, P.ga);
+                hipLaunchKernelGGL(k_gateup_dma, dim3(P.tiles * (FF / (16 * kGdRT))), dim3(512), 0, s, P.ga);
             break;
         case ST_DOWN:
             if (P.skinny)
@@ -2251,7 +2451,7 @@ int q36moe_forward(q36moe_ctx *c, const q36moe_weights *w, const void *x, int x_
     // sorted path: skinny tiles (<= 32 rows) while the average expert has at
     // most kSkinnyRows rows, else fat tiles of up to kTileTok rows
     const bool skinny = pm == 4 || (pm == 0 && (size_t)n <= (size_t)kSkinnyRows * E);
-    const int tn = skinny ? kSkTok : kTileTok;
+    const int tn = skinny ? kSkTok : kGdTok;
     int tiles = n / tn + (n < E ? n : E) + (has_sh ? (T + tn - 1) / tn : 0);
     tiles = (tiles + 7) & ~7;   // whole groups of 8 for the XCD-major tile order
 
