@@ -33,6 +33,7 @@ typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 #ifdef Q36MOE_TRACE
 __device__ unsigned long long g_q36_trace[64];
+__device__ unsigned long long g_q36_clk[64];
 __device__ unsigned long long g_q36_wg[2 * 4096];
 #define Q36_TRACE_WG(n)                                                                  \
     do {                                                                                 \
@@ -41,7 +42,10 @@ __device__ unsigned long long g_q36_wg[2 * 4096];
     } while (0)
 #define Q36_TRACE_AT(n)                                                                  \
     do {                                                                                 \
-        if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) g_q36_trace[n] = wall_clock64(); \
+        if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) {                  \
+            g_q36_trace[n] = wall_clock64();                                             \
+            g_q36_clk[n] = __builtin_amdgcn_s_memtime();                                 \
+        }                                                                                \
     } while (0)
 #else
 #define Q36_TRACE_AT(n) do {} while (0)
@@ -147,15 +151,6 @@ __device__ __forceinline__ v4f mfma_f4xf8(const v8i &a, const v8i &b, const v4f 
     return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 4, 0, SEL, sa, SELB, sb);
 }
 
-// Workgroup barrier ordering LDS only.  __syncthreads() also waits for
-// every outstanding global load (s_waitcnt vmcnt(0)), which would drain the
-// prefetch rings at each K-step.
-__device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 template <int I, int N, typename F>
 __device__ __forceinline__ void static_for(F &&f) {
     if constexpr (I < N) {
@@ -176,8 +171,6 @@ __device__ __forceinline__ uint32_t logit_key(float f) {
     const uint32_t k = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
     return (u & 0x7fffffffu) > 0x7f800000u ? 0u : k;   // selects, no branch
 }
-
-__device__ __forceinline__ int popc_ballot(bool p) { return __popcll(__ballot(p)); }
 
 // Top-k routing of one token by one wavefront, without k serial rounds of
 // cross-lane argmax:
@@ -664,28 +657,6 @@ struct GemmArgs {
     int ldo;                  // output row length
 };
 
-#ifndef Q36_TILE_TOK
-#define Q36_TILE_TOK 256
-#endif
-constexpr int kTileTok = Q36_TILE_TOK;
-
-// tile shapes of the grouped GEMMs: row tiles of 16 per workgroup (per
-// matrix) and the depth of the register ring for B (K-steps)
-#ifndef Q36_GU_RT
-#define Q36_GU_RT 4
-#endif
-#ifndef Q36_GU_BR
-#define Q36_GU_BR 3
-#endif
-#ifndef Q36_DN_RT
-#define Q36_DN_RT 8
-#endif
-#ifndef Q36_DN_BR
-#define Q36_DN_BR 4
-#endif
-constexpr int kGuRT = Q36_GU_RT, kGuBR = Q36_GU_BR;
-constexpr int kDnRT = Q36_DN_RT, kDnBR = Q36_DN_BR;
-
 // op_sel byte of both scale dwords (A and B hold 4 K-steps each), fixed once
 // the K loop is unrolled
 __device__ __forceinline__ v4f mfma_sel(int sel, const v8i &a, const v8i &b, const v4f &c, int sa, int sb) {
@@ -697,373 +668,25 @@ __device__ __forceinline__ v4f mfma_sel(int sel, const v8i &a, const v8i &b, con
     }
 }
 
-#ifndef Q36_GW
-#define Q36_GW 8
-#endif
-constexpr int kGW = Q36_GW;            // waves per grouped-GEMM workgroup
-constexpr int kGT = 64 * kGW;          // threads
-
-template <int MODE, int RT, int KD>
-struct GroupedLds {
-    static constexpr int NMAT = MODE == MODE_GATEUP ? 2 : 1;
-    static constexpr int NAT = NMAT * RT;
-    static constexpr int NKT = KD / 128;
-    __align__(16) uint8_t a[2][NAT * 1024];
-    __align__(16) uint32_t sc[NAT][NKT / 4][64];   // lane-contiguous: conflict-free reads
-    int row[kTileTok];
-};
-
-#ifndef Q36_RA
-#define Q36_RA 4
-#endif
-constexpr int kRA = Q36_RA;   // depth of the register ring that carries A from HBM to LDS
-
-// NJ = number of 16-token tiles this wave owns (tiles wave, wave+kGW).
-// Pipeline per K-step kt (all rings indexed by compile-time slots: the K
-// loop is a runtime loop over groups of 4 steps, unrolled inside):
-//   1. issue B rows of step kt+BR-1 into the B register ring (and, on the
-//      first step of a group, the B scale dwords of the next group);
-//   2. issue A of step kt+kRA into the A register ring;
-//   3. MFMAs of step kt: A from LDS slot kt%2, B from the ring;
-//   4. write A of step kt+1 (loaded kRA-1 steps ago) into LDS slot (kt+1)%2;
-//   5. barrier.
-// B loads are issued before A loads in every step, so the in-order vmcnt
-// wait for the B of the current step leaves the later A loads in flight;
-// A gets kRA-1 steps of compute to arrive.  Prefetch indices are clamped to
-// the last step (redundant in-bounds loads), so the body has no branches.
-// Both scale operands come straight from loads, the byte chosen by op_sel.
-template <int MODE, int RT, int KD, int BR, int NJ>
-__device__ __forceinline__ void grouped_body(const GemmArgs &A, GroupedLds<MODE, RT, KD> &L,
-                                             const uint8_t *W0, const uint8_t *W1, int mt0, int p0,
-                                             int p1) {
-    using LT = GroupedLds<MODE, RT, KD>;
-    constexpr int NAT = LT::NAT, NKT = LT::NKT;
-    constexpr int APT = NAT * 1024 / kGT / 16;   // 16-byte A chunks per thread per K-step
-    constexpr int NJ1 = NJ > 0 ? NJ : 1;
-    constexpr int NG = NKT / 4;                  // groups of 4 K-steps
-    static_assert(NKT % 4 == 0 && BR >= 2 && kRA >= 2, "rings");
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int q = lane >> 4;
-
-    const uint8_t *asrc[APT];
-#pragma unroll
-    for (int u = 0; u < APT; u++) {
-        const int c = tid + kGT * u;
-        const int at = c >> 6;
-        const uint8_t *Wm = (LT::NMAT == 2 && at >= RT) ? W1 : W0;
-        asrc[u] = Wm + (size_t)(mt0 + at % RT) * NKT * 1024 + (c & 63) * 16;
-    }
-    // padding columns (r < 0) read row 0: they are computed but never stored,
-    // and nothing mixes columns (the h amax reduces lanes of one column)
-    const uint8_t *brp[NJ1];
-    const uint32_t *bsp[NJ1];
-#pragma unroll
-    for (int j = 0; j < NJ; j++) {
-        const int r0 = L.row[(wave + kGW * j) * 16 + (lane & 15)];
-        const int r = r0 >= 0 ? r0 : 0;
-        brp[j] = A.bq + (size_t)r * KD + q * 16;
-        bsp[j] = reinterpret_cast<const uint32_t *>(A.bs2 + (size_t)r * (KD / 32) + q * NKT);
-    }
-
-    v4f acc[NAT][NJ1];
-#pragma unroll
-    for (int a = 0; a < NAT; a++)
-#pragma unroll
-        for (int j = 0; j < NJ; j++) acc[a][j] = v4f{0.f, 0.f, 0.f, 0.f};
-
-    // Rings indexed by the (compile-time) K-step, so no register is copied
-    // between steps: a VALU write into a register that an in-flight MFMA
-    // still reads (operand or scale) stalls the wave until that MFMA is done.
-    //   B rows of step k:      bq[k % NB]     (loaded NB-1 steps ahead)
-    //   A slices of step k:    ra[k % NR]     (loaded NR-1 steps ahead, then
-    //                                          written to LDS one step ahead)
-    //   A fragments of step k: fx[k & 1]      (read from LDS one step ahead)
-    //   scale dwords:          all groups held from the start
-    constexpr int NB = BR - 1 + 1, NR = kRA;
-    u32x4 bq[NB][NJ1][2];
-    u32x4 ra[NR][APT];
-    u32x4 fx[2][NAT];
-    uint32_t scA[NG][NAT];     // A scale dwords per group of 4 K-steps
-    uint32_t scB[NG][NJ1];     // B scale dwords per group
-#pragma unroll
-    for (int g = 0; g < NG; g++) {
-#pragma unroll
-        for (int a = 0; a < NAT; a++) scA[g][a] = L.sc[a][g][lane];
-#pragma unroll
-        for (int j = 0; j < NJ; j++) scB[g][j] = bsp[j][g];
-    }
-    static_for<0, NB - 1>([&](auto R) {
-        constexpr int r = decltype(R)::value;
-#pragma unroll
-        for (int j = 0; j < NJ; j++) {
-            bq[r][j][0] = *reinterpret_cast<const u32x4 *>(brp[j] + min(r, NKT - 1) * 128);
-            bq[r][j][1] = *reinterpret_cast<const u32x4 *>(brp[j] + min(r, NKT - 1) * 128 + 64);
-        }
-    });
-    static_for<1, NR>([&](auto R) {
-        constexpr int r = decltype(R)::value;
-#pragma unroll
-        for (int u = 0; u < APT; u++)
-            ra[r][u] = *reinterpret_cast<const u32x4 *>(asrc[u] + (size_t)min(r, NKT - 1) * 1024);
-    });
-#pragma unroll
-    for (int a = 0; a < NAT; a++) fx[0][a] = *reinterpret_cast<const u32x4 *>(&L.a[0][a * 1024 + lane * 16]);
-
-    // the K loop is instantiated per step (static_for), so every ring index
-    // is a constant when the arrays are scalarised
-    static_for<0, NKT>([&](auto KT) {
-        constexpr int kt = decltype(KT)::value;
-        constexpr int ks = kt & 3, kg = kt >> 2;
-        if (MODE == MODE_GATEUP && wave == 0) Q36_TRACE_AT(30 + kt);
-        // 1. B rows of step kt+NB-1
-        if constexpr (kt + NB - 1 < NKT) {
-#pragma unroll
-            for (int j = 0; j < NJ; j++) {
-                bq[(kt + NB - 1) % NB][j][0] = *reinterpret_cast<const u32x4 *>(brp[j] + (kt + NB - 1) * 128);
-                bq[(kt + NB - 1) % NB][j][1] = *reinterpret_cast<const u32x4 *>(brp[j] + (kt + NB - 1) * 128 + 64);
-            }
-        }
-        // 2. A slices of step kt+NR
-        if constexpr (kt + NR < NKT) {
-#pragma unroll
-            for (int u = 0; u < APT; u++)
-                ra[(kt + NR) % NR][u] = *reinterpret_cast<const u32x4 *>(asrc[u] + (size_t)(kt + NR) * 1024);
-        }
-        // 3. A of step kt+1 into the other LDS slot (its last readers,
-        //    the fragment loads of step kt-1, finished before barrier kt-1)
-        if constexpr (kt + 1 < NKT) {
-#pragma unroll
-            for (int u = 0; u < APT; u++)
-                *reinterpret_cast<u32x4 *>(&L.a[(kt + 1) & 1][(tid + kGT * u) * 16]) = ra[(kt + 1) % NR][u];
-        }
-        // pin the previous step's MFMAs here: without a use they sink to the
-        // epilogue and keep every step's operands live at once; pinning one
-        // step late lets them overlap this step's loads and LDS write
-        if constexpr (kt > 0) {
-#pragma unroll
-            for (int a = 0; a < NAT; a++)
-#pragma unroll
-                for (int j = 0; j < NJ; j++) asm volatile("" : "+v"(acc[a][j]));
-        }
-        // 4. MFMAs of step kt, first half
-        v8i bv[NJ1];
-#pragma unroll
-        for (int j = 0; j < NJ; j++) {
-            const u32x4 b0 = bq[kt % NB][j][0], b1 = bq[kt % NB][j][1];
-            bv[j] = v8i{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
-        }
-        auto mfmas = [&](int a0, int a1) {
-#pragma unroll
-            for (int a = a0; a < a1; a++) {
-                const u32x4 f = fx[kt & 1][a];
-                const v8i afr = v8i{(int)f[0], (int)f[1], (int)f[2], (int)f[3], 0, 0, 0, 0};
-#pragma unroll
-                for (int j = 0; j < NJ; j++)
-                    acc[a][j] = mfma_sel(ks, afr, bv[j], acc[a][j], (int)scA[kg][a], (int)scB[kg][j]);
-            }
-        };
-        mfmas(0, NAT / 2);
-        // 5. barrier: step kt+1's A slot is complete (the first half stays
-        //    before it: the scheduler would otherwise sink those MFMAs past
-        //    the barrier, which orders memory only)
-        if constexpr (kt + 1 < NKT) {
-            __builtin_amdgcn_sched_barrier(0);
-            lds_barrier();
-            __builtin_amdgcn_sched_barrier(0);
-            // 6. step kt+1's A fragments
-#pragma unroll
-            for (int a = 0; a < NAT; a++)
-                fx[(kt + 1) & 1][a] = *reinterpret_cast<const u32x4 *>(&L.a[(kt + 1) & 1][a * 1024 + lane * 16]);
-            __builtin_amdgcn_sched_barrier(0);   // issue those reads before the second half
-        }
-        // 7. second half
-        mfmas(NAT / 2, NAT);
-    });
-
-    if (MODE == MODE_GATEUP && wave == 0) Q36_TRACE_AT(47);
-    if constexpr (MODE == MODE_GATEUP) {
-#pragma unroll
-        for (int j = 0; j < NJ; j++) {
-            const int p = p0 + (wave + kGW * j) * 16 + (lane & 15);
-#pragma unroll
-            for (int hb = 0; hb < RT / 2; hb++) {
-                float h[2][4];
-                float amax = 0.0f;
-#pragma unroll
-                for (int r = 0; r < 2; r++)
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        h[r][i] = silu(acc[2 * hb + r][j][i]) * acc[RT + 2 * hb + r][j][i];
-                        amax = fmaxf(amax, fabsf(h[r][i]));
-                    }
-                amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
-                amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
-                const int e2 = quant_exp(amax);
-                const float mul = inv_scale(e2);
-                const int ffb = (mt0 + 2 * hb) * 16;
-                if (p < p1) {
-#pragma unroll
-                    for (int r = 0; r < 2; r++) {
-                        const uint32_t w = e4m3x4(h[r][0] * mul, h[r][1] * mul, h[r][2] * mul,
-                                                  h[r][3] * mul);
-                        *reinterpret_cast<uint32_t *>(A.hq + (size_t)p * A.ldo + ffb + r * 16 + 4 * q) = w;
-                    }
-                    if (lane < 16) {
-                        const int b = ffb / 32, nb = A.ldo / 32;
-                        A.hs[(size_t)p * nb + b] = (uint8_t)(127 + e2);
-                        A.hs2[(size_t)p * nb + (b & 3) * (nb / 4) + (b >> 2)] = (uint8_t)(127 + e2);
-                    }
-                }
-            }
-        }
-    } else {
-#pragma unroll
-        for (int j = 0; j < NJ; j++) {
-            const int p = p0 + (wave + kGW * j) * 16 + (lane & 15);
-            if (p >= p1) continue;
-            const float w = A.row_w[p];
-#pragma unroll
-            for (int a = 0; a < RT; a++) {
-                const int row = (mt0 + a) * 16 + 4 * q;
-                const v4f c = acc[a][j];
-                *reinterpret_cast<float4 *>(A.dnw + (size_t)p * A.ldo + row) =
-                    make_float4(c[0] * w, c[1] * w, c[2] * w, c[3] * w);
-            }
-        }
-    }
-}
-
-// Grouped expert GEMM, one workgroup per (expert tile, row block).  The
-// tile holds every routed row of one expert up to kTileTok (longer experts
-// are split), so an expert's weights leave HBM once per row block.  A
-// (E2M1 fragments of NAT row tiles, NAT KB per K-step of 128) reaches LDS
-// through a register ring; B (e4m3 rows) goes straight to the registers of
-// the wave that owns those 16-token tiles (tiles w and w+8 of wave w); A
-// scales for all K sit in LDS from the start.
-// GATEUP: A tiles 0..RT-1 are gate rows, RT..2RT-1 the same up rows; the
-// epilogue applies SwiGLU and quantises h per 32 rows.  DOWN: RT row tiles
-// of the output, scaled by the routing weight into the staging rows.
-template <int MODE, int RT, int KD, int BR>
-__global__ __launch_bounds__(kGT) void k_grouped(GemmArgs A) {
-    using LT = GroupedLds<MODE, RT, KD>;
-    constexpr int NAT = LT::NAT, NKT = LT::NKT;
-    static_assert((NAT * 1024) % (kGT * 16) == 0, "A stage");
-    static_assert(MODE != MODE_GATEUP || RT % 2 == 0, "h blocks of 32 rows");
-    __shared__ LT L;
-
-    // XCD-major order: workgroups are dealt to the 8 XCDs round-robin
-    // (linear id % 8), so the j-th workgroup of XCD x takes row block
-    // j % NRB of tile 8 * (j / NRB) + x: the row blocks of one tile run
-    // back to back on one XCD and share its L2 copy of the tile's B rows.
-    constexpr int NRB = (MODE == MODE_GATEUP ? 512 : 2048) / (16 * RT);
-    const int xcd = blockIdx.x & 7, jx = blockIdx.x >> 3;
-    const int ti = 8 * (jx / NRB) + xcd;
-    const int mt0 = (jx % NRB) * RT;
-    if (ti >= *A.ntiles) return;
-    Q36_TRACE_WG(0);
-    if (MODE == MODE_GATEUP) Q36_TRACE_AT(28);
-    const int4 tile = A.tiles[ti];
-    const int e = tile.x, p0 = tile.y, p1 = tile.z;
-    const int tid = threadIdx.x, wave = tid >> 6;
-    const size_t nib_bytes = (size_t)A.M * KD / 2;
-    const uint8_t *W0 = e < A.E ? A.wa + (size_t)e * A.wstride : A.sa;
-    const uint8_t *W1 = W0;
-    if constexpr (LT::NMAT == 2) W1 = e < A.E ? A.wb + (size_t)e * A.wstride : A.sb;
-
-    // A scales for all K of this row block: per matrix a contiguous
-    // [row tile][lane][K/128] byte block, stored transposed as
-    // sc[tile][group of 4 K-steps][lane]
-    {
-        constexpr int G = NKT / 4, SBD = RT * 64 * G;   // dwords per matrix
-        for (int c = tid; c < LT::NMAT * SBD / 4; c += kGT) {
-            const int m = c / (SBD / 4), d0 = (c % (SBD / 4)) * 4;
-            const uint4 v = *reinterpret_cast<const uint4 *>((m == 0 ? W0 : W1) + nib_bytes +
-                                                             (size_t)mt0 * 64 * NKT + (size_t)d0 * 4);
-            const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const int d = d0 + u, at = d / (64 * G), ln = (d / G) % 64, g = d % G;
-                L.sc[m * RT + at][g][ln] = vv[u];
-            }
-        }
-    }
-    for (int i = tid; i < kTileTok; i += kGT) {
-        const int p = p0 + i;
-        L.row[i] = p < p1 ? (MODE == MODE_GATEUP ? A.row_tok[p] : p) : -1;
-    }
-    // A of K-step 0
-    {
-        constexpr int APT = NAT * 1024 / kGT / 16;
-#pragma unroll
-        for (int u = 0; u < APT; u++) {
-            const int c = tid + kGT * u;
-            const int at = c >> 6;
-            const uint8_t *Wm = (LT::NMAT == 2 && at >= RT) ? W1 : W0;
-            *reinterpret_cast<uint4 *>(&L.a[0][c * 16]) = *reinterpret_cast<const uint4 *>(
-                Wm + (size_t)(mt0 + at % RT) * NKT * 1024 + (c & 63) * 16);
-        }
-    }
-    __syncthreads();
-    if (MODE == MODE_GATEUP) Q36_TRACE_AT(29);
-    const int ntt = (p1 - p0 + 15) >> 4;
-    static_assert(kTileTok % (16 * kGW) == 0 && kTileTok <= 4 * 16 * kGW, "1..4 token tiles per wave");
-    const int nj = ntt > wave ? (ntt - wave + kGW - 1) / kGW : 0;
-    constexpr int NJMAX = kTileTok / (16 * kGW);
-    switch (nj) {
-        case 0: grouped_body<MODE, RT, KD, BR, 0>(A, L, W0, W1, mt0, p0, p1); break;
-        case 1: grouped_body<MODE, RT, KD, BR, 1>(A, L, W0, W1, mt0, p0, p1); break;
-        case 2:
-            if constexpr (NJMAX >= 2) grouped_body<MODE, RT, KD, BR, 2>(A, L, W0, W1, mt0, p0, p1);
-            break;
-        case 3:
-            if constexpr (NJMAX >= 3) grouped_body<MODE, RT, KD, BR, 3>(A, L, W0, W1, mt0, p0, p1);
-            break;
-        default:
-            if constexpr (NJMAX >= 4) grouped_body<MODE, RT, KD, BR, 4>(A, L, W0, W1, mt0, p0, p1);
-            break;
-    }
-    if (MODE == MODE_GATEUP) Q36_TRACE_AT(46);
-    Q36_TRACE_WG(1);
-}
-
 // ---------------------------------------------------------------------------
 // fat gate/up: A and B staged in LDS by direct-to-LDS loads
 // ---------------------------------------------------------------------------
-// Workgroup = (expert tile of up to kGdTok rows, 128 rows of gate and the same
-// 128 rows of up), 8 waves.  Per K-step of 128 the workgroup stages 16 A tiles
-// (16 KiB of E2M1 fragments, contiguous in the packed layout) and the tile's
-// B rows (128 B of each e4m3 x row) with global_load_lds_dwordx4: the data
-// goes from L2 to LDS without passing through VGPRs, 8 lanes cover one
-// 128-byte x row, and three stages keep two K-steps of loads in flight.
-// Waves form a 2 x 4 grid: wave w computes gate and up tiles 4(w&1)..+3
-// (8 A fragments) against column tiles (w>>1) + 4j, so each B row in LDS is
-// read by two waves and each A fragment by four.  B rows sit in LDS as
-// 256-byte lines of two rows with the 16-byte slot index XORed by the line
-// index, so the 16 lanes of a fragment read hit 16 distinct bank groups.
-constexpr int kGdRT = 8;                         // row tiles per matrix per workgroup
+// Workgroup = (expert tile of up to kGdTok rows, 64 rows of gate and the same
+// 64 rows of up), 4 waves, two workgroups per CU: while one waits at its
+// per-step barrier the other keeps the matrix pipes busy.  Per K-step of 128
+// the workgroup stages 8 A tiles (8 KiB of E2M1 fragments, contiguous in the
+// packed layout) and the tile's B rows (128 B of each e4m3 x row) with
+// global_load_lds_dwordx4: the data goes from L2 to LDS without passing
+// through VGPRs, and 8 lanes cover one 128-byte x row.  A streams from HBM
+// with three stages (two K-steps in flight); B mostly hits L2 and has two.
+// Waves form a 2 x 2 grid: wave w computes gate and up tiles 2(w&1)..+1
+// against column tiles (w>>1) + 2j.  B rows sit in LDS as 256-byte lines of
+// two rows with the 16-byte slot index XORed by the line index, so the 16
+// lanes of a fragment read hit 16 distinct bank groups.
 constexpr int kGdTok = 192;                      // rows per fat tile (12 column tiles)
-constexpr int kGdStages = 3;
-constexpr int kGdNJ = kGdTok / 16 / 4;           // column tiles per wave, max
-
-struct GdLds {
-    __align__(16) uint8_t a[kGdStages][2 * kGdRT * 1024];
-    __align__(16) uint8_t b[kGdStages][kGdTok * 128];
-    __align__(16) uint8_t sc[2 * kGdRT * 1024];   // A scales as packed: [tile][lane][16 K-steps]
-};
 
 __device__ __forceinline__ void dma16(const void *g, void *lds) {
     __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 0);
-}
-
-// s_waitcnt vmcnt(n) for the few counts the pipeline needs (an immediate)
-__device__ __forceinline__ void wait_vm(int n) {
-    switch (n) {
-        case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
-        case 2: asm volatile("s_waitcnt vmcnt(2)" ::: "memory"); break;
-        case 3: asm volatile("s_waitcnt vmcnt(3)" ::: "memory"); break;
-        case 4: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
-        default: asm volatile("s_waitcnt vmcnt(5)" ::: "memory"); break;
-    }
 }
 
 // Barrier for the staging pipeline.  A fence-based barrier would make the
@@ -1073,7 +696,11 @@ __device__ __forceinline__ void wait_vm(int n) {
 // the previous stage are complete before any wave passes the barrier and
 // restages that slot.
 __device__ __forceinline__ void dma_barrier() {
+    // the scheduler may move MFMAs across an asm barrier: pin them (and all
+    // else) to their step, or every step's fragments stay live at once
+    __builtin_amdgcn_sched_barrier(0);
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
 }
 
 // byte offset of (row r, 16-byte chunk c) in a B stage
@@ -1082,135 +709,175 @@ __device__ __forceinline__ int gd_boff(int r, int c) {
     return m * 256 + ((((r & 1) << 3) | c) ^ (m & 7)) * 16;
 }
 
+namespace gdma {
+constexpr int RT = 4, W = 4, TOK = kGdTok;
+constexpr int STA = 3, STB = 2;
+struct Lds {
+    __align__(16) uint8_t a[STA][2 * RT * 1024];
+    __align__(16) uint8_t b[STB][TOK * 128];
+    __align__(16) uint8_t sc[2 * RT * 1024];
+};
+static_assert(sizeof(Lds) * 2 <= 160 * 1024, "two workgroups per CU");
+
+__device__ __forceinline__ void wait_vm(int n) {
+    if (n == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+}
+
 template <int NJ>
-__device__ __forceinline__ void gateup_dma_body(const GemmArgs &A, GdLds &L, const uint8_t *Wg,
-                                                const uint8_t *Wu, int mt0, int p0, int p1) {
+__device__ __forceinline__ void body(const GemmArgs &A, Lds &L, const uint8_t *Wg, const uint8_t *Wu,
+                                     int mt0, int p0, int p1) {
     constexpr int KD = 2048, NKT = KD / 128;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n = lane & 15, q = lane >> 4;
     const int wa = wave & 1, wt = wave >> 1;
     const int ntok = p1 - p0;
-
-    // staging sources: A tiles mt0+wave of gate and of up; B row groups
-    // wave, wave+8, wave+16 (8 rows each) that hold rows of the tile
-    const uint8_t *ag = Wg + (size_t)(mt0 + wave) * NKT * 1024 + lane * 16;
-    const uint8_t *au = Wu + (size_t)(mt0 + wave) * NKT * 1024 + lane * 16;
+    // A: wave w stages gate tile mt0+w and up tile mt0+w; B: row groups
+    // w + 4i (8 rows each) holding rows of the tile.  Sources are a uniform
+    // base plus a 32-bit per-lane offset (the saddr form of the load).
+    const uint32_t aoff = (uint32_t)(mt0 + wave) * NKT * 1024 + lane * 16;
     const int nrg = (ntok + 7) >> 3;
-    const int nbw = nrg > wave ? (nrg - wave + 7) >> 3 : 0;
-    const uint8_t *bsrc[3];
+    const int nbw = nrg > wave ? (nrg - wave + W - 1) / W : 0;
+    constexpr int NBI = TOK / 8 / W;
+    uint32_t boff[NBI];
 #pragma unroll
-    for (int i = 0; i < 3; i++) {
-        const int m = 4 * (wave + 8 * i) + (lane >> 4);      // 256-byte line
-        const int s = (lane & 15) ^ (m & 7);                  // its logical slot
-        const int r = min(2 * m + (s >> 3), ntok - 1);        // rows past the tile repeat its last
-        bsrc[i] = A.bq + (size_t)A.row_tok[p0 + r] * KD + (s & 7) * 16;
+    for (int i = 0; i < NBI; i++) {
+        const int m = 4 * (wave + W * i) + (lane >> 4);
+        const int s = (lane & 15) ^ (m & 7);
+        const int r = min(2 * m + (s >> 3), ntok - 1);
+        boff[i] = (uint32_t)A.row_tok[p0 + r] * KD + (s & 7) * 16;
     }
-    auto issue = [&](int kt, int st) {
-        dma16(ag + kt * 1024, &L.a[st][wave * 1024]);
-        dma16(au + kt * 1024, &L.a[st][(kGdRT + wave) * 1024]);
+    auto issue_a = [&](int kt, int slot) {
+        dma16(Wg + (aoff + kt * 1024), &L.a[slot][wave * 1024]);
+        dma16(Wu + (aoff + kt * 1024), &L.a[slot][(RT + wave) * 1024]);
+    };
+    auto issue_b = [&](int kt, int slot) {
 #pragma unroll
-        for (int i = 0; i < 3; i++)
-            if (i < nbw) dma16(bsrc[i] + kt * 128, &L.b[st][(wave + 8 * i) * 1024]);
+        for (int i = 0; i < NBI; i++)
+            if (i < nbw) dma16(A.bq + (boff[i] + kt * 128), &L.b[slot][(wave + W * i) * 1024]);
     };
     const size_t nib = (size_t)512 * KD / 2;
     dma16(Wg + nib + ((size_t)(mt0 + wave) * 64 + lane) * 16, &L.sc[wave * 1024]);
-    dma16(Wu + nib + ((size_t)(mt0 + wave) * 64 + lane) * 16, &L.sc[(kGdRT + wave) * 1024]);
-    // B scale dwords of this wave's column tiles, all K (lane-group-major rows)
+    dma16(Wu + nib + ((size_t)(mt0 + wave) * 64 + lane) * 16, &L.sc[(RT + wave) * 1024]);
     constexpr int NJ1 = NJ > 0 ? NJ : 1;
     u32x4 sb[NJ1];
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
-        const int r = min(16 * (wt + 4 * j) + n, ntok - 1);
+        const int r = min(16 * (wt + 2 * j) + n, ntok - 1);
         sb[j] = *reinterpret_cast<const u32x4 *>(A.bs2 + (size_t)A.row_tok[p0 + r] * (KD / 32) + q * 16);
     }
-    issue(0, 0);
-    issue(1, 1);
+    // step kt issues B(kt+1) then A(kt+2) after its MFMAs; when step kt
+    // needs B(kt), only A(kt+1) was issued after it
+    issue_a(0, 0);
+    issue_b(0, 0);
+    issue_a(1, 1);
 
-    v4f acc[8][NJ1];
+    v4f acc[4][NJ1];
 #pragma unroll
-    for (int a = 0; a < 8; a++)
+    for (int a = 0; a < 4; a++)
 #pragma unroll
         for (int j = 0; j < NJ; j++) acc[a][j] = v4f{0.f, 0.f, 0.f, 0.f};
-    uint32_t sa[8];
-    static_for<0, NKT>([&](auto KT) {
-        constexpr int kt = decltype(KT)::value;
-        constexpr int st = kt % kGdStages;
-        wait_vm(kt + 1 < NKT ? 2 + nbw : 0);
-        dma_barrier();
-        if constexpr (kt + 2 < NKT) issue(kt + 2, (kt + 2) % kGdStages);
-        if constexpr (kt % 4 == 0) {
+    uint32_t sa[4];
+    uint32_t sbg[NJ1];
+    int sla = 0;          // A stage of the current step
+#pragma unroll 1
+    for (int g = 0; g < NKT / 4; g++) {
 #pragma unroll
-            for (int a = 0; a < 8; a++) {
-                const int slot = (a < 4 ? 0 : kGdRT) + 4 * wa + (a & 3);
-                sa[a] = *reinterpret_cast<const uint32_t *>(&L.sc[slot * 1024 + lane * 16 + kt]);
+        for (int j = 0; j < NJ; j++) sbg[j] = g == 0 ? sb[j][0] : g == 1 ? sb[j][1] : g == 2 ? sb[j][2] : sb[j][3];
+        static_for<0, 4>([&](auto S) {
+            constexpr int st = decltype(S)::value;
+            const int kt = 4 * g + st;
+            // pin the previous step's MFMAs before the barrier: the compiler
+            // would otherwise sink them to the end and keep every step's
+            // fragments live at once
+#pragma unroll
+            for (int a = 0; a < 4; a++)
+#pragma unroll
+                for (int j = 0; j < NJ; j++) asm volatile("" : "+v"(acc[a][j]));
+            wait_vm(kt + 1 < NKT ? 2 : 0);
+            dma_barrier();
+            if constexpr (st == 0) {
+#pragma unroll
+                for (int a = 0; a < 4; a++) {
+                    const int slot = (a < 2 ? 0 : RT) + 2 * wa + (a & 1);
+                    sa[a] = *reinterpret_cast<const uint32_t *>(&L.sc[slot * 1024 + lane * 16 + 4 * g]);
+                }
             }
-        }
-        u32x4 af[8];
+            // A fragments first (4, held for the step), then column tile j's
+            // B fragment is read while the MFMAs of tile j-1 run
+            u32x4 af[4];
 #pragma unroll
-        for (int a = 0; a < 8; a++) {
-            const int slot = (a < 4 ? 0 : kGdRT) + 4 * wa + (a & 3);
-            af[a] = *reinterpret_cast<const u32x4 *>(&L.a[st][slot * 1024 + lane * 16]);
-        }
-        v8i bv[NJ1];
+            for (int a = 0; a < 4; a++) {
+                const int slot = (a < 2 ? 0 : RT) + 2 * wa + (a & 1);
+                af[a] = *reinterpret_cast<const u32x4 *>(&L.a[sla][slot * 1024 + lane * 16]);
+            }
 #pragma unroll
-        for (int j = 0; j < NJ; j++) {
-            const int r = 16 * (wt + 4 * j) + n;
-            const u32x4 b0 = *reinterpret_cast<const u32x4 *>(&L.b[st][gd_boff(r, q)]);
-            const u32x4 b1 = *reinterpret_cast<const u32x4 *>(&L.b[st][gd_boff(r, 4 + q)]);
-            bv[j] = v8i{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
-        }
+            for (int j = 0; j < NJ; j++) {
+                const int r = 16 * (wt + 2 * j) + n;
+                const u32x4 b0 = *reinterpret_cast<const u32x4 *>(&L.b[st & 1][gd_boff(r, q)]);
+                const u32x4 b1 = *reinterpret_cast<const u32x4 *>(&L.b[st & 1][gd_boff(r, 4 + q)]);
+                const v8i bv = v8i{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
 #pragma unroll
-        for (int a = 0; a < 8; a++) {
-            const v8i av = v8i{(int)af[a][0], (int)af[a][1], (int)af[a][2], (int)af[a][3], 0, 0, 0, 0};
+                for (int a = 0; a < 4; a++) {
+                    const v8i av = v8i{(int)af[a][0], (int)af[a][1], (int)af[a][2], (int)af[a][3], 0, 0, 0, 0};
+                    acc[a][j] = mfma_f4xf8<st, st>(av, bv, acc[a][j], (int)sa[a], (int)sbg[j]);
+                }
+            }
+            if constexpr (NJ > 0) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 4 + 2 + (st == 0 ? 4 : 0), 0);
 #pragma unroll
-            for (int j = 0; j < NJ; j++)
-                acc[a][j] = mfma_sel(kt & 3, av, bv[j], acc[a][j], (int)sa[a], (int)sb[j][kt >> 2]);
-        }
-    });
+                for (int j = 0; j < NJ; j++) {
+                    if (j + 1 < NJ) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+                }
+            }
+            // restage the slots read in the previous step
+            if (kt + 1 < NKT) issue_b(kt + 1, (st + 1) & 1);
+            if (kt + 2 < NKT) issue_a(kt + 2, sla == 0 ? 2 : sla - 1);
+            sla = sla == 2 ? 0 : sla + 1;
+        });
+    }
 
-    // SwiGLU of gate tile i and up tile i, per-32-row quantisation of h
+    // SwiGLU of gate tile i and up tile i (i = 0, 1: one 32-row h block)
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
-        const int p = p0 + 16 * (wt + 4 * j) + n;
+        const int p = p0 + 16 * (wt + 2 * j) + n;
+        float h[2][4];
+        float amax = 0.0f;
 #pragma unroll
-        for (int hb = 0; hb < 2; hb++) {
-            float h[2][4];
-            float amax = 0.0f;
+        for (int r = 0; r < 2; r++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                h[r][i] = silu(acc[r][j][i]) * acc[2 + r][j][i];
+                amax = fmaxf(amax, fabsf(h[r][i]));
+            }
+        amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+        amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+        const int e2 = quant_exp(amax);
+        const float mul = inv_scale(e2);
+        const int ffb = (mt0 + 2 * wa) * 16;
+        if (p < p1) {
 #pragma unroll
             for (int r = 0; r < 2; r++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    h[r][i] = silu(acc[2 * hb + r][j][i]) * acc[4 + 2 * hb + r][j][i];
-                    amax = fmaxf(amax, fabsf(h[r][i]));
-                }
-            amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
-            amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
-            const int e2 = quant_exp(amax);
-            const float mul = inv_scale(e2);
-            const int ffb = (mt0 + 4 * wa + 2 * hb) * 16;
-            if (p < p1) {
-#pragma unroll
-                for (int r = 0; r < 2; r++)
-                    *reinterpret_cast<uint32_t *>(A.hq + (size_t)p * A.ldo + ffb + r * 16 + 4 * q) =
-                        e4m3x4(h[r][0] * mul, h[r][1] * mul, h[r][2] * mul, h[r][3] * mul);
-                if (lane < 16) {
-                    const int b = ffb / 32, nb = A.ldo / 32;
-                    A.hs[(size_t)p * nb + b] = (uint8_t)(127 + e2);
-                    A.hs2[(size_t)p * nb + (b & 3) * (nb / 4) + (b >> 2)] = (uint8_t)(127 + e2);
-                }
+                *reinterpret_cast<uint32_t *>(A.hq + (size_t)p * A.ldo + ffb + r * 16 + 4 * q) =
+                    e4m3x4(h[r][0] * mul, h[r][1] * mul, h[r][2] * mul, h[r][3] * mul);
+            if (lane < 16) {
+                const int b = ffb / 32, nb = A.ldo / 32;
+                A.hs[(size_t)p * nb + b] = (uint8_t)(127 + e2);
+                A.hs2[(size_t)p * nb + (b & 3) * (nb / 4) + (b >> 2)] = (uint8_t)(127 + e2);
             }
         }
     }
 }
+}  // namespace gdma
 
-// XCD-major order as in k_grouped: the 4 row blocks of one tile run back to
-// back on one XCD and share its L2 copy of the tile's x rows.
-__global__ __launch_bounds__(512) void k_gateup_dma(GemmArgs A) {
-    __shared__ GdLds L;
-    constexpr int NRB = 512 / (16 * kGdRT);
+__global__ __launch_bounds__(256, 2) void k_gateup_dma(GemmArgs A) {
+    __shared__ gdma::Lds L;
+    constexpr int NRB = 512 / (16 * gdma::RT);
     const int xcd = blockIdx.x & 7, jx = blockIdx.x >> 3;
     const int ti = 8 * (jx / NRB) + xcd;
-    const int mt0 = (jx % NRB) * kGdRT;
+    const int mt0 = (jx % NRB) * gdma::RT;
     if (ti >= *A.ntiles) return;
     const int4 tile = A.tiles[ti];
     const int e = tile.x, p0 = tile.y, p1 = tile.z;
@@ -1218,12 +885,15 @@ __global__ __launch_bounds__(512) void k_gateup_dma(GemmArgs A) {
     const uint8_t *Wu = e < A.E ? A.wb + (size_t)e * A.wstride : A.sb;
     const int ntt = (p1 - p0 + 15) >> 4;
     const int wt = (threadIdx.x >> 6) >> 1;
-    const int nj = ntt > wt ? (ntt - wt + 3) >> 2 : 0;
+    const int nj = ntt > wt ? (ntt - wt + 1) >> 1 : 0;
     switch (nj) {
-        case 0: gateup_dma_body<0>(A, L, Wg, Wu, mt0, p0, p1); break;
-        case 1: gateup_dma_body<1>(A, L, Wg, Wu, mt0, p0, p1); break;
-        case 2: gateup_dma_body<2>(A, L, Wg, Wu, mt0, p0, p1); break;
-        default: gateup_dma_body<3>(A, L, Wg, Wu, mt0, p0, p1); break;
+        case 0: gdma::body<0>(A, L, Wg, Wu, mt0, p0, p1); break;
+        case 1: gdma::body<1>(A, L, Wg, Wu, mt0, p0, p1); break;
+        case 2: gdma::body<2>(A, L, Wg, Wu, mt0, p0, p1); break;
+        case 3: gdma::body<3>(A, L, Wg, Wu, mt0, p0, p1); break;
+        case 4: gdma::body<4>(A, L, Wg, Wu, mt0, p0, p1); break;
+        case 5: gdma::body<5>(A, L, Wg, Wu, mt0, p0, p1); break;
+        default: gdma::body<6>(A, L, Wg, Wu, mt0, p0, p1); break;
     }
 }
 
@@ -1507,7 +1177,7 @@ __device__ __forceinline__ void skinny_down(const GemmArgs &A, const uint8_t *W,
     }
 }
 
-// XCD-major order as in k_grouped: the 16 row blocks of one tile run back to
+// XCD-major order: the 16 row blocks of one tile run back to
 // back on one XCD.
 template <int MODE>
 __global__ __launch_bounds__(64 * kSkW) void k_skinny(GemmArgs A) {
@@ -1540,14 +1210,15 @@ __global__ __launch_bounds__(64 * kSkW) void k_skinny(GemmArgs A) {
 // then each wave walks the 16-row column tiles, reading each B fragment once
 // for 4 MFMAs, and stores the finished column tile (x routing weight) before
 // the next: no accumulator outlives its column tile.
-//   workgroup = (tile, 256 output rows), 4 waves; tiles longer than 128 rows
-//   are staged in chunks of 128.
+//   workgroup = (tile, 256 output rows), 4 waves of 4 row tiles each; tiles
+//   longer than 128 rows are staged in chunks of 128.
 constexpr int kDlW = 4;                  // waves
+constexpr int kDlRT = 4;                 // row tiles per wave
 constexpr int kDlRows = 128;             // B rows staged per chunk
 constexpr int kDlStride = 512 + 16;      // LDS row stride: conflict-free fragment reads
 
 __global__ __launch_bounds__(64 * kDlW) void k_down_lds(GemmArgs A) {
-    constexpr int KD = 512, NKT = KD / 128, NRB = 2048 / 256;
+    constexpr int KD = 512, NKT = KD / 128, NRB = 2048 / (16 * kDlRT * kDlW);
     __shared__ __align__(16) uint8_t sb[kDlRows * kDlStride];
     __shared__ uint32_t ss[kDlRows][4];       // B scale dwords: [row][lane group]
     __shared__ float ws[kDlRows];             // routing weight of each row
@@ -1561,12 +1232,12 @@ __global__ __launch_bounds__(64 * kDlW) void k_down_lds(GemmArgs A) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q = lane >> 4, n = lane & 15;
     const uint8_t *W = e < A.E ? A.wa + (size_t)e * A.wstride : A.sa;
     const size_t nib = (size_t)2048 * KD / 2;
-    // this wave's A: row tiles rb*16 + 4*wave + i, all 4 K-steps
-    const int mt0 = rb * 16 + 4 * wave;
-    u32x4 af[4][NKT];
-    uint32_t sa[4];
+    // this wave's A: row tiles mt0 + i, all 4 K-steps
+    const int mt0 = (rb * kDlW + wave) * kDlRT;
+    u32x4 af[kDlRT][NKT];
+    uint32_t sa[kDlRT];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
+    for (int i = 0; i < kDlRT; i++) {
 #pragma unroll
         for (int kt = 0; kt < NKT; kt++)
             af[i][kt] = *reinterpret_cast<const u32x4 *>(W + ((size_t)(mt0 + i) * NKT + kt) * 1024 + lane * 16);
@@ -1614,13 +1285,13 @@ __global__ __launch_bounds__(64 * kDlW) void k_down_lds(GemmArgs A) {
                 bv[kt] = v8i{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
             }
             const uint32_t sbw = ss[r][q];
-            v4f acc[4];
+            v4f acc[kDlRT];
 #pragma unroll
-            for (int i = 0; i < 4; i++) acc[i] = v4f{0.f, 0.f, 0.f, 0.f};
+            for (int i = 0; i < kDlRT; i++) acc[i] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int kt = 0; kt < NKT; kt++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
+                for (int i = 0; i < kDlRT; i++) {
                     const u32x4 f = af[i][kt];
                     const v8i av = v8i{(int)f[0], (int)f[1], (int)f[2], (int)f[3], 0, 0, 0, 0};
                     acc[i] = mfma_sel(kt, av, bv[kt], acc[i], (int)sa[i], (int)sbw);
@@ -1629,7 +1300,7 @@ __global__ __launch_bounds__(64 * kDlW) void k_down_lds(GemmArgs A) {
                 const int p = c0 + j * 16 + n;
                 const float w = ws[j * 16 + n];
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
+                for (int i = 0; i < kDlRT; i++) {
                     const v4f c = acc[i];
                     *reinterpret_cast<float4 *>(A.dnw + (size_t)p * A.ldo + (mt0 + i) * 16 + 4 * q) =
                         make_float4(c[0] * w, c[1] * w, c[2] * w, c[3] * w);
@@ -2397,13 +2068,14 @@ static void launch_stage(const q36moe_ctx *c, const Plan &P, int st, hipStream_t
             if (P.skinny)
                 hipLaunchKernelGGL(k_skinny<MODE_GATEUP>, dim3(P.tiles * 16), dim3(64 * kSkW), 0, s, P.ga);
             else
-                hipLaunchKernelGGL(k_gateup_dma, dim3(P.tiles * (FF / (16 * kGdRT))), dim3(512), 0, s, P.ga);
+                hipLaunchKernelGGL(k_gateup_dma, dim3(P.tiles * (FF / (16 * gdma::RT))), dim3(64 * gdma::W), 0, s,
+                                   P.ga);
             break;
         case ST_DOWN:
             if (P.skinny)
                 hipLaunchKernelGGL(k_skinny<MODE_DOWN>, dim3(P.tiles * 16), dim3(64 * kSkW), 0, s, P.da);
             else
-                hipLaunchKernelGGL(k_down_lds, dim3(P.tiles * (D / 256)), dim3(64 * kDlW), 0, s, P.da);
+                hipLaunchKernelGGL(k_down_lds, dim3(P.tiles * (D / (16 * kDlRT * kDlW))), dim3(64 * kDlW), 0, s, P.da);
             break;
         case ST_COMBINE:
             hipLaunchKernelGGL(k_combine, dim3(T), dim3(256), 0, s, c->dnw, c->pos, T, K, D, P.has_sh,
@@ -2449,7 +2121,7 @@ int q36moe_forward(q36moe_ctx *c, const q36moe_weights *w, const void *x, int x_
                                                                                       : (T <= kDirectMaxT);
     if ((pm == 2 || pm == 3) && !direct) return Q36MOE_EINVAL;
     // sorted path: skinny tiles (<= 32 rows) while the average expert has at
-    // most kSkinnyRows rows, else fat tiles of up to kTileTok rows
+    // most kSkinnyRows rows, else fat tiles of up to kGdTok rows
     const bool skinny = pm == 4 || (pm == 0 && (size_t)n <= (size_t)kSkinnyRows * E);
     const int tn = skinny ? kSkTok : kGdTok;
     int tiles = n / tn + (n < E ? n : E) + (has_sh ? (T + tn - 1) / tn : 0);

@@ -400,6 +400,19 @@ def test_forward_ragged64_zipf(dev, oracle, layer_w, path):
     _check_layer("ragged64", dev, oracle, layer_w, x, lg, None, path=path)
 
 
+def test_forward_fat_skewed(dev, oracle, layer_w):
+    """Fat-tile path with Zipf routing at T=700: the most popular experts hold
+    more rows than one fat tile (split tiles), the tail holds 0-2 rows, so
+    every column-tile count per wave occurs."""
+    rng = np.random.default_rng(66)
+    x, lg = synth.hidden(rng, 700), synth.zipf_logits(rng, 700)
+    counts = np.bincount(np.argsort(-lg, axis=1)[:, :8].ravel(), minlength=256)
+    assert counts.max() > 3 * 192 and (counts <= 2).sum() > 10
+    rng2 = np.random.default_rng(67)
+    sample = np.sort(rng2.choice(700, size=40, replace=False))
+    _check_layer("fat_skewed", dev, oracle, layer_w, x, lg, None, path=1, sample=sample)
+
+
 def test_forward_prefill4096(dev, oracle, layer_w):
     x, lg, _ = synth.config_inputs("prefill4096", 3)
     rng = np.random.default_rng(33)
