@@ -1215,11 +1215,15 @@ __global__ __launch_bounds__(64 * kSkW) void k_skinny(GemmArgs A) {
 constexpr int kDlW = 4;                  // waves
 constexpr int kDlRT = 4;                 // row tiles per wave
 constexpr int kDlRows = 128;             // B rows staged per chunk
-constexpr int kDlStride = 512 + 16;      // LDS row stride: conflict-free fragment reads
+
+// byte offset of (row r, 16-byte chunk c) of a staged h row: rows of 512 B,
+// chunk index XORed (low 4 bits) with the row, so the 16 rows of a fragment
+// read fall in 16 distinct bank groups
+__device__ __forceinline__ int dl_boff(int r, int c) { return r * 512 + ((c & 16) | ((c ^ r) & 15)) * 16; }
 
 __global__ __launch_bounds__(64 * kDlW) void k_down_lds(GemmArgs A) {
     constexpr int KD = 512, NKT = KD / 128, NRB = 2048 / (16 * kDlRT * kDlW);
-    __shared__ __align__(16) uint8_t sb[kDlRows * kDlStride];
+    __shared__ __align__(16) uint8_t sb[kDlRows * 512];
     __shared__ uint32_t ss[kDlRows][4];       // B scale dwords: [row][lane group]
     __shared__ float ws[kDlRows];             // routing weight of each row
     const int xcd = blockIdx.x & 7, jx = blockIdx.x >> 3;
@@ -1246,24 +1250,19 @@ __global__ __launch_bounds__(64 * kDlW) void k_down_lds(GemmArgs A) {
     for (int c0 = p0; c0 < p1; c0 += kDlRows) {
         const int nr = min(kDlRows, p1 - c0);
         if (c0 != p0) __syncthreads();   // previous chunk fully read
-        // stage rows c0 .. c0+nr of h (contiguous in sorted order), their
+        // stage rows c0 .. c0+nr of h (contiguous in sorted order) with
+        // direct-to-LDS loads, all in flight at once: wave w loads row pairs
+        // w + 4u (1 KiB each, lane-contiguous in LDS), then their
         // lane-group-major scale dwords and routing weights
-        // 16 pieces of 16 B per thread, 8 loads in flight at a time (a
-        // plain loop would wait on each load before the next)
-        constexpr int PT = kDlRows * (KD / 16) / (64 * kDlW);
+        const int npair = __builtin_amdgcn_readfirstlane((nr + 1) >> 1);
+        const int wv = __builtin_amdgcn_readfirstlane(wave);
 #pragma unroll
-        for (int h2 = 0; h2 < PT; h2 += 8) {
-            u32x4 v[8];
-#pragma unroll
-            for (int u = 0; u < 8; u++) {
-                const int c = tid + 64 * kDlW * (h2 + u);
-                const int r = min(c / (KD / 16), nr - 1);   // rows past nr: never read
-                v[u] = *reinterpret_cast<const u32x4 *>(A.bq + (size_t)(c0 + r) * KD + (c % (KD / 16)) * 16);
-            }
-#pragma unroll
-            for (int u = 0; u < 8; u++) {
-                const int c = tid + 64 * kDlW * (h2 + u);
-                *reinterpret_cast<u32x4 *>(&sb[(c / (KD / 16)) * kDlStride + (c % (KD / 16)) * 16]) = v[u];
+        for (int u = 0; u < kDlRows / 2 / kDlW; u++) {
+            const int pr = wv + kDlW * u;
+            if (pr < npair) {
+                const int r = 2 * pr + (lane >> 5), ph = lane & 31;
+                const int c = (ph & 16) | ((ph ^ r) & 15);       // logical chunk in this slot
+                dma16(A.bq + (size_t)(c0 + min(r, nr - 1)) * KD + c * 16, &sb[pr * 1024]);
             }
         }
         for (int c = tid; c < nr; c += 64 * kDlW) {
@@ -1276,12 +1275,11 @@ __global__ __launch_bounds__(64 * kDlW) void k_down_lds(GemmArgs A) {
         for (int j = 0; j < ntt; j++) {
             // padding columns read row 0 of the chunk; never stored
             const int r = j * 16 + n < nr ? j * 16 + n : 0;
-            const uint8_t *bp = &sb[r * kDlStride + q * 16];
             v8i bv[NKT];
 #pragma unroll
             for (int kt = 0; kt < NKT; kt++) {
-                const u32x4 b0 = *reinterpret_cast<const u32x4 *>(bp + kt * 128);
-                const u32x4 b1 = *reinterpret_cast<const u32x4 *>(bp + kt * 128 + 64);
+                const u32x4 b0 = *reinterpret_cast<const u32x4 *>(&sb[dl_boff(r, 8 * kt + q)]);
+                const u32x4 b1 = *reinterpret_cast<const u32x4 *>(&sb[dl_boff(r, 8 * kt + 4 + q)]);
                 bv[kt] = v8i{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
             }
             const uint32_t sbw = ss[r][q];
