@@ -641,7 +641,6 @@ __global__ __launch_bounds__(256) void k_scatter(ScanArgs A) {
 // ---------------------------------------------------------------------------
 // grouped expert GEMM on scaled MFMA
 // ---------------------------------------------------------------------------
-enum { MODE_GATEUP = 0, MODE_DOWN = 1 };
 
 struct GemmArgs {
     const uint8_t *wa, *wb;   // routed experts: gate/up (GATEUP) or down (DOWN)
@@ -1014,17 +1013,15 @@ __global__ __launch_bounds__(256) void k_router_f16(const float *__restrict__ W,
 }
 
 // ---------------------------------------------------------------------------
-// skinny grouped GEMMs: tiles of at most 32 rows (few rows per expert)
+// skinny gate/up: tiles of at most 32 rows (few rows per expert)
 // ---------------------------------------------------------------------------
 // With a handful of rows per expert the grouped GEMM is a weight stream.
-// These kernels keep every wave's A (E2M1 fragments) in its own registers,
-// loaded all at once straight from HBM: no LDS staging of A and, for down, no
-// barrier at all.  B rows (e4m3) come from L2 into registers.
-//   GATEUP: workgroup = (tile, 32-row block of gate and up); the 8 waves split
-//           K into 8 x 256, partial sums meet in LDS in wave order, then
-//           SwiGLU and the per-32 quantisation of h (one block per row).
-//   DOWN:   workgroup = (tile, 128 output rows); wave w owns row tile w with
-//           all of K = 512, scales by the routing weight into the staging.
+// Every wave keeps its A (E2M1 fragments) in its own registers, loaded all at
+// once straight from HBM, with no LDS staging of A; B rows (e4m3) come from
+// L2 into registers.  Workgroup = (tile, 32-row block of gate and up); the 8
+// waves split K into 8 x 256, partial sums meet in LDS in wave order, then
+// SwiGLU and the per-32 quantisation of h (one block per row).  The down
+// projection of skinny tiles runs in k_down_lds, as for fat tiles.
 constexpr int kSkTok = 32;     // rows per skinny tile (two 16-row column tiles)
 constexpr int kSkinnyRows = 8; // auto mode: skinny while T*k <= kSkinnyRows * n_expert
 constexpr int kSkW = 8;        // waves per workgroup
@@ -1127,78 +1124,20 @@ __device__ __forceinline__ void skinny_gateup(const GemmArgs &A, const uint8_t *
     }
 }
 
-template <int NJ>
-__device__ __forceinline__ void skinny_down(const GemmArgs &A, const uint8_t *W, int mt0, int p0, int p1) {
-    constexpr int KD = 512, NKT = KD / 128;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q = lane >> 4;
-    const size_t nib = (size_t)2048 * KD / 2;
-    const int mt = mt0 + wave;
-    u32x4 af[NKT];
-#pragma unroll
-    for (int kt = 0; kt < NKT; kt++)
-        af[kt] = *reinterpret_cast<const u32x4 *>(W + ((size_t)mt * NKT + kt) * 1024 + lane * 16);
-    const uint32_t sa = *reinterpret_cast<const uint32_t *>(W + nib + ((size_t)mt * 64 + lane) * NKT);
-    u32x4 bf[NJ][NKT][2];
-    uint32_t sb[NJ];
-#pragma unroll
-    for (int j = 0; j < NJ; j++) {
-        const int p = p0 + j * 16 + (lane & 15);
-        const int r = p < p1 ? p : p0;
-        const uint8_t *bp = A.bq + (size_t)r * KD + q * 16;
-#pragma unroll
-        for (int kt = 0; kt < NKT; kt++) {
-            bf[j][kt][0] = *reinterpret_cast<const u32x4 *>(bp + kt * 128);
-            bf[j][kt][1] = *reinterpret_cast<const u32x4 *>(bp + kt * 128 + 64);
-        }
-        sb[j] = *reinterpret_cast<const uint32_t *>(A.bs2 + (size_t)r * (KD / 32) + q * NKT);
-    }
-    v4f acc[NJ];
-#pragma unroll
-    for (int j = 0; j < NJ; j++) acc[j] = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kt = 0; kt < NKT; kt++) {
-        const u32x4 f = af[kt];
-        const v8i av = v8i{(int)f[0], (int)f[1], (int)f[2], (int)f[3], 0, 0, 0, 0};
-#pragma unroll
-        for (int j = 0; j < NJ; j++) {
-            const u32x4 b0 = bf[j][kt][0], b1 = bf[j][kt][1];
-            const v8i bv = v8i{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
-            acc[j] = mfma_sel(kt, av, bv, acc[j], (int)sa, (int)sb[j]);
-        }
-    }
-#pragma unroll
-    for (int j = 0; j < NJ; j++) {
-        const int p = p0 + j * 16 + (lane & 15);
-        if (p >= p1) continue;
-        const float w = A.row_w[p];
-        const v4f c = acc[j];
-        *reinterpret_cast<float4 *>(A.dnw + (size_t)p * A.ldo + mt * 16 + 4 * q) =
-            make_float4(c[0] * w, c[1] * w, c[2] * w, c[3] * w);
-    }
-}
-
-// XCD-major order: the 16 row blocks of one tile run back to
-// back on one XCD.
-template <int MODE>
-__global__ __launch_bounds__(64 * kSkW) void k_skinny(GemmArgs A) {
+// XCD-major order: the 16 row blocks of one tile run back to back on one XCD.
+__global__ __launch_bounds__(64 * kSkW) void k_skinny_gateup(GemmArgs A) {
     constexpr int NRB = 16;
+    __shared__ __align__(16) float red[kSkW][4][64][4];
     const int xcd = blockIdx.x & 7, jx = blockIdx.x >> 3;
     const int ti = 8 * (jx / NRB) + xcd, rb = jx % NRB;
     if (ti >= *A.ntiles) return;
     const int4 tile = A.tiles[ti];
     const int e = tile.x, p0 = tile.y, p1 = tile.z;
     const int nj = (p1 - p0 + 15) >> 4;
-    if constexpr (MODE == MODE_GATEUP) {
-        __shared__ __align__(16) float red[kSkW][4][64][4];
-        const uint8_t *Wg = e < A.E ? A.wa + (size_t)e * A.wstride : A.sa;
-        const uint8_t *Wu = e < A.E ? A.wb + (size_t)e * A.wstride : A.sb;
-        if (nj <= 1) skinny_gateup<1>(A, Wg, Wu, rb * 2, p0, p1, red);
-        else skinny_gateup<2>(A, Wg, Wu, rb * 2, p0, p1, red);
-    } else {
-        const uint8_t *W = e < A.E ? A.wa + (size_t)e * A.wstride : A.sa;
-        if (nj <= 1) skinny_down<1>(A, W, rb * 8, p0, p1);
-        else skinny_down<2>(A, W, rb * 8, p0, p1);
-    }
+    const uint8_t *Wg = e < A.E ? A.wa + (size_t)e * A.wstride : A.sa;
+    const uint8_t *Wu = e < A.E ? A.wb + (size_t)e * A.wstride : A.sb;
+    if (nj <= 1) skinny_gateup<1>(A, Wg, Wu, rb * 2, p0, p1, red);
+    else skinny_gateup<2>(A, Wg, Wu, rb * 2, p0, p1, red);
 }
 
 // ---------------------------------------------------------------------------
@@ -2064,16 +2003,13 @@ static void launch_stage(const q36moe_ctx *c, const Plan &P, int st, hipStream_t
             break;
         case ST_GATEUP:
             if (P.skinny)
-                hipLaunchKernelGGL(k_skinny<MODE_GATEUP>, dim3(P.tiles * 16), dim3(64 * kSkW), 0, s, P.ga);
+                hipLaunchKernelGGL(k_skinny_gateup, dim3(P.tiles * 16), dim3(64 * kSkW), 0, s, P.ga);
             else
                 hipLaunchKernelGGL(k_gateup_dma, dim3(P.tiles * (FF / (16 * gdma::RT))), dim3(64 * gdma::W), 0, s,
                                    P.ga);
             break;
         case ST_DOWN:
-            if (P.skinny)
-                hipLaunchKernelGGL(k_skinny<MODE_DOWN>, dim3(P.tiles * 16), dim3(64 * kSkW), 0, s, P.da);
-            else
-                hipLaunchKernelGGL(k_down_lds, dim3(P.tiles * (D / (16 * kDlRT * kDlW))), dim3(64 * kDlW), 0, s, P.da);
+            hipLaunchKernelGGL(k_down_lds, dim3(P.tiles * (D / (16 * kDlRT * kDlW))), dim3(64 * kDlW), 0, s, P.da);
             break;
         case ST_COMBINE:
             hipLaunchKernelGGL(k_combine, dim3(T), dim3(256), 0, s, c->dnw, c->pos, T, K, D, P.has_sh,
