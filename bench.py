@@ -278,6 +278,14 @@ def main():
                 "frac": ach / HBM_PEAK_GBS, "traffic": None, "kernel": dom,
                 "kernel_us": st_us[dom], "bytes_per_launch": by}
     roof["traffic"] = measured_traffic(args.config, dom)
+    # both grouped GEMMs against both ceilings (the dominant one is `roof`)
+    gemm = {}
+    for st in ("gateup", "down"):
+        fl, by = kernel_flops(st, T, shared), kernel_bytes(st, T, U, shared)
+        gemm[st] = {"us": st_us[st], "tflops": fl / (st_us[st] * 1e-6) / 1e12,
+                    "mfma_frac": fl / (st_us[st] * 1e-6) / 1e12 / MFMA_FP8_PEAK_TFS,
+                    "gbs": by / (st_us[st] * 1e-6) / 1e9,
+                    "hbm_frac": by / (st_us[st] * 1e-6) / 1e9 / HBM_PEAK_GBS}
     # the forward once more, so `out` holds a real result again
     step(0)
     torch.cuda.synchronize()
@@ -307,6 +315,7 @@ def main():
         "distinct_experts": U,
         "stage_us": st_us,
         "roofline": roof,
+        "grouped_gemms": gemm,
     }
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(args.config, T, args.cpu_seconds, shared)
