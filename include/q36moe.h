@@ -136,8 +136,28 @@ int q36moe_router_logits(const float *w, int n_rows, int n_expert, const void *x
 int q36moe_quant_e4m3(const void *x, int x_fmt, int T, int K,
                       uint8_t *xq, uint8_t *xs, void *stream);
 
+/* The producer of the MoE input in one pass: residual add, RMSNorm and the
+ * per-32 E8M0 + e4m3 quantisation (replaces k_add_rmsnorm + k_quant_e4m3,
+ * q36_engine.cu:696-706 and :2411-2428; k_rmsnorm_b, :3230-3240, when a is
+ * NULL).  For each token t (rows of d_model == 2048 f32, device pointers):
+ *   if a: h[t] += a[t] (written back);  y[t] = h[t] * rsqrt(mean(h[t]^2) + eps) * w
+ * y [T][d_model] f32 is written when non-NULL (the router input); xq
+ * [T][d_model] e4m3 and xs [T][d_model/32] E8M0 when non-NULL (the MoE input
+ * of q36moe_forward_q8).  Asynchronous on `stream`. */
+int q36moe_add_rmsnorm_quant(float *h, const float *a, const float *w, int T, int d_model,
+                             float eps, float *y, uint8_t *xq, uint8_t *xs, void *stream);
+
+/* q36moe_forward on activations already quantised by
+ * q36moe_add_rmsnorm_quant (or q36moe_quant_e4m3): xq [T][d_model] e4m3,
+ * xs [T][d_model/32] E8M0, device pointers that must stay valid until the
+ * forward has run (and while its XQ/XS taps are read).  Same result as
+ * q36moe_forward on the x they were quantised from. */
+int q36moe_forward_q8(q36moe_ctx *c, const q36moe_weights *w, const uint8_t *xq, const uint8_t *xs,
+                      const float *logits, int ld_logits, const float *shg, int T, float scale,
+                      void *out, int out_fmt);
+
 /* Execution path of q36moe_forward.  The sorted path (route + sort + grouped
- * expert GEMMs + combine) serves any T, with fat tiles (up to 256 rows per
+ * expert GEMMs + combine) serves any T, with fat tiles (up to 192 rows per
  * expert tile, weights staged through LDS) or skinny tiles (up to 32 rows,
  * weights streamed straight into registers); the direct path (no sort,
  * slots combined in registers) serves T <= 16 as two kernels (gate/up, then

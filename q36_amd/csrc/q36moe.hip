@@ -382,12 +382,20 @@ __device__ __forceinline__ uint8_t quant8_lane(const float (&v)[8], int lane, ui
 
 // 8 activations as raw bits, then widened to float: split so the load can be
 // issued early (before routing) without the conversion waiting on it there.
+// activations handed over already quantised (q36moe_forward_q8): x is the
+// e4m3 codes [T][D], xs_in the E8M0 scales [T][D/32]
+constexpr int kFmtE4M3 = 2;
+
 struct X8 {
     u32x4 a, b;
 };
 __device__ __forceinline__ X8 load8_raw(const void *x, int fmt, size_t off) {
     X8 r;
-    if (fmt == Q36MOE_FMT_F32) {
+    if (fmt == kFmtE4M3) {
+        const uint2 v = *reinterpret_cast<const uint2 *>(static_cast<const uint8_t *>(x) + off);
+        r.a = u32x4{v.x, v.y, 0u, 0u};
+        r.b = u32x4{0u, 0u, 0u, 0u};
+    } else if (fmt == Q36MOE_FMT_F32) {
         const u32x4 *p = reinterpret_cast<const u32x4 *>(static_cast<const float *>(x) + off);
         r.a = p[0];
         r.b = p[1];
@@ -421,6 +429,7 @@ struct RouteArgs {
     const void *x; int x_fmt; int D; int nb;
     int32_t *idx; float *wt; uint8_t *xq; uint8_t *xs; uint8_t *xs2;
     int32_t *blk_cnt; int32_t *rank;
+    const uint8_t *xs_in;     // scales of pre-quantised x (x_fmt kFmtE4M3)
 };
 
 // One wavefront per token, TPB tokens per workgroup: top-k routing,
@@ -446,9 +455,12 @@ __global__ __launch_bounds__(64 * TPB) void k_route(RouteArgs A) {
     if (t < A.T) {
         // x of the token (kRouteD values, 8 per lane per pass) is loaded
         // before routing so both latencies overlap
+        const bool preq = A.x_fmt == kFmtE4M3;
         X8 xr[kRouteD / 512];
+        if (!preq) {
 #pragma unroll
-        for (int c = 0; c < kRouteD / 512; c++) xr[c] = load8_raw(A.x, A.x_fmt, (size_t)t * A.D + c * 512 + lane * 8);
+            for (int c = 0; c < kRouteD / 512; c++) xr[c] = load8_raw(A.x, A.x_fmt, (size_t)t * A.D + c * 512 + lane * 8);
+        }
         const Pick P = route_pick(A.logits + (size_t)t * A.ld, A.E, A.k, A.scale, rlds[wave]);
         if (lane < A.k) {
             A.idx[(size_t)t * A.k + lane] = P.idx;
@@ -457,6 +469,12 @@ __global__ __launch_bounds__(64 * TPB) void k_route(RouteArgs A) {
             atomicOr(&tmask[P.idx], 1u << wave);
         }
         Q36_TRACE_AT(21);
+        if (preq) {
+            // codes stay where the caller put them; only the lane-group-major
+            // copy of the scales is made for the grouped GEMM
+            for (int b = lane; b < nb32; b += 64)
+                A.xs2[(size_t)t * nb32 + (b & 3) * (nb32 / 4) + (b >> 2)] = A.xs_in[(size_t)t * nb32 + b];
+        } else {
 #pragma unroll
         for (int c = 0; c < kRouteD / 512; c++) {
             const size_t o = (size_t)t * A.D + c * 512 + lane * 8;
@@ -466,6 +484,7 @@ __global__ __launch_bounds__(64 * TPB) void k_route(RouteArgs A) {
             const uint8_t sb = quant8_lane(v, lane, A.xq + o, A.xs + (size_t)t * nb32 + b);
             // lane-group-major copy for the grouped GEMM: [t][b % 4][b / 4]
             if ((lane & 3) == 0) A.xs2[(size_t)t * nb32 + (b & 3) * (nb32 / 4) + (b >> 2)] = sb;
+        }
         }
     }
     Q36_TRACE_AT(22);
@@ -1013,6 +1032,50 @@ __global__ __launch_bounds__(256) void k_router_f16(const float *__restrict__ W,
 }
 
 // ---------------------------------------------------------------------------
+// the producer of the MoE input: residual add + RMSNorm + quantisation
+// ---------------------------------------------------------------------------
+// One token row per workgroup, 4 waves x 512 values, 8 per lane (the lane
+// layout of quant8_lane, so each 32-block is quantised by 4 lanes of one
+// wave straight from registers).  h += a is written back; the sum of
+// squares is fp32 per lane, a wave butterfly, then the 4 wave sums in
+// wave order; y = h * rsqrt(mean + eps) * w (k_add_rmsnorm,
+// q36_engine.cu:696-706) goes to y and / or to e4m3 + E8M0.
+__global__ __launch_bounds__(256) void k_add_rmsnorm_quant(float *__restrict__ h, const float *__restrict__ a,
+                                                          const float *__restrict__ w, float eps,
+                                                          float *__restrict__ y, uint8_t *__restrict__ xq,
+                                                          uint8_t *__restrict__ xs) {
+    __shared__ float part[4];
+    const int t = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const size_t o = (size_t)t * kRtD + wave * 512 + lane * 8;
+    const float4 h0 = *reinterpret_cast<const float4 *>(h + o), h1 = *reinterpret_cast<const float4 *>(h + o + 4);
+    const float4 g0 = *reinterpret_cast<const float4 *>(w + wave * 512 + lane * 8);
+    const float4 g1 = *reinterpret_cast<const float4 *>(w + wave * 512 + lane * 8 + 4);
+    float v[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+    const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+    if (a) {
+        const float4 a0 = *reinterpret_cast<const float4 *>(a + o), a1 = *reinterpret_cast<const float4 *>(a + o + 4);
+        v[0] += a0.x; v[1] += a0.y; v[2] += a0.z; v[3] += a0.w;
+        v[4] += a1.x; v[5] += a1.y; v[6] += a1.z; v[7] += a1.w;
+        *reinterpret_cast<float4 *>(h + o) = make_float4(v[0], v[1], v[2], v[3]);
+        *reinterpret_cast<float4 *>(h + o + 4) = make_float4(v[4], v[5], v[6], v[7]);
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) ss = fmaf(v[i], v[i], ss);
+    ss = wave_sum(ss);
+    if (lane == 0) part[wave] = ss;
+    __syncthreads();
+    const float r = rsqrtf((part[0] + part[1] + part[2] + part[3]) / (float)kRtD + eps);
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = v[i] * r * g[i];
+    if (y) {
+        *reinterpret_cast<float4 *>(y + o) = make_float4(v[0], v[1], v[2], v[3]);
+        *reinterpret_cast<float4 *>(y + o + 4) = make_float4(v[4], v[5], v[6], v[7]);
+    }
+    if (xq) quant8_lane(v, lane, xq + o, xs + (size_t)t * (kRtD / 32) + wave * 16 + (lane >> 2));
+}
+
+// ---------------------------------------------------------------------------
 // skinny gate/up: tiles of at most 32 rows (few rows per expert)
 // ---------------------------------------------------------------------------
 // With a handful of rows per expert the grouped GEMM is a weight stream.
@@ -1268,6 +1331,7 @@ struct DirectArgs {
     // fused kernel only: per-token arrival / departure counters (zero
     // between calls), error flag, and the number of gate/up workgroups
     uint32_t *arrive; uint32_t *depart; uint32_t *err; int n_gateup_wg;
+    const uint8_t *xs_in;                       // scales of pre-quantised x (x_fmt kFmtE4M3)
 };
 
 constexpr int kDD = 2048;   // d_model of the instantiated kernels
@@ -1329,9 +1393,14 @@ __device__ __forceinline__ void direct_gateup_body(const DirectArgs &A, int i, i
     const int sag = *reinterpret_cast<const int *>(Wg + so);
     const int sau = *reinterpret_cast<const int *>(Wu + so);
 
-    float xv[8];
-    cvt8(xr, A.x_fmt, xv);
-    quant8_lane(xv, lane, sx + wave * 512 + lane * 8, sxs + wave * 16 + (lane >> 2));
+    if (A.x_fmt == kFmtE4M3) {
+        *reinterpret_cast<uint2 *>(sx + wave * 512 + lane * 8) = make_uint2(xr.a[0], xr.a[1]);
+        if ((lane & 3) == 0) sxs[wave * 16 + (lane >> 2)] = A.xs_in[(size_t)t * (kDD / 32) + wave * 16 + (lane >> 2)];
+    } else {
+        float xv[8];
+        cvt8(xr, A.x_fmt, xv);
+        quant8_lane(xv, lane, sx + wave * 512 + lane * 8, sxs + wave * 16 + (lane >> 2));
+    }
     Q36_TRACE_AT(2);
     if (threadIdx.x < 8) reinterpret_cast<uint32_t *>(sx + kDD)[threadIdx.x] = 0u;
     __syncthreads();
@@ -1726,6 +1795,7 @@ struct q36moe_ctx {
     void *base;
     int32_t *topk_idx; float *topk_w; int32_t *rank;
     uint8_t *xq, *xs, *xs2;
+    const uint8_t *tap_xq, *tap_xs;   // where the last forward's quantised x is
     int32_t *blk_cnt, *blk_off, *tot, *e_off, *perm, *pos, *row_tok;
     float *row_w;
     int4 *tiles; int32_t *ntiles;
@@ -1918,6 +1988,7 @@ int q36moe_ctx_create(int max_tokens, int n_expert, int d_model, int d_ff, int t
     c->topk_w = reinterpret_cast<float *>(b + o_w);
     c->rank = reinterpret_cast<int32_t *>(b + o_rank);
     c->xq = b + o_xq; c->xs = b + o_xs; c->xs2 = b + o_xs2;
+    c->tap_xq = c->xq; c->tap_xs = c->xs;
     c->blk_cnt = reinterpret_cast<int32_t *>(b + o_bc);
     c->blk_off = reinterpret_cast<int32_t *>(b + o_bo);
     c->tot = reinterpret_cast<int32_t *>(b + o_tot);
@@ -2030,18 +2101,19 @@ int q36moe_ctx_replay(q36moe_ctx *c, const q36moe_weights *w, int stage) {
     return hipGetLastError() == hipSuccess ? Q36MOE_OK : Q36MOE_EHIP;
 }
 
-int q36moe_forward(q36moe_ctx *c, const q36moe_weights *w, const void *x, int x_fmt,
-                   const float *logits, int ld_logits, const float *shg, int T, float scale,
-                   void *out, int out_fmt) {
+// x_fmt: Q36MOE_FMT_F32 / _BF16, or kFmtE4M3 with x the codes and xs_in the
+// scales of already quantised activations
+static int forward_impl(q36moe_ctx *c, const q36moe_weights *w, const void *x, int x_fmt,
+                        const uint8_t *xs_in, const float *logits, int ld_logits, const float *shg,
+                        int T, float scale, void *out, int out_fmt) {
     if (!c || !w || T < 0 || T > c->max_T) return Q36MOE_EINVAL;
     if (w->E != c->E || w->D != c->D || w->FF != c->FF) return Q36MOE_EINVAL;
-    if ((x_fmt != Q36MOE_FMT_F32 && x_fmt != Q36MOE_FMT_BF16) ||
-        (out_fmt != Q36MOE_FMT_F32 && out_fmt != Q36MOE_FMT_BF16))
-        return Q36MOE_EINVAL;
+    if (out_fmt != Q36MOE_FMT_F32 && out_fmt != Q36MOE_FMT_BF16) return Q36MOE_EINVAL;
     // kernels are instantiated for the q36 shape (q36.h:78-84)
     if (c->D != 2048 || c->FF != 512) return Q36MOE_EINVAL;
     if (T == 0) return Q36MOE_OK;
     if (!x || !logits || !out || ld_logits < c->E) return Q36MOE_EINVAL;
+    if (x_fmt == kFmtE4M3 && !xs_in) return Q36MOE_EINVAL;
     if (shg && !w->sh_gate) return Q36MOE_EINVAL;
     const int has_sh = shg != nullptr;
     const int E = c->E, D = c->D, FF = c->FF, K = c->K;
@@ -2071,17 +2143,19 @@ int q36moe_forward(q36moe_ctx *c, const q36moe_weights *w, const void *x, int x_
                           nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0,
                           c->topk_idx, c->topk_w, c->pos, c->perm, c->xq, c->xs, c->hf,
                           c->hq, c->hs, out, out_fmt, c->sync, c->sync + kDirectMaxT,
-                          c->sync + 2 * kDirectMaxT, ngu};
+                          c->sync + 2 * kDirectMaxT, ngu, xs_in};
     } else {
         P.ra = RouteArgs{logits, ld_logits, T, E, K, scale, x, x_fmt, D, nb,
-                         c->topk_idx, c->topk_w, c->xq, c->xs, c->xs2, c->blk_cnt, c->rank};
+                         c->topk_idx, c->topk_w, c->xq, c->xs, c->xs2, c->blk_cnt, c->rank, xs_in};
         P.sa = ScanArgs{c->blk_cnt, nb, tpb, nb <= kScanInlineBlocks ? 1 : 0, E, T, K, c->topk_idx, c->topk_w, c->rank, shg, tn,
                         c->blk_off, c->tot, c->e_off, c->perm, c->pos, c->row_tok, c->row_w, c->tiles,
                         c->ntiles};
         GemmArgs &ga = P.ga;
         ga.E = E; ga.M = FF;
         ga.tiles = c->tiles; ga.ntiles = c->ntiles;
-        ga.bq = c->xq; ga.bs2 = c->xs2; ga.row_tok = c->row_tok; ga.row_w = c->row_w;
+        // pre-quantised codes are read where the caller left them
+        ga.bq = x_fmt == kFmtE4M3 ? static_cast<const uint8_t *>(x) : c->xq;
+        ga.bs2 = c->xs2; ga.row_tok = c->row_tok; ga.row_w = c->row_w;
         ga.hq = c->hq; ga.hs = c->hs; ga.hs2 = c->hs2; ga.ldo = FF;
         GemmArgs &da = P.da;
         da = ga;
@@ -2097,6 +2171,11 @@ int q36moe_forward(q36moe_ctx *c, const q36moe_weights *w, const void *x, int x_
     c->last_T = T;
     c->last_sh = has_sh;
     c->last_path = direct ? 1 : skinny ? 2 : 0;
+    // the sorted path reads pre-quantised codes in place; the direct path
+    // copies every token's codes into the context
+    const bool in_place = !direct && x_fmt == kFmtE4M3;
+    c->tap_xq = in_place ? static_cast<const uint8_t *>(x) : c->xq;
+    c->tap_xs = in_place ? xs_in : c->xs;
     if (hipGetLastError() != hipSuccess) return Q36MOE_EHIP;
     if (c->timing) {
         if (hipEventSynchronize(c->ev[ST_COUNT]) != hipSuccess) return Q36MOE_EHIP;
@@ -2108,6 +2187,20 @@ int q36moe_forward(q36moe_ctx *c, const q36moe_weights *w, const void *x, int x_
         }
     }
     return Q36MOE_OK;
+}
+
+int q36moe_forward(q36moe_ctx *c, const q36moe_weights *w, const void *x, int x_fmt,
+                   const float *logits, int ld_logits, const float *shg, int T, float scale,
+                   void *out, int out_fmt) {
+    if (x_fmt != Q36MOE_FMT_F32 && x_fmt != Q36MOE_FMT_BF16) return Q36MOE_EINVAL;
+    return forward_impl(c, w, x, x_fmt, nullptr, logits, ld_logits, shg, T, scale, out, out_fmt);
+}
+
+int q36moe_forward_q8(q36moe_ctx *c, const q36moe_weights *w, const uint8_t *xq, const uint8_t *xs,
+                      const float *logits, int ld_logits, const float *shg, int T, float scale,
+                      void *out, int out_fmt) {
+    if (T > 0 && !xs) return Q36MOE_EINVAL;
+    return forward_impl(c, w, xq, kFmtE4M3, xs, logits, ld_logits, shg, T, scale, out, out_fmt);
 }
 
 int q36moe_router_topk(const float *logits, int T, int n_expert, int ld, int k, float scale,
@@ -2140,6 +2233,16 @@ int q36moe_router_logits(const float *w, int n_rows, int n_expert, const void *x
     return hip_rc(hipGetLastError());
 }
 
+int q36moe_add_rmsnorm_quant(float *h, const float *a, const float *w, int T, int d_model,
+                             float eps, float *y, uint8_t *xq, uint8_t *xs, void *stream) {
+    if (T < 0 || d_model != kRtD || !(eps >= 0.0f) || (!xq) != (!xs)) return Q36MOE_EINVAL;
+    if (T == 0) return Q36MOE_OK;
+    if (!h || !w || (!y && !xq)) return Q36MOE_EINVAL;
+    hipLaunchKernelGGL(k_add_rmsnorm_quant, dim3(T), dim3(256), 0, static_cast<hipStream_t>(stream), h, a, w,
+                       eps, y, xq, xs);
+    return hip_rc(hipGetLastError());
+}
+
 int q36moe_quant_e4m3(const void *x, int x_fmt, int T, int K, uint8_t *xq, uint8_t *xs,
                       void *stream) {
     if (T < 0 || K <= 0 || K % 32 != 0 || (x_fmt != Q36MOE_FMT_F32 && x_fmt != Q36MOE_FMT_BF16))
@@ -2160,8 +2263,8 @@ int q36moe_ctx_copy_tap(q36moe_ctx *c, int tap, void *dst, size_t bytes, size_t 
     switch (tap) {
         case Q36MOE_TAP_TOPK_IDX: src = c->topk_idx; sz = n * 4; break;
         case Q36MOE_TAP_TOPK_W: src = c->topk_w; sz = n * 4; break;
-        case Q36MOE_TAP_XQ: src = c->xq; sz = T * c->D; break;
-        case Q36MOE_TAP_XS: src = c->xs; sz = T * c->D / 32; break;
+        case Q36MOE_TAP_XQ: src = c->tap_xq; sz = T * c->D; break;
+        case Q36MOE_TAP_XS: src = c->tap_xs; sz = T * c->D / 32; break;
         case Q36MOE_TAP_EOFF:
             if (c->last_path == 1) return Q36MOE_EINVAL;   // the direct path does not sort
             src = c->e_off; sz = (size_t)(c->E + 1) * 4; break;

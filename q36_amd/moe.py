@@ -59,6 +59,8 @@ def lib():
     L.q36moe_router_topk.argtypes = [vp, i, i, i, i, f, i, vp, vp, vp]
     L.q36moe_router_logits.argtypes = [vp, i, i, vp, i, i, i, i, vp, i, vp, vp]
     L.q36moe_quant_e4m3.argtypes = [vp, i, i, i, vp, vp, vp]
+    L.q36moe_add_rmsnorm_quant.argtypes = [vp, vp, vp, i, i, f, vp, vp, vp, vp]
+    L.q36moe_forward_q8.argtypes = [vp, vp, vp, vp, vp, i, vp, i, f, vp, i]
     L.q36moe_ctx_copy_tap.argtypes = [vp, i, vp, sz, ctypes.POINTER(sz)]
     L.q36moe_ctx_set_path.argtypes = [vp, i]
     L.q36moe_ctx_last_path.argtypes = [vp]
@@ -242,6 +244,26 @@ class MoELayer:
         self.last_shared = shg is not None
         return out
 
+    def forward_q8(self, weights, xq, xs, logits, shg=None, scale=1.0, out_dtype=torch.bfloat16, out=None):
+        """forward on activations already quantised (add_rmsnorm_quant or
+        quant_e4m3): xq u8 [T, d_model] e4m3, xs u8 [T, d_model/32] E8M0."""
+        T = xq.shape[0]
+        if out is None:
+            out = torch.empty((T, self.d_model), dtype=out_dtype, device=xq.device)
+        of = FMT_F32 if out.dtype == torch.float32 else FMT_BF16
+        if logits.dim() != 2 or logits.shape[0] != T or logits.stride(1) != 1:
+            raise Q36MoEError("logits must be [T, n_expert] with contiguous rows")
+        lp = _dev(logits, "logits", torch.float32) if T else None
+        sp = _dev(shg, "shg", torch.float32) if shg is not None else None
+        qp = _dev(xq, "xq", torch.uint8) if T else None
+        sc = _dev(xs, "xs", torch.uint8) if T else None
+        op = _dev(out, "out") if T else None
+        check(lib().q36moe_forward_q8(self._h, weights._h, qp, sc, lp, logits.stride(0), sp, T, float(scale),
+                                      op, of), "q36moe_forward_q8")
+        self.last_T = T
+        self.last_shared = shg is not None
+        return out
+
     def tap(self, which):
         """Copy of an internal buffer of the last forward (see TAP_*)."""
         T, k, D, FF, E = self.last_T, self.top_k, self.d_model, self.d_ff, self.n_expert
@@ -351,6 +373,23 @@ def router_logits(w, x, n_expert, mode=ROUTER_AUTO):
                                      ctypes.c_void_p(shg.data_ptr()) if shg is not None else None,
                                      _stream()), "q36moe_router_logits")
     return logits, shg
+
+
+def add_rmsnorm_quant(h, a, w, eps=1e-6, want_y=True, want_q=True):
+    """Residual add + RMSNorm + per-32 quantisation in one kernel
+    (k_add_rmsnorm q36_engine.cu:696-706, then k_quant_e4m3 :2411-2428):
+    h [T, 2048] f32 (h += a in place when a is given), w [2048] f32 ->
+    (y f32 [T, 2048] or None, xq u8 [T, 2048] or None, xs u8 [T, 64] or None)."""
+    T, D = h.shape
+    y = torch.empty((T, D), dtype=torch.float32, device=h.device) if want_y else None
+    xq = torch.empty((T, D), dtype=torch.uint8, device=h.device) if want_q else None
+    xs = torch.empty((T, D // 32), dtype=torch.uint8, device=h.device) if want_q else None
+    hp = _dev(h, "h", torch.float32) if T else None
+    ap = _dev(a, "a", torch.float32) if (a is not None and T) else None
+    ptr = lambda t: ctypes.c_void_p(t.data_ptr()) if (t is not None and T) else None
+    check(lib().q36moe_add_rmsnorm_quant(hp, ap, _dev(w, "w", torch.float32), T, D, float(eps),
+                                         ptr(y), ptr(xq), ptr(xs), _stream()), "q36moe_add_rmsnorm_quant")
+    return y, xq, xs
 
 
 def quant_e4m3(x):

@@ -101,6 +101,12 @@ def test_entry_points_reject_bad_args_without_gpu(L):
     assert rl(None, 256, 256, None, 0, 4, 2048, 3, None, 256, None, None) == -22   # mode
     assert rl(None, 256, 256, None, 0, 4, 2048, 0, None, 255, None, None) == -22   # ld < E
     assert rl(None, 257, 256, None, 0, 0, 2048, 0, None, 256, None, None) == 0     # T = 0
+    arq = L.q36moe_add_rmsnorm_quant
+    assert arq(None, None, None, 4, 1024, ctypes.c_float(1e-6), None, None, None, None) == -22  # d_model
+    assert arq(None, None, None, 4, 2048, ctypes.c_float(-1.0), None, None, None, None) == -22  # eps
+    assert arq(None, None, None, 4, 2048, ctypes.c_float(1e-6), None, None, ctypes.c_void_p(8), None) == -22  # xq w/o xs
+    assert arq(None, None, None, 0, 2048, ctypes.c_float(1e-6), None, None, None, None) == 0
+    assert L.q36moe_forward_q8(None, None, None, None, None, 256, None, 1, ctypes.c_float(1.0), None, 0) == -22
     assert L.q36moe_quant_e4m3(None, 2, 4, 128, None, None, None) == -22
     assert L.q36moe_quant_e4m3(None, 0, 0, 128, None, None, None) == 0
     h = ctypes.c_void_p()

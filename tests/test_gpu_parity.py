@@ -546,3 +546,52 @@ def test_router_logits_bf16_input_and_no_shared(dev):
     assert shg is None
     ref, mag = _router_ref(w, xb.float().cpu().numpy(), False)
     assert (np.abs(lg.cpu().numpy() - ref) / mag).max() <= 2e-6
+
+
+@pytest.mark.parametrize("T,with_a", [(1, True), (5, True), (300, True), (7, False)])
+def test_add_rmsnorm_quant(dev, oracle, T, with_a):
+    """Fused residual add + RMSNorm + quantisation: h += a bit-exact (one
+    fp32 add), y against fp64 within fp32 rounding of the sum and rsqrt, and
+    the codes / scales bit-exact against the oracle's quantisation of y."""
+    rng = np.random.default_rng(900 + T)
+    h = (rng.standard_normal((T, 2048)) * 3).astype(np.float32)
+    a = rng.standard_normal((T, 2048)).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(2048)).astype(np.float32)
+    h[0, :64] = 0.0                                   # a zero 32-block (scale 2^-127)
+    ht = torch.from_numpy(h).to(dev)
+    y, xq, xs = moe.add_rmsnorm_quant(ht, torch.from_numpy(a).to(dev) if with_a else None,
+                                      torch.from_numpy(w).to(dev), eps=1e-6)
+    torch.cuda.synchronize()
+    v = (h + a) if with_a else h                      # fp32 add, as the kernel
+    np.testing.assert_array_equal(ht.cpu().numpy(), v)
+    v64 = v.astype(np.float64)
+    ref = v64 / np.sqrt((v64 * v64).mean(axis=1, keepdims=True) + 1e-6) * w
+    yg = y.cpu().numpy()
+    err = np.abs(yg - ref).max() / np.abs(ref).max()
+    _metrics("add_rmsnorm_quant", T=T, with_a=with_a, max_rel=float(err))
+    assert err <= 4e-6, err
+    oq, os_ = oracle.quant_e4m3(yg)
+    np.testing.assert_array_equal(xq.cpu().numpy(), oq)
+    np.testing.assert_array_equal(xs.cpu().numpy(), os_)
+
+
+@pytest.mark.parametrize("T,path", [(1, 0), (5, 2), (5, 3), (40, 4), (40, 1), (600, 0)])
+def test_forward_q8_equals_forward(dev, layer_w, T, path):
+    """The pre-quantised entry gives bit-identical results (outputs and
+    routing/quantisation taps) to forward on the x it was quantised from, on
+    every path."""
+    _, dw = layer_w
+    rng = np.random.default_rng(950 + T)
+    x = torch.from_numpy(synth.hidden(rng, T)).to(dev)
+    lg = torch.from_numpy(synth.normal_logits(rng, T)).to(dev)
+    shg = torch.from_numpy(rng.standard_normal(T).astype(np.float32)).to(dev)
+    xq, xs = moe.quant_e4m3(x)
+    la, lb = moe.MoELayer(T), moe.MoELayer(T)
+    la.set_path(path)
+    lb.set_path(path)
+    ya = la.forward(dw, x, lg, shg, out_dtype=torch.float32)
+    yb = lb.forward_q8(dw, xq, xs, lg, shg, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(ya.cpu().numpy(), yb.cpu().numpy())
+    for tap in (moe.TAP_TOPK_IDX, moe.TAP_XQ, moe.TAP_XS, moe.TAP_HQ):
+        np.testing.assert_array_equal(la.tap(tap).cpu().numpy(), lb.tap(tap).cpu().numpy())
