@@ -41,6 +41,8 @@ extern "C" {
 #define Q36MOE_EINVAL (-22)
 #define Q36MOE_ENOMEM (-12)
 #define Q36MOE_EHIP   (-1000)
+#define Q36MOE_EIO    (-5)    /* the file could not be opened or mapped */
+#define Q36MOE_ENOENT (-2)    /* no such tensor / metadata key          */
 
 /* activation / output element formats */
 #define Q36MOE_FMT_F32  0
@@ -198,6 +200,37 @@ int q36moe_num_stages(void);
  * event overhead.  The stage's outputs are rewritten; call forward again
  * before reading results.  No counterpart in the reference (profiling aid). */
 int q36moe_ctx_replay(q36moe_ctx *c, const q36moe_weights *w, int stage);
+
+/* GGUF v3 ingest (replaces gguf_open, gguf.c, and bind_moe + upload,
+ * q36_model.c:54-77 and q36_engine.cu:196-228, for the MoE tensors).  The
+ * file is mapped read-only and its header, metadata and tensor directory
+ * parsed; tensor data is never copied by the reader.  Errors: Q36MOE_EIO
+ * (open/map), Q36MOE_EINVAL (not GGUF v3, malformed, or a tensor past the
+ * end of the file), Q36MOE_ENOENT (no such tensor or key). */
+typedef struct q36moe_gguf q36moe_gguf;
+int q36moe_gguf_open(const char *path, q36moe_gguf **out);
+void q36moe_gguf_close(q36moe_gguf *g);
+int q36moe_gguf_info(const q36moe_gguf *g, uint32_t *version, uint64_t *n_tensors, uint64_t *n_kv,
+                     uint32_t *alignment, uint64_t *data_offset);
+/* Tensor by exact name: ggml type id, n_dims, dims[4] (dims[0] innermost,
+ * unused dims 1), absolute file offset, host pointer into the mapping and
+ * byte size (0 for a type without a known block size).  Any out pointer
+ * may be NULL. */
+int q36moe_gguf_tensor(const q36moe_gguf *g, const char *name, uint32_t *ggml_type, uint32_t *n_dims,
+                       uint64_t *dims, uint64_t *file_offset, const void **data, uint64_t *nbytes);
+int q36moe_gguf_u32(const q36moe_gguf *g, const char *key, uint32_t *out);
+/* Uploads block `layer`'s experts: blk.N.ffn_{gate,up,down}_exps.weight,
+ * MXFP4 (ggml type 39) of ggml dims [d_model][d_ff][E] / [d_ff][d_model][E];
+ * with with_shared, also blk.N.ffn_{gate,up,down}_shexp.weight (MXFP4 only:
+ * the reference's Q8_0 shared expert is EINVAL here). */
+int q36moe_weights_from_gguf(const q36moe_gguf *g, int layer, int with_shared, q36moe_weights **out);
+/* The router rows of block `layer` as host f32 for q36moe_router_logits:
+ * blk.N.ffn_gate_inp.weight [n_expert][d_model] (F32 or BF16, widened
+ * exactly) and, when present, blk.N.ffn_gate_inp_shexp.weight as row
+ * n_expert.  dst holds dst_floats floats (EINVAL if the rows do not fit);
+ * *n_rows and *d_model receive the shape written. */
+int q36moe_router_from_gguf(const q36moe_gguf *g, int layer, float *dst, size_t dst_floats, int *n_rows,
+                            int *d_model);
 
 /* One v_mfma_scale_f32_16x16x128_f8f6f4 on caller-packed operands:
  * a, b: 64 lanes x 32 bytes; sa, sb: 64 lane scale dwords (byte 0 used);

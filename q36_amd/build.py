@@ -9,7 +9,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 LIB = os.path.join(HERE, "libq36moe.so")
-SOURCES = [os.path.join(HERE, "csrc", f) for f in ("q36moe.hip", "q36moe_pack.cpp")]
+SOURCES = [os.path.join(HERE, "csrc", f) for f in ("q36moe.hip", "q36moe_pack.cpp", "q36moe_gguf.cpp")]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 FLAGS = [

@@ -73,6 +73,15 @@ def lib():
     L.q36moe_num_stages.argtypes = []
     L.q36moe_probe_mfma.argtypes = [vp, vp, vp, vp, i, i, vp, vp]
     L.q36moe_ctx_replay.argtypes = [vp, vp, i]
+    u32p, u64p = ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_uint64)
+    L.q36moe_gguf_open.argtypes = [ctypes.c_char_p, pp]
+    L.q36moe_gguf_close.argtypes = [vp]
+    L.q36moe_gguf_close.restype = None
+    L.q36moe_gguf_info.argtypes = [vp, u32p, u64p, u64p, u32p, u64p]
+    L.q36moe_gguf_tensor.argtypes = [vp, ctypes.c_char_p, u32p, u32p, u64p, u64p, pp, u64p]
+    L.q36moe_gguf_u32.argtypes = [vp, ctypes.c_char_p, u32p]
+    L.q36moe_weights_from_gguf.argtypes = [vp, i, i, pp]
+    L.q36moe_router_from_gguf.argtypes = [vp, i, vp, sz, ctypes.POINTER(i), ctypes.POINTER(i)]
     _lib = L
     return L
 
@@ -139,6 +148,16 @@ class MoEWeights:
         check(lib().q36moe_weights_upload(*ptrs, E, d_model, d_ff, d_ff_sh, ctypes.byref(h)),
               "q36moe_weights_upload")
         return cls(h, E, d_model, d_ff, d_ff_sh)
+
+    @classmethod
+    def from_gguf(cls, gguf, layer, with_shared=False):
+        """Block `layer`'s MXFP4 experts (and shared expert) of an open GGUF."""
+        h = ctypes.c_void_p()
+        check(lib().q36moe_weights_from_gguf(gguf._h, layer, int(with_shared), ctypes.byref(h)),
+              "q36moe_weights_from_gguf")
+        t = gguf.tensor(f"blk.{layer}.ffn_gate_exps.weight")
+        D, FF, E = t["dims"][:3]
+        return cls(h, E, D, FF, FF if with_shared else 0)
 
     @classmethod
     def alloc(cls, n_expert, d_model, d_ff, d_ff_sh=0):
@@ -373,6 +392,58 @@ def router_logits(w, x, n_expert, mode=ROUTER_AUTO):
                                      ctypes.c_void_p(shg.data_ptr()) if shg is not None else None,
                                      _stream()), "q36moe_router_logits")
     return logits, shg
+
+
+class GGUF:
+    """A GGUF v3 file mapped by the library (q36moe_gguf_*)."""
+
+    def __init__(self, path):
+        self._h = ctypes.c_void_p()
+        check(lib().q36moe_gguf_open(os.fsencode(path), ctypes.byref(self._h)), "q36moe_gguf_open")
+
+    def close(self):
+        if self._h:
+            lib().q36moe_gguf_close(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def info(self):
+        v, al = ctypes.c_uint32(), ctypes.c_uint32()
+        nt, nk, off = ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_uint64()
+        check(lib().q36moe_gguf_info(self._h, ctypes.byref(v), ctypes.byref(nt), ctypes.byref(nk),
+                                     ctypes.byref(al), ctypes.byref(off)), "q36moe_gguf_info")
+        return {"version": v.value, "n_tensors": nt.value, "n_kv": nk.value, "alignment": al.value,
+                "data_offset": off.value}
+
+    def tensor(self, name):
+        ty, nd = ctypes.c_uint32(), ctypes.c_uint32()
+        dims = (ctypes.c_uint64 * 4)()
+        off, nb = ctypes.c_uint64(), ctypes.c_uint64()
+        data = ctypes.c_void_p()
+        check(lib().q36moe_gguf_tensor(self._h, name.encode(), ctypes.byref(ty), ctypes.byref(nd), dims,
+                                       ctypes.byref(off), ctypes.byref(data), ctypes.byref(nb)),
+              "q36moe_gguf_tensor")
+        return {"type": ty.value, "n_dims": nd.value, "dims": list(dims), "file_offset": off.value,
+                "nbytes": nb.value}
+
+    def u32(self, key):
+        v = ctypes.c_uint32()
+        check(lib().q36moe_gguf_u32(self._h, key.encode(), ctypes.byref(v)), "q36moe_gguf_u32")
+        return v.value
+
+    def router(self, layer):
+        """Host f32 router rows [n_expert (+1 shared gate), d_model]."""
+        t = self.tensor(f"blk.{layer}.ffn_gate_inp.weight")
+        dst = np.empty((t["dims"][1] + 1) * t["dims"][0], dtype=np.float32)
+        nr, dm = ctypes.c_int(), ctypes.c_int()
+        check(lib().q36moe_router_from_gguf(self._h, layer, ctypes.c_void_p(dst.ctypes.data), dst.size,
+                                            ctypes.byref(nr), ctypes.byref(dm)), "q36moe_router_from_gguf")
+        return dst[: nr.value * dm.value].reshape(nr.value, dm.value).copy()
 
 
 def add_rmsnorm_quant(h, a, w, eps=1e-6, want_y=True, want_q=True):
