@@ -701,7 +701,7 @@ __device__ __forceinline__ v4f mfma_sel(int sel, const v8i &a, const v8i &b, con
 // against column tiles (w>>1) + 2j.  B rows sit in LDS as 256-byte lines of
 // two rows with the 16-byte slot index XORed by the line index, so the 16
 // lanes of a fragment read hit 16 distinct bank groups.
-constexpr int kGdTok = 192;                      // rows per fat tile (12 column tiles)
+constexpr int kGdTok = 160;                      // rows per fat tile (10 column tiles)
 
 __device__ __forceinline__ void dma16(const void *g, void *lds) {
     __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 0);
@@ -729,6 +729,7 @@ __device__ __forceinline__ int gd_boff(int r, int c) {
 
 namespace gdma {
 constexpr int RT = 4, W = 4, TOK = kGdTok;
+static_assert(TOK == 16 * 2 * 5, "column tiles per wave: at most 5 (the largest body instantiated)");
 constexpr int STA = 3, STB = 2;
 struct Lds {
     __align__(16) uint8_t a[STA][2 * RT * 1024];
@@ -790,6 +791,7 @@ __device__ __forceinline__ void body(const GemmArgs &A, Lds &L, const uint8_t *W
     issue_a(0, 0);
     issue_b(0, 0);
     issue_a(1, 1);
+    if (wave == 0) Q36_TRACE_AT(29);
 
     v4f acc[4][NJ1];
 #pragma unroll
@@ -815,6 +817,7 @@ __device__ __forceinline__ void body(const GemmArgs &A, Lds &L, const uint8_t *W
                 for (int j = 0; j < NJ; j++) asm volatile("" : "+v"(acc[a][j]));
             wait_vm(kt + 1 < NKT ? 2 : 0);
             dma_barrier();
+            if (wave == 0) Q36_TRACE_AT(30 + kt);
             if constexpr (st == 0) {
 #pragma unroll
                 for (int a = 0; a < 4; a++) {
@@ -857,6 +860,7 @@ __device__ __forceinline__ void body(const GemmArgs &A, Lds &L, const uint8_t *W
         });
     }
 
+    if (wave == 0) Q36_TRACE_AT(46);
     // SwiGLU of gate tile i and up tile i (i = 0, 1: one 32-row h block)
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
@@ -897,6 +901,8 @@ __global__ __launch_bounds__(256, 2) void k_gateup_dma(GemmArgs A) {
     const int ti = 8 * (jx / NRB) + xcd;
     const int mt0 = (jx % NRB) * gdma::RT;
     if (ti >= *A.ntiles) return;
+    Q36_TRACE_WG(0);
+    Q36_TRACE_AT(28);
     const int4 tile = A.tiles[ti];
     const int e = tile.x, p0 = tile.y, p1 = tile.z;
     const uint8_t *Wg = e < A.E ? A.wa + (size_t)e * A.wstride : A.sa;
@@ -910,9 +916,10 @@ __global__ __launch_bounds__(256, 2) void k_gateup_dma(GemmArgs A) {
         case 2: gdma::body<2>(A, L, Wg, Wu, mt0, p0, p1); break;
         case 3: gdma::body<3>(A, L, Wg, Wu, mt0, p0, p1); break;
         case 4: gdma::body<4>(A, L, Wg, Wu, mt0, p0, p1); break;
-        case 5: gdma::body<5>(A, L, Wg, Wu, mt0, p0, p1); break;
-        default: gdma::body<6>(A, L, Wg, Wu, mt0, p0, p1); break;
+        default: gdma::body<5>(A, L, Wg, Wu, mt0, p0, p1); break;
     }
+    Q36_TRACE_AT(47);
+    Q36_TRACE_WG(1);
 }
 
 // ---------------------------------------------------------------------------
