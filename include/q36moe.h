@@ -159,7 +159,7 @@ int q36moe_forward_q8(q36moe_ctx *c, const q36moe_weights *w, const uint8_t *xq,
                       void *out, int out_fmt);
 
 /* Execution path of q36moe_forward.  The sorted path (route + sort + grouped
- * expert GEMMs + combine) serves any T, with fat tiles (up to 192 rows per
+ * expert GEMMs + combine) serves any T, with fat tiles (up to 160 rows per
  * expert tile, weights staged through LDS) or skinny tiles (up to 32 rows,
  * weights streamed straight into registers); the direct path (no sort,
  * slots combined in registers) serves T <= 16 as two kernels (gate/up, then
