@@ -676,7 +676,10 @@ struct GemmArgs {
 };
 
 // op_sel byte of both scale dwords (A and B hold 4 K-steps each), fixed once
-// the K loop is unrolled
+// the K loop is unrolled.  `sel` must be a compile-time constant or
+// wave-uniform as the compiler sees it (readfirstlane): a per-lane value
+// turns the switch into EXEC-masked branches around the MFMAs, which gave
+// wrong results on gfx950.
 __device__ __forceinline__ v4f mfma_sel(int sel, const v8i &a, const v8i &b, const v4f &c, int sa, int sb) {
     switch (sel & 3) {
         case 0: return mfma_f4xf8<0, 0>(a, b, c, sa, sb);
@@ -908,7 +911,7 @@ __global__ __launch_bounds__(256, 2) void k_gateup_dma(GemmArgs A) {
     const uint8_t *Wg = e < A.E ? A.wa + (size_t)e * A.wstride : A.sa;
     const uint8_t *Wu = e < A.E ? A.wb + (size_t)e * A.wstride : A.sb;
     const int ntt = (p1 - p0 + 15) >> 4;
-    const int wt = (threadIdx.x >> 6) >> 1;
+    const int wt = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) >> 1;   // uniform: the switch below is a scalar branch
     const int nj = ntt > wt ? (ntt - wt + 1) >> 1 : 0;
     switch (nj) {
         case 0: gdma::body<0>(A, L, Wg, Wu, mt0, p0, p1); break;
@@ -1004,7 +1007,7 @@ __global__ __launch_bounds__(256) void k_router_f16(const float *__restrict__ W,
                                                     const void *__restrict__ x, int x_fmt, int T,
                                                     float *__restrict__ logits, int ld,
                                                     float *__restrict__ shg) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, n = lane & 15, g = lane >> 4;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), n = lane & 15, g = lane >> 4;
     const int r0 = blockIdx.x * 64, t0 = blockIdx.y * 64 + wave * 16;
     const int tok = min(t0 + n, T - 1);                  // padding columns repeat the last token
     int rows[4];
@@ -1100,7 +1103,10 @@ template <int NJ>
 __device__ __forceinline__ void skinny_gateup(const GemmArgs &A, const uint8_t *Wg, const uint8_t *Wu,
                                               int mt0, int p0, int p1, float (*red)[4][64][4]) {
     constexpr int KD = 2048, NKT = KD / 128;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q = lane >> 4;
+    // the wave index is made wave-uniform for the compiler: the MFMA op_sel
+    // below depends on it and must be chosen by scalar branches
+    const int tid = threadIdx.x, lane = tid & 63, q = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const size_t nib = (size_t)512 * KD / 2;
     // this wave's K-steps: 2w and 2w+1 (one scale dword group, op_sel 2w%4 and +1)
     const int kt0 = 2 * wave, g = kt0 >> 2;
@@ -1242,7 +1248,7 @@ __global__ __launch_bounds__(64 * kDlW) void k_down_lds(GemmArgs A) {
     Q36_TRACE_AT(48);
     const int4 tile = A.tiles[ti];
     const int e = tile.x, p0 = tile.y, p1 = tile.z;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q = lane >> 4, n = lane & 15;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), q = lane >> 4, n = lane & 15;
     const uint8_t *W = e < A.E ? A.wa + (size_t)e * A.wstride : A.sa;
     const size_t nib = (size_t)2048 * KD / 2;
     // this wave's A: row tiles mt0 + i, all 4 K-steps
@@ -1362,7 +1368,7 @@ __device__ __forceinline__ void direct_gateup_body(const DirectArgs &A, int i, i
     uint8_t *sxs = L_.sxs;
     auto &red = L_.red;
     auto &rlds = L_.rlds;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int nr = A.T * A.k;
     const bool routed = i < nr;
     const int t = routed ? i / A.k : i - nr;
@@ -1492,7 +1498,7 @@ __global__ __launch_bounds__(576) void k_direct_down(DirectArgs A) {
     __shared__ uint8_t shs[kMaxTopK + 1][kDF / 32];
     __shared__ float red[kMaxTopK + 1][16];
     const int rt = blockIdx.x, t = blockIdx.y;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int nslot = blockDim.x >> 6;
     const int nr = A.T * A.k;
     const bool routed = wave < A.k;
@@ -1570,7 +1576,7 @@ __global__ __launch_bounds__(256) void k_decode_fused(DirectArgs A) {
     }
     const int d = bid - A.n_gateup_wg;
     const int t = d / (kDD / 16), rt = d % (kDD / 16);
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const bool has_sh = A.sh_down != nullptr;
     const int nslot = A.k + (has_sh ? 1 : 0);
     // slots of this wave: wave, wave + 4, wave + 8
