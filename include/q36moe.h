@@ -8,6 +8,13 @@
  * Reference interfaces replaced (file:line in the q36 tree):
  *   q36moe_weights_upload  <- upload() MXFP4 expert branch, q36_engine.cu:196-228
  *                             (GGUF block_mxfp4 [E][M][K/32], q36.h:112-114)
+ *   q36moe_weights_upload_typed
+ *                          <- upload() with its Q5_K / Q6_K expert branch,
+ *                             q36_engine.cu:229-252 (requantised to q8_0-split,
+ *                             h_q8_row :73-86); the down projection of such
+ *                             experts runs as k_gemm_expert_i8 (:2526-2618)
+ *                             after k_quant_q8b (:2627-2640)
+ *   q36moe_requant_q8      <- that branch's host repack, one matrix
  *   q36moe_ctx_create      <- MoE scratch allocated in q36_engine_create,
  *                             q36_engine.cu:1467-1512 (no allocation in forward)
  *   q36moe_forward         <- moe_ffn, q36_engine.cu:1592-1654 (decode) and
@@ -59,6 +66,8 @@ extern "C" {
 #define Q36MOE_TAP_HQ        7  /* u8    [T*k+T][d_ff] e4m3 SwiGLU rows */
 #define Q36MOE_TAP_HS        8  /* u8    [T*k+T][d_ff/32] E8M0          */
 #define Q36MOE_TAP_DNW       9  /* f32   [T*k+T][d_model] w * down rows */
+#define Q36MOE_TAP_HSF      10  /* f32   [T*k+T][d_ff/32] int8 h scales
+                                   (q8_0-split down; HQ then holds int8) */
 
 typedef struct q36moe_weights q36moe_weights;
 typedef struct q36moe_ctx q36moe_ctx;
@@ -79,6 +88,24 @@ int q36moe_weights_upload(const void *gate, const void *up, const void *down,
                           const void *sh_gate, const void *sh_up, const void *sh_down,
                           int n_expert, int d_model, int d_ff, int d_ff_sh,
                           q36moe_weights **out);
+
+/* As q36moe_weights_upload, with the routed down projection in any of the
+ * reference's expert types: down_type is the ggml type of `down` --
+ * 39 MXFP4 (the call above), 13 Q5_K, 14 Q6_K (super-blocks of 256, so
+ * d_ff % 256 == 0) or 8 Q8_0 -- as [n_expert][d_model][row blocks].  A
+ * Q5_K / Q6_K down is dequantised and requantised on the host to int8 codes
+ * with one f16 scale per 32 (the reference's q8_0-split layout), a Q8_0 one
+ * is split as it is.  Such a layer quantises h per 32 to int8 with an fp32
+ * scale (d = amax/127) and runs the down projection on int8 MFMA, each
+ * 32-block's integer dot product scaled by both f16 and fp32 scales.  The
+ * shared expert (sh_*) stays MXFP4.  Decode path 3 (the one-kernel variant)
+ * is MXFP4-only: forward with it on such weights is EINVAL. */
+int q36moe_weights_upload_typed(const void *gate, const void *up, const void *down, int down_type,
+                                const void *sh_gate, const void *sh_up, const void *sh_down,
+                                int n_expert, int d_model, int d_ff, int d_ff_sh,
+                                q36moe_weights **out);
+/* ggml type of the routed down projection of w as uploaded (39 or 8). */
+int q36moe_weights_down_type(const q36moe_weights *w);
 
 /* Allocate a weight set on the device without filling it; the caller fills
  * the packed buffers returned by q36moe_weights_device_ptrs (e.g. with
@@ -104,6 +131,19 @@ int q36moe_weights_fill_synthetic(q36moe_weights *w, uint64_t seed, int exp_lo, 
  * device layout (and back).  Pure host code; used by upload and by tests. */
 int q36moe_pack_mxfp4(const void *gguf_blocks, int M, int K, void *packed);
 int q36moe_unpack_mxfp4(const void *packed, int M, int K, void *gguf_blocks);
+
+/* Host-side: one [M][K] matrix of GGUF blocks of ggml_type (8 Q8_0, 13
+ * Q5_K, 14 Q6_K) to the q8_0-split layout: codes [M][K] int8 and f16
+ * scales [M][K/32] (bit patterns), value = scale * code.  Q5_K / Q6_K are
+ * dequantised exactly as q36_dequant.cuh:128-165 and requantised per 32
+ * with d = amax/127 rounded to f16 and codes rint(v * (1/d)) clamped to
+ * [-128, 127] (h_q8_row, q36_engine.cu:73-86). */
+int q36moe_requant_q8(int ggml_type, const void *src, int M, int K, int8_t *codes, uint16_t *scales);
+/* Host-side repack of a q8_0-split matrix into the packed device layout
+ * (M*K code bytes then M*K/16 scale bytes), and back.  An inf/NaN scale
+ * -> EINVAL.  M % 16 == 0, K % 64 == 0. */
+int q36moe_pack_q8(const int8_t *codes, const uint16_t *scales, int M, int K, void *packed);
+int q36moe_unpack_q8(const void *packed, int M, int K, int8_t *codes, uint16_t *scales);
 
 /* Context: per-stream scratch for up to max_tokens tokens.  All scratch is
  * allocated here; q36moe_forward allocates nothing. */
@@ -219,10 +259,12 @@ int q36moe_gguf_info(const q36moe_gguf *g, uint32_t *version, uint64_t *n_tensor
 int q36moe_gguf_tensor(const q36moe_gguf *g, const char *name, uint32_t *ggml_type, uint32_t *n_dims,
                        uint64_t *dims, uint64_t *file_offset, const void **data, uint64_t *nbytes);
 int q36moe_gguf_u32(const q36moe_gguf *g, const char *key, uint32_t *out);
-/* Uploads block `layer`'s experts: blk.N.ffn_{gate,up,down}_exps.weight,
- * MXFP4 (ggml type 39) of ggml dims [d_model][d_ff][E] / [d_ff][d_model][E];
- * with with_shared, also blk.N.ffn_{gate,up,down}_shexp.weight (MXFP4 only:
- * the reference's Q8_0 shared expert is EINVAL here). */
+/* Uploads block `layer`'s experts: blk.N.ffn_{gate,up,down}_exps.weight of
+ * ggml dims [d_model][d_ff][E] / [d_ff][d_model][E]; gate and up MXFP4
+ * (ggml type 39), down MXFP4, Q5_K, Q6_K or Q8_0 (as
+ * q36moe_weights_upload_typed); with with_shared, also
+ * blk.N.ffn_{gate,up,down}_shexp.weight (MXFP4 only: a Q8_0 shared expert
+ * is EINVAL here). */
 int q36moe_weights_from_gguf(const q36moe_gguf *g, int layer, int with_shared, q36moe_weights **out);
 /* The router rows of block `layer` as host f32 for q36moe_router_logits:
  * blk.N.ffn_gate_inp.weight [n_expert][d_model] (F32 or BF16, widened

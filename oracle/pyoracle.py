@@ -48,6 +48,15 @@ def lib():
         L.or_expert_down.argtypes = [vp, i, i, vp, vp]
         L.or_moe_forward.argtypes = [vp, vp, vp, i, vp, i, i, f, i, vp, i, vp]
         L.or_moe_forward_f32.argtypes = [vp, vp, vp, i, vp, i, i, f, vp, i]
+        L.or_f16_encode.argtypes = [ctypes.c_float]
+        L.or_f16_encode.restype = ctypes.c_uint16
+        L.or_f16_decode.argtypes = [ctypes.c_uint16]
+        L.or_f16_decode.restype = ctypes.c_float
+        L.or_deq_row.argtypes = [ctypes.c_uint32, vp, i, vp]
+        L.or_requant_q8_row.argtypes = [vp, i, vp, vp]
+        L.or_requant_q8.argtypes = [ctypes.c_uint32, vp, i, i, vp, vp]
+        L.or_quant_q8b.argtypes = [vp, i, vp, vp]
+        L.or_expert_down_q8.argtypes = [vp, vp, i, i, vp, vp]
         _lib = L
     return _lib
 
@@ -60,15 +69,24 @@ class _W(ctypes.Structure):
     _fields_ = [("gate", ctypes.c_void_p), ("up", ctypes.c_void_p), ("down", ctypes.c_void_p),
                 ("sh_gate", ctypes.c_void_p), ("sh_up", ctypes.c_void_p), ("sh_down", ctypes.c_void_p),
                 ("n_expert", ctypes.c_int), ("d_model", ctypes.c_int), ("d_ff", ctypes.c_int),
-                ("d_ff_sh", ctypes.c_int)]
+                ("d_ff_sh", ctypes.c_int), ("down_q8", ctypes.c_void_p), ("down_q8d", ctypes.c_void_p)]
 
 
 def _wstruct(w):
-    keep = {k: np.ascontiguousarray(v, dtype=np.uint8) for k, v in w.items()}
+    """w: gate/up (/down) GGUF MXFP4 blocks [E][M][K/32][17], optional
+    sh_*; or down_q8 (int8 [E][D][FF]) + down_q8d (f16 bits [E][D][FF/32])
+    for the q8_0-split routed down."""
+    keep = {}
+    for k, v in w.items():
+        if v is None:
+            continue
+        dt = {"down_q8": np.int8, "down_q8d": np.uint16}.get(k, np.uint8)
+        keep[k] = np.ascontiguousarray(v, dtype=dt)
     E, FF, nb, _ = keep["gate"].shape
-    s = _W(_p(keep["gate"]), _p(keep["up"]), _p(keep["down"]),
+    s = _W(_p(keep["gate"]), _p(keep["up"]), _p(keep.get("down")),
            _p(keep.get("sh_gate")), _p(keep.get("sh_up")), _p(keep.get("sh_down")),
-           E, nb * 32, FF, keep["sh_gate"].shape[0] if "sh_gate" in keep else 0)
+           E, nb * 32, FF, keep["sh_gate"].shape[0] if "sh_gate" in keep else 0,
+           _p(keep.get("down_q8")), _p(keep.get("down_q8d")))
     return s, keep
 
 
@@ -182,6 +200,59 @@ def expert_down(down_e, hd):
     return y
 
 
+# ---- Q8 formats ----
+def f16_encode(v):
+    return lib().or_f16_encode(float(v))
+
+
+def f16_decode(h):
+    return lib().or_f16_decode(int(h))
+
+
+def deq_row(ggml_type, blocks, n):
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    out = np.empty(n, dtype=np.float32)
+    if lib().or_deq_row(ggml_type, _p(blocks), n, _p(out)) != 0:
+        raise ValueError("unsupported type or size")
+    return out
+
+
+def requant_q8_row(x):
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    qs = np.empty(x.size, dtype=np.int8)
+    ds = np.empty(x.size // 32, dtype=np.uint16)
+    lib().or_requant_q8_row(_p(x), x.size, _p(qs), _p(ds))
+    return qs, ds
+
+
+def requant_q8(ggml_type, src, M, K):
+    """One expert matrix of GGUF blocks -> (codes int8 [M][K], f16 bits [M][K/32])."""
+    src = np.ascontiguousarray(src, dtype=np.uint8)
+    qs = np.empty((M, K), dtype=np.int8)
+    ds = np.empty((M, K // 32), dtype=np.uint16)
+    if lib().or_requant_q8(ggml_type, _p(src), M, K, _p(qs), _p(ds)) != 0:
+        raise ValueError("unsupported type or size")
+    return qs, ds
+
+
+def quant_q8b(x):
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    q = np.empty(x.size, dtype=np.int8)
+    d = np.empty(x.size // 32, dtype=np.float32)
+    lib().or_quant_q8b(_p(x), x.size, _p(q), _p(d))
+    return q, d
+
+
+def expert_down_q8(qs, ds, hd):
+    qs = np.ascontiguousarray(qs, dtype=np.int8)
+    ds = np.ascontiguousarray(ds, dtype=np.uint16)
+    hd = np.ascontiguousarray(hd, dtype=np.float64)
+    D, FF = qs.shape
+    y = np.empty(D, dtype=np.float64)
+    lib().or_expert_down_q8(_p(qs), _p(ds), D, FF, _p(hd), _p(y))
+    return y
+
+
 def moe_forward(w, x, logits, shg=None, k=8, scale=1.0, act_mode=0, tokens=None):
     """double [n_tok, d_model]; act_mode 0 = W4A8, 1 = W4A32."""
     s, keep = _wstruct(w)
@@ -223,5 +294,8 @@ def ref_lib():
         L.ref_e8m0_half.restype = ctypes.c_float
         L.ref_deq_row_mxfp4.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
         L.ref_sizeof_block_mxfp4.restype = ctypes.c_int
+        L.ref_deq_row.argtypes = [ctypes.c_uint32, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+        L.ref_fp16.argtypes = [ctypes.c_uint16]
+        L.ref_fp16.restype = ctypes.c_float
         _ref = L
     return _ref

@@ -18,6 +18,14 @@
  *       (logit desc, index asc) and fp64 softmax.
  *   or_sort                             -- brute force + bijection /
  *       histogram / scan invariants.
+ *   or_f16_encode / or_f16_decode       -- numpy float16 (an independent
+ *       library routine) over every f16 pattern and every rounding tie.
+ *   or_deq_q8_0 / _q5_K / _q6_K         -- the reference's own q36_deq_row
+ *       compiled from its header (oracle/_ref/), bit-exact on random
+ *       blocks, plus hand-computed single-element cases.
+ *   or_requant_q8_row / or_quant_q8b    -- closed forms of
+ *       q36_engine.cu:73-86 and :2627-2640 plus invariants (|q| <= 127 /
+ *       128, the block maximum maps to +-127, numpy rint / float16).
  *   or_gemv_* / or_moe_forward          -- fp64 brute force on tiny shapes
  *       and closed forms (rank-1 weights, single non-zero block, linearity
  *       in the routing weights).
@@ -263,6 +271,190 @@ void or_gemv_mxfp4_f32_mt(const uint8_t *W, int M, int K,
 /* ---------------------------------------------------------------------- */
 /* Whole layer                                                             */
 /* ---------------------------------------------------------------------- */
+/* ---------------------------------------------------------------------- */
+/* Q8 formats: the reference's requantised expert layout (q8_0-split)      */
+/* ---------------------------------------------------------------------- */
+
+/* IEEE binary16 from float, round to nearest even, overflow to inf (the
+ * __float2half conversion of the reference's h_f16, q36_engine.cu:69-71). */
+uint16_t or_f16_encode(float f) {
+    uint32_t u; memcpy(&u, &f, 4);
+    uint32_t sign = (u >> 16) & 0x8000u, a = u & 0x7fffffffu;
+    if (a > 0x7f800000u) return (uint16_t)(sign | 0x7e00u);           /* NaN */
+    if (a >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);          /* >= 65520 -> inf */
+    if (a < 0x38800000u) {                                            /* below 2^-14: subnormal */
+        float q = fabsf(f) * 16777216.0f;                              /* units of 2^-24 (exact) */
+        return (uint16_t)(sign | (uint32_t)rintf(q));
+    }
+    uint32_t r = ((a >> 13) - (112u << 10));                           /* rebias 127 -> 15 */
+    uint32_t rem = a & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (r & 1u))) r++;
+    return (uint16_t)(sign | r);
+}
+
+float or_f16_decode(uint16_t h) {
+    int s = h >> 15, e = (h >> 10) & 31, m = h & 1023;
+    float v;
+    if (e == 31) v = m ? NAN : INFINITY;
+    else if (e == 0) v = ldexpf((float)m, -24);
+    else v = ldexpf((float)(1024 + m), e - 25);
+    return s ? -v : v;
+}
+
+/* Q8_0 block (34 B: f16 d, 32 int8): d * q  (q36_dequant.cuh:116-119). */
+void or_deq_q8_0_block(const uint8_t *b, float *out) {
+    uint16_t dh; memcpy(&dh, b, 2);
+    float d = or_f16_decode(dh);
+    for (int j = 0; j < 32; j++) out[j] = d * (float)(int8_t)b[2 + j];
+}
+
+/* 6-bit scale / min of sub-block j of a Q5_K super-block (q36_dequant.cuh:
+ * 121-126, ggml get_scale_min_k4): sub-blocks 0-3 take the low 6 bits of
+ * bytes j and j+4; 4-7 take a nibble of byte j+4 and the top two bits of
+ * bytes j-4 (scale) and j (min). */
+static void k4_scale_min(int j, const uint8_t *q, int *sc, int *mn) {
+    if (j < 4) {
+        *sc = q[j] & 63;
+        *mn = q[j + 4] & 63;
+    } else {
+        *sc = (q[j + 4] & 15) | ((q[j - 4] >> 6) << 4);
+        *mn = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+    }
+}
+
+/* Q5_K super-block (176 B: f16 d, f16 dmin, scales[12], qh[32], qs[128]),
+ * 256 values (q36_dequant.cuh:128-142).  Value i = 64c + 32h + l (chunk c,
+ * half h): 5-bit q = nibble h of qs[32c + l] | bit (2c + h) of qh[l] << 4;
+ * y = (d*sc) * q - (dmin*mn) for sub-block 2c + h. */
+void or_deq_q5_K_block(const uint8_t *b, float *out) {
+    uint16_t dh, mh; memcpy(&dh, b, 2); memcpy(&mh, b + 2, 2);
+    const float d = or_f16_decode(dh), dmin = or_f16_decode(mh);
+    const uint8_t *sc = b + 4, *qh = b + 16, *qs = b + 48;
+    for (int c = 0; c < 4; c++)
+        for (int h = 0; h < 2; h++) {
+            int s, m;
+            k4_scale_min(2 * c + h, sc, &s, &m);
+            const float d1 = d * (float)s, m1 = dmin * (float)m;
+            for (int l = 0; l < 32; l++) {
+                int q = (h ? qs[32 * c + l] >> 4 : qs[32 * c + l] & 15) |
+                        (((qh[l] >> (2 * c + h)) & 1) << 4);
+                float t = d1 * (float)q;   /* product, then difference: no fused multiply-add */
+                out[64 * c + 32 * h + l] = t - m1;
+            }
+        }
+}
+
+/* Q6_K super-block (210 B: ql[128], qh[64], int8 scales[16], f16 d), 256
+ * values (q36_dequant.cuh:144-165).  Half n (128 values), quarter g, lane l:
+ * 6-bit q = nibble (g >= 2) of ql[64n + 32(g & 1) + l] | bits 2g..2g+1 of
+ * qh[32n + l] << 4, minus 32; y = d * sc[8n + 2g + l/16] * q. */
+void or_deq_q6_K_block(const uint8_t *b, float *out) {
+    const uint8_t *ql = b, *qh = b + 128;
+    const int8_t *sc = (const int8_t *)(b + 192);
+    uint16_t dh; memcpy(&dh, b + 208, 2);
+    const float d = or_f16_decode(dh);
+    for (int n = 0; n < 2; n++)
+        for (int g = 0; g < 4; g++)
+            for (int l = 0; l < 32; l++) {
+                int lo = ql[64 * n + 32 * (g & 1) + l];
+                lo = g >= 2 ? lo >> 4 : lo & 15;
+                int q = (lo | (((qh[32 * n + l] >> (2 * g)) & 3) << 4)) - 32;
+                float t = d * (float)sc[8 * n + 2 * g + l / 16];
+                out[128 * n + 32 * g + l] = t * (float)q;
+            }
+}
+
+int or_deq_row(uint32_t type, const void *blocks, int n, float *out) {
+    const uint8_t *p = (const uint8_t *)blocks;
+    switch (type) {
+        case 8:  if (n % 32) return -1; for (int i = 0; i < n / 32; i++) or_deq_q8_0_block(p + 34 * i, out + 32 * i); return 0;
+        case 13: if (n % 256) return -1; for (int i = 0; i < n / 256; i++) or_deq_q5_K_block(p + 176 * i, out + 256 * i); return 0;
+        case 14: if (n % 256) return -1; for (int i = 0; i < n / 256; i++) or_deq_q6_K_block(p + 210 * i, out + 256 * i); return 0;
+        case 39: if (n % 32) return -1; or_deq_mxfp4_row(p, n, out); return 0;
+        default: return -1;
+    }
+}
+
+/* h_q8_row (q36_engine.cu:73-86): per 32 values d = amax/127 (fp32),
+ * stored as f16; q = rint(v * (1/d)) with 1/d from the fp32 d, clamped to
+ * [-128, 127]. */
+void or_requant_q8_row(const float *x, int K, int8_t *qs, uint16_t *ds) {
+    for (int b = 0; b < K / 32; b++) {
+        float amax = 0.0f;
+        for (int j = 0; j < 32; j++) { float v = fabsf(x[32 * b + j]); if (v > amax) amax = v; }
+        const float d = amax / 127.0f, id = d != 0.0f ? 1.0f / d : 0.0f;
+        ds[b] = or_f16_encode(d);
+        for (int j = 0; j < 32; j++) {
+            long q = lrintf(x[32 * b + j] * id);
+            qs[32 * b + j] = (int8_t)(q > 127 ? 127 : q < -128 ? -128 : q);
+        }
+    }
+}
+
+/* One expert matrix of M rows x K from GGUF blocks of `type` to the
+ * q8_0-split layout (codes [M][K], f16 scales [M][K/32]).  Q5_K / Q6_K are
+ * dequantised and requantised as the reference's upload does
+ * (q36_engine.cu:229-252); Q8_0 blocks are split as they are. */
+int or_requant_q8(uint32_t type, const void *src, int M, int K, int8_t *qs, uint16_t *ds) {
+    size_t rb;
+    if (type == 13) rb = (size_t)K / 256 * 176;
+    else if (type == 14) rb = (size_t)K / 256 * 210;
+    else if (type == 8) rb = (size_t)K / 32 * 34;
+    else return -1;
+    if (K % (type == 8 ? 32 : 256)) return -1;
+    float *row = (float *)malloc(sizeof(float) * (size_t)K);
+    for (int r = 0; r < M; r++) {
+        const uint8_t *p = (const uint8_t *)src + rb * r;
+        if (type == 8) {
+            for (int b = 0; b < K / 32; b++) {
+                memcpy(&ds[(size_t)r * (K / 32) + b], p + 34 * b, 2);
+                memcpy(&qs[(size_t)r * K + 32 * b], p + 34 * b + 2, 32);
+            }
+        } else {
+            or_deq_row(type, p, K, row);
+            or_requant_q8_row(row, K, qs + (size_t)r * K, ds + (size_t)r * (K / 32));
+        }
+    }
+    free(row);
+    return 0;
+}
+
+/* k_quant_q8b (q36_engine.cu:2627-2640): per 32 values d = amax/127,
+ * q = rint(v * 127/amax) clamped to [-127, 127] (0 for an all-zero block).
+ * The reference divides with CUDA's fast __fdividef; this is the IEEE
+ * quotient. */
+void or_quant_q8b(const float *x, int K, int8_t *q, float *d) {
+    for (int b = 0; b < K / 32; b++) {
+        float a = 0.0f;
+        for (int j = 0; j < 32; j++) a = fmaxf(a, fabsf(x[32 * b + j]));
+        const float id = a > 0.0f ? 127.0f / a : 0.0f;
+        d[b] = a / 127.0f;
+        for (int j = 0; j < 32; j++) {
+            long v = lrintf(x[32 * b + j] * id);
+            q[32 * b + j] = (int8_t)(v > 127 ? 127 : v < -127 ? -127 : v);
+        }
+    }
+}
+
+/* y[r] = sum_b f16(ds[r][b]) * sum_j qs[r][32b+j] * h[32b+j] over q8_0-split
+ * rows, h in double (the down GEMV of the requantised layout,
+ * q36_engine.cu:736-741). */
+static void mv_q8_d(const int8_t *qs, const uint16_t *ds, int M, int K, const double *h, double *y) {
+    for (int r = 0; r < M; r++) {
+        double acc = 0.0;
+        for (int b = 0; b < K / 32; b++) {
+            double p = 0.0;
+            for (int j = 0; j < 32; j++) p += (double)qs[(size_t)r * K + 32 * b + j] * h[32 * b + j];
+            acc += (double)or_f16_decode(ds[(size_t)r * (K / 32) + b]) * p;
+        }
+        y[r] = acc;
+    }
+}
+
+void or_expert_down_q8(const int8_t *qs, const uint16_t *ds, int D, int FF, const double *h, double *y) {
+    mv_q8_d(qs, ds, D, FF, h, y);
+}
+
 static double silu_d(double g) { return g / (1.0 + exp(-g)); }
 static double sigm_d(double g) { return 1.0 / (1.0 + exp(-g)); }
 
@@ -295,6 +487,7 @@ static void quant_roundtrip(const float *v, int K, double *out) {
  * W4A8 prefill path (q36_engine.cu:2411-2428, :3437-3441) applied to x and
  * to the SwiGLU output when act_mode==0. */
 static void expert_d(const uint8_t *g, const uint8_t *u, const uint8_t *d,
+                     const int8_t *dq, const uint16_t *dd,
                      int D, int FF, const double *xin, int act_mode, double *out) {
     double *gv = (double *)malloc(sizeof(double) * (size_t)FF);
     double *uv = (double *)malloc(sizeof(double) * (size_t)FF);
@@ -303,9 +496,25 @@ static void expert_d(const uint8_t *g, const uint8_t *u, const uint8_t *d,
     mv_d(g, FF, D, xin, gv);
     mv_d(u, FF, D, xin, uv);
     for (int f = 0; f < FF; f++) hf[f] = (float)(silu_d(gv[f]) * uv[f]);
-    if (act_mode == 0) quant_roundtrip(hf, FF, hd);
-    else for (int f = 0; f < FF; f++) hd[f] = hf[f];
-    mv_d(d, D, FF, hd, out);
+    if (dq) {
+        /* q8_0-split down (the reference's requantised Q5_K / Q6_K experts):
+         * h quantised per 32 to int8 with an fp32 scale (k_quant_q8b ->
+         * k_gemm_expert_i8, q36_engine.cu:3452-3458) under act_mode 0 */
+        if (act_mode == 0) {
+            int8_t *q = (int8_t *)malloc((size_t)FF);
+            float *hs = (float *)malloc(sizeof(float) * (size_t)FF / 32);
+            or_quant_q8b(hf, FF, q, hs);
+            for (int f = 0; f < FF; f++) hd[f] = (double)q[f] * (double)hs[f / 32];
+            free(q); free(hs);
+        } else {
+            for (int f = 0; f < FF; f++) hd[f] = hf[f];
+        }
+        mv_q8_d(dq, dd, D, FF, hd, out);
+    } else {
+        if (act_mode == 0) quant_roundtrip(hf, FF, hd);
+        else for (int f = 0; f < FF; f++) hd[f] = hf[f];
+        mv_d(d, D, FF, hd, out);
+    }
     free(gv); free(uv); free(hd); free(hf);
 }
 
@@ -348,11 +557,13 @@ void or_moe_forward(const or_weights *w, const float *x, const float *logits,
          * (k_moe_combine, q36_engine.cu:784-791; k_moe_combine_pf :3393-3401) */
         for (int s = 0; s < k; s++) {
             int e = idx[s];
-            expert_d(w->gate + es * e, w->up + es * e, w->down + ds * e, D, FF, xd, act_mode, y);
+            expert_d(w->gate + es * e, w->up + es * e, w->down ? w->down + ds * e : 0,
+                     w->down_q8 ? w->down_q8 + (size_t)D * FF * e : 0,
+                     w->down_q8 ? w->down_q8d + (size_t)D * (FF / 32) * e : 0, D, FF, xd, act_mode, y);
             for (int j = 0; j < D; j++) o[j] += wt[s] * y[j];
         }
         if (shg && w->sh_gate) {
-            expert_d(w->sh_gate, w->sh_up, w->sh_down, D, w->d_ff_sh, xd, act_mode, y);
+            expert_d(w->sh_gate, w->sh_up, w->sh_down, 0, 0, D, w->d_ff_sh, xd, act_mode, y);
             double gsh = sigm_d((double)shg[t]);
             for (int j = 0; j < D; j++) o[j] += gsh * y[j];
         }
@@ -388,6 +599,7 @@ static void quant_roundtrip_f(const float *v, int K, float *out) {
 void or_moe_forward_f32(const or_weights *w, const float *x, const float *logits,
                         int ld_logits, const float *shg, int T, int k,
                         float scale, float *out, int nthreads) {
+    if (!w->down) return;   /* MXFP4 down only (the timed baseline's format) */
     int D = w->d_model, FF = w->d_ff, E = w->n_expert;
     int FFm = FF > w->d_ff_sh ? FF : w->d_ff_sh;
     size_t es = (size_t)FF * (D / 32) * 17, ds = (size_t)D * (FF / 32) * 17;

@@ -56,11 +56,28 @@ void or_gemv_mxfp4_f32_mt(const uint8_t *W, int M, int K,
                           const uint8_t *xq, const uint8_t *xs, float *y,
                           int nthreads);
 
+/* ---- Q8 formats (requantised expert layout) ---------------------------- */
+uint16_t or_f16_encode(float f);           /* IEEE binary16, RNE            */
+float  or_f16_decode(uint16_t h);
+void or_deq_q8_0_block(const uint8_t *b34, float *out32);
+void or_deq_q5_K_block(const uint8_t *b176, float *out256);
+void or_deq_q6_K_block(const uint8_t *b210, float *out256);
+/* ggml type 8 / 13 / 14 / 39; -1 for another type or a ragged n */
+int  or_deq_row(uint32_t type, const void *blocks, int n, float *out);
+void or_requant_q8_row(const float *x, int K, int8_t *qs, uint16_t *ds);
+int  or_requant_q8(uint32_t type, const void *src, int M, int K, int8_t *qs, uint16_t *ds);
+void or_quant_q8b(const float *x, int K, int8_t *q, float *d);
+void or_expert_down_q8(const int8_t *qs, const uint16_t *ds, int D, int FF, const double *h, double *y);
+
 /* ---- the whole layer --------------------------------------------------- */
 typedef struct {
     const uint8_t *gate, *up, *down;          /* GGUF blocks [E][M][K/32]   */
     const uint8_t *sh_gate, *sh_up, *sh_down; /* GGUF blocks [M][K/32] or 0 */
     int n_expert, d_model, d_ff, d_ff_sh;
+    /* routed down in the q8_0-split layout instead of `down` (NULL = MXFP4):
+     * codes [E][d_model][d_ff] int8, f16 scales [E][d_model][d_ff/32] */
+    const int8_t *down_q8;
+    const uint16_t *down_q8d;
 } or_weights;
 
 /* act_mode 0: W4A8 -- x and h quantised exactly as the product does

@@ -13,3 +13,8 @@ void ref_deq_row_mxfp4(const uint8_t *blocks, int n, float *out) {
     q36_deq_row(Q36_GGML_MXFP4, blocks, n, out);
 }
 int ref_sizeof_block_mxfp4(void) { return (int)sizeof(block_mxfp4); }
+/* any type q36_deq_row handles (Q8_0, MXFP4, Q5_K, Q6_K, F32) */
+void ref_deq_row(uint32_t type, const void *blocks, int n, float *out) {
+    q36_deq_row(type, blocks, n, out);
+}
+float ref_fp16(uint16_t h) { return q36_fp16(h); }

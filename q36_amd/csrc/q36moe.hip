@@ -52,6 +52,7 @@ __device__ unsigned long long g_q36_wg[2 * 4096];
 #define Q36_TRACE_WG(n) do {} while (0)
 #endif
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef int v4i __attribute__((ext_vector_type(4)));
 
 namespace {
 
@@ -673,7 +674,62 @@ struct GemmArgs {
     uint8_t *hq, *hs, *hs2;   // GATEUP output rows (sorted slot): h, natural and lane-major scales
     float *dnw;               // DOWN output rows (sorted slot), weighted
     int ldo;                  // output row length
+    // q8_0-split routed down: GATEUP writes the routed rows of h as int8
+    // with fp32 scales (hsf [row][ldo/32]); DOWN reads them from bsf
+    int hq8;
+    float *hsf; const float *bsf;
 };
+
+// The per-32 int8 quantiser of h for a q8_0-split down (k_quant_q8b,
+// q36_engine.cu:2627-2640): d = amax/127, code = rint(v * 127/amax) clamped
+// to [-127, 127], all zero for an all-zero block.
+__device__ __forceinline__ float q8b_inv(float amax) { return amax > 0.0f ? 127.0f / amax : 0.0f; }
+__device__ __forceinline__ uint32_t q8b4(float a, float b, float c, float d, float inv) {
+    auto one = [inv](float v) {
+        const float r = fminf(fmaxf(__builtin_rintf(v * inv), -127.0f), 127.0f);
+        return (uint32_t)((int)r & 255);
+    };
+    return one(a) | (one(b) << 8) | (one(c) << 16) | (one(d) << 24);
+}
+
+// Quantise and store one lane's share of a 32-row block of h for sorted row
+// p: h[r][i] is row ffb + 16r + 4q + i (the MFMA result layout of two row
+// tiles); lanes q = 0..3 of a column hold the block.  E8M0 + e4m3 for an
+// MXFP4 down, int8 + fp32 scale when q8 is set.
+__device__ __forceinline__ void store_h_block(const GemmArgs &A, bool q8, int p, bool valid, int ffb,
+                                              int q, int lane, const float (&h)[2][4]) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 2; r++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) amax = fmaxf(amax, fabsf(h[r][i]));
+    amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+    const int b = ffb / 32, nb = A.ldo / 32;
+    if (q8) {
+        const float inv = q8b_inv(amax);
+        if (valid) {
+#pragma unroll
+            for (int r = 0; r < 2; r++)
+                *reinterpret_cast<uint32_t *>(A.hq + (size_t)p * A.ldo + ffb + r * 16 + 4 * q) =
+                    q8b4(h[r][0], h[r][1], h[r][2], h[r][3], inv);
+            if (lane < 16) A.hsf[(size_t)p * nb + b] = amax / 127.0f;
+        }
+        return;
+    }
+    const int e2 = quant_exp(amax);
+    const float mul = inv_scale(e2);
+    if (valid) {
+#pragma unroll
+        for (int r = 0; r < 2; r++)
+            *reinterpret_cast<uint32_t *>(A.hq + (size_t)p * A.ldo + ffb + r * 16 + 4 * q) =
+                e4m3x4(h[r][0] * mul, h[r][1] * mul, h[r][2] * mul, h[r][3] * mul);
+        if (lane < 16) {
+            A.hs[(size_t)p * nb + b] = (uint8_t)(127 + e2);
+            A.hs2[(size_t)p * nb + (b & 3) * (nb / 4) + (b >> 2)] = (uint8_t)(127 + e2);
+        }
+    }
+}
 
 // op_sel byte of both scale dwords (A and B hold 4 K-steps each), fixed once
 // the K loop is unrolled.  `sel` must be a compile-time constant or
@@ -748,7 +804,7 @@ __device__ __forceinline__ void wait_vm(int n) {
 
 template <int NJ>
 __device__ __forceinline__ void body(const GemmArgs &A, Lds &L, const uint8_t *Wg, const uint8_t *Wu,
-                                     int mt0, int p0, int p1) {
+                                     int mt0, int p0, int p1, bool hq8) {
     constexpr int KD = 2048, NKT = KD / 128;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -869,30 +925,11 @@ __device__ __forceinline__ void body(const GemmArgs &A, Lds &L, const uint8_t *W
     for (int j = 0; j < NJ; j++) {
         const int p = p0 + 16 * (wt + 2 * j) + n;
         float h[2][4];
-        float amax = 0.0f;
 #pragma unroll
         for (int r = 0; r < 2; r++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                h[r][i] = silu(acc[r][j][i]) * acc[2 + r][j][i];
-                amax = fmaxf(amax, fabsf(h[r][i]));
-            }
-        amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
-        amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
-        const int e2 = quant_exp(amax);
-        const float mul = inv_scale(e2);
-        const int ffb = (mt0 + 2 * wa) * 16;
-        if (p < p1) {
-#pragma unroll
-            for (int r = 0; r < 2; r++)
-                *reinterpret_cast<uint32_t *>(A.hq + (size_t)p * A.ldo + ffb + r * 16 + 4 * q) =
-                    e4m3x4(h[r][0] * mul, h[r][1] * mul, h[r][2] * mul, h[r][3] * mul);
-            if (lane < 16) {
-                const int b = ffb / 32, nb = A.ldo / 32;
-                A.hs[(size_t)p * nb + b] = (uint8_t)(127 + e2);
-                A.hs2[(size_t)p * nb + (b & 3) * (nb / 4) + (b >> 2)] = (uint8_t)(127 + e2);
-            }
-        }
+            for (int i = 0; i < 4; i++) h[r][i] = silu(acc[r][j][i]) * acc[2 + r][j][i];
+        store_h_block(A, hq8, p, p < p1, (mt0 + 2 * wa) * 16, q, lane, h);
     }
 }
 }  // namespace gdma
@@ -912,14 +949,15 @@ __global__ __launch_bounds__(256, 2) void k_gateup_dma(GemmArgs A) {
     const uint8_t *Wu = e < A.E ? A.wb + (size_t)e * A.wstride : A.sb;
     const int ntt = (p1 - p0 + 15) >> 4;
     const int wt = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) >> 1;   // uniform: the switch below is a scalar branch
+    const bool hq8 = A.hq8 && e < A.E;   // the shared expert's down stays MXFP4
     const int nj = ntt > wt ? (ntt - wt + 1) >> 1 : 0;
     switch (nj) {
-        case 0: gdma::body<0>(A, L, Wg, Wu, mt0, p0, p1); break;
-        case 1: gdma::body<1>(A, L, Wg, Wu, mt0, p0, p1); break;
-        case 2: gdma::body<2>(A, L, Wg, Wu, mt0, p0, p1); break;
-        case 3: gdma::body<3>(A, L, Wg, Wu, mt0, p0, p1); break;
-        case 4: gdma::body<4>(A, L, Wg, Wu, mt0, p0, p1); break;
-        default: gdma::body<5>(A, L, Wg, Wu, mt0, p0, p1); break;
+        case 0: gdma::body<0>(A, L, Wg, Wu, mt0, p0, p1, hq8); break;
+        case 1: gdma::body<1>(A, L, Wg, Wu, mt0, p0, p1, hq8); break;
+        case 2: gdma::body<2>(A, L, Wg, Wu, mt0, p0, p1, hq8); break;
+        case 3: gdma::body<3>(A, L, Wg, Wu, mt0, p0, p1, hq8); break;
+        case 4: gdma::body<4>(A, L, Wg, Wu, mt0, p0, p1, hq8); break;
+        default: gdma::body<5>(A, L, Wg, Wu, mt0, p0, p1, hq8); break;
     }
     Q36_TRACE_AT(47);
     Q36_TRACE_WG(1);
@@ -1101,7 +1139,7 @@ constexpr int kSkW = 8;        // waves per workgroup
 
 template <int NJ>
 __device__ __forceinline__ void skinny_gateup(const GemmArgs &A, const uint8_t *Wg, const uint8_t *Wu,
-                                              int mt0, int p0, int p1, float (*red)[4][64][4]) {
+                                              int mt0, int p0, int p1, float (*red)[4][64][4], bool hq8) {
     constexpr int KD = 2048, NKT = KD / 128;
     // the wave index is made wave-uniform for the compiler: the MFMA op_sel
     // below depends on it and must be chosen by scalar branches
@@ -1165,7 +1203,6 @@ __device__ __forceinline__ void skinny_gateup(const GemmArgs &A, const uint8_t *
         // wave 0 finishes column tile j: sums over the 8 K-slices in wave order
         const int p = p0 + j * 16 + (lane & 15);
         float h[2][4];
-        float amax = 0.0f;
 #pragma unroll
         for (int r = 0; r < 2; r++) {
             v4f gs = *reinterpret_cast<const v4f *>(&red[0][r][lane][0]);
@@ -1176,27 +1213,9 @@ __device__ __forceinline__ void skinny_gateup(const GemmArgs &A, const uint8_t *
                 us += *reinterpret_cast<const v4f *>(&red[w][2 + r][lane][0]);
             }
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                h[r][i] = silu(gs[i]) * us[i];
-                amax = fmaxf(amax, fabsf(h[r][i]));
-            }
+            for (int i = 0; i < 4; i++) h[r][i] = silu(gs[i]) * us[i];
         }
-        amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
-        amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
-        const int e2 = quant_exp(amax);
-        const float mul = inv_scale(e2);
-        if (p < p1) {
-            const int ffb = mt0 * 16;
-#pragma unroll
-            for (int r = 0; r < 2; r++)
-                *reinterpret_cast<uint32_t *>(A.hq + (size_t)p * A.ldo + ffb + r * 16 + 4 * q) =
-                    e4m3x4(h[r][0] * mul, h[r][1] * mul, h[r][2] * mul, h[r][3] * mul);
-            if (lane < 16) {
-                const int b = ffb / 32, nb = A.ldo / 32;
-                A.hs[(size_t)p * nb + b] = (uint8_t)(127 + e2);
-                A.hs2[(size_t)p * nb + (b & 3) * (nb / 4) + (b >> 2)] = (uint8_t)(127 + e2);
-            }
-        }
+        store_h_block(A, hq8, p, p < p1, mt0 * 16, q, lane, h);
     }
 }
 
@@ -1212,8 +1231,9 @@ __global__ __launch_bounds__(64 * kSkW) void k_skinny_gateup(GemmArgs A) {
     const int nj = (p1 - p0 + 15) >> 4;
     const uint8_t *Wg = e < A.E ? A.wa + (size_t)e * A.wstride : A.sa;
     const uint8_t *Wu = e < A.E ? A.wb + (size_t)e * A.wstride : A.sb;
-    if (nj <= 1) skinny_gateup<1>(A, Wg, Wu, rb * 2, p0, p1, red);
-    else skinny_gateup<2>(A, Wg, Wu, rb * 2, p0, p1, red);
+    const bool hq8 = A.hq8 && e < A.E;   // the shared expert's down stays MXFP4
+    if (nj <= 1) skinny_gateup<1>(A, Wg, Wu, rb * 2, p0, p1, red, hq8);
+    else skinny_gateup<2>(A, Wg, Wu, rb * 2, p0, p1, red, hq8);
 }
 
 // ---------------------------------------------------------------------------
@@ -1236,18 +1256,147 @@ constexpr int kDlRows = 128;             // B rows staged per chunk
 // read fall in 16 distinct bank groups
 __device__ __forceinline__ int dl_boff(int r, int c) { return r * 512 + ((c & 16) | ((c ^ r) & 15)) * 16; }
 
-__global__ __launch_bounds__(64 * kDlW) void k_down_lds(GemmArgs A) {
+// f16 bit patterns (low / high half of a dword) to float
+__device__ __forceinline__ float f16lo(uint32_t d) { return (float)__builtin_bit_cast(_Float16, (uint16_t)d); }
+__device__ __forceinline__ float f16hi(uint32_t d) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(d >> 16)); }
+
+// Stage h rows c0 .. c0+nr (sorted order, 512 B each) into sb with
+// direct-to-LDS loads, all in flight at once: wave w loads row pairs w + 4u
+// (1 KiB each, lane-contiguous in LDS, chunk order of dl_boff).
+__device__ __forceinline__ void stage_h_rows(const uint8_t *bq, int c0, int nr, uint8_t *sb) {
+    constexpr int KD = 512;
+    const int lane = threadIdx.x & 63;
+    const int npair = __builtin_amdgcn_readfirstlane((nr + 1) >> 1);
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+#pragma unroll
+    for (int u = 0; u < kDlRows / 2 / kDlW; u++) {
+        const int pr = wv + kDlW * u;
+        if (pr < npair) {
+            const int r = 2 * pr + (lane >> 5), ph = lane & 31;
+            const int c = (ph & 16) | ((ph ^ r) & 15);       // logical chunk in this slot
+            dma16(bq + (size_t)(c0 + min(r, nr - 1)) * KD + c * 16, &sb[pr * 1024]);
+        }
+    }
+}
+
+// Row stride of the staged fp32 h scales: 20 floats, so the 16 rows of a
+// fragment read (16 B each) start in 16 distinct bank groups.
+constexpr int kDlSfStride = 20;
+
+// Down projection of one routed tile whose expert is in the q8_0-split
+// layout (k_gemm_expert_i8, q36_engine.cu:2526-2618): int8 h rows with fp32
+// scales against int8 weights with f16 scales.  Each 32-block is one
+// v_mfma_i32_16x16x32_i8 whose exact integer result is scaled by the
+// weight row's f16 scale times the h row's fp32 scale and accumulated in
+// fp32.  The wave's 4 row tiles run as two passes of 2 (codes and scales of
+// 2 row tiles are 128 VGPRs); B is staged once per chunk, as in the MXFP4
+// body.
+__device__ __forceinline__ void down_q8_tile(const GemmArgs &A, int e, int p0, int p1, int rb, uint8_t *sb,
+                                             float (*ssf)[kDlSfStride], float *ws) {
+    constexpr int KD = 512, NKP = KD / 64, NKB = KD / 32;
+    const int tid = threadIdx.x, lane = tid & 63, q = lane >> 4, n = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint8_t *W = A.wa + (size_t)e * A.wstride;
+    const uint8_t *Wsc = W + (size_t)2048 * KD;   // f16 scales after the codes
+    const int mt0 = (rb * kDlW + wave) * kDlRT;
+    for (int c0 = p0; c0 < p1; c0 += kDlRows) {
+        const int nr = min(kDlRows, p1 - c0);
+        if (c0 != p0) __syncthreads();   // previous chunk fully read
+        stage_h_rows(A.bq, c0, nr, sb);
+        for (int c = tid; c < nr; c += 64 * kDlW) {
+            const float4 *src = reinterpret_cast<const float4 *>(A.bsf + (size_t)(c0 + c) * NKB);
+#pragma unroll
+            for (int u = 0; u < 4; u++) *reinterpret_cast<float4 *>(&ssf[c][4 * u]) = src[u];
+            ws[c] = A.row_w[c0 + c];
+        }
+        __syncthreads();
+        const int ntt = (nr + 15) >> 4;
+#pragma unroll 1
+        for (int ps = 0; ps < kDlRT / 2; ps++) {
+            u32x4 ac[2][NKP], as[2][NKP];
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                const int mt = mt0 + 2 * ps + t;
+#pragma unroll
+                for (int kp = 0; kp < NKP; kp++) {
+                    ac[t][kp] = *reinterpret_cast<const u32x4 *>(W + ((size_t)mt * NKP + kp) * 1024 + lane * 16);
+                    as[t][kp] = *reinterpret_cast<const u32x4 *>(Wsc + (((size_t)mt * 4 + q) * NKB + 2 * kp) * 8);
+                }
+            }
+            for (int j = 0; j < ntt; j++) {
+                // padding columns read row 0 of the chunk; never stored
+                const int r = j * 16 + n < nr ? j * 16 + n : 0;
+                float dh[NKB];
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const float4 v = *reinterpret_cast<const float4 *>(&ssf[r][4 * u]);
+                    dh[4 * u] = v.x; dh[4 * u + 1] = v.y; dh[4 * u + 2] = v.z; dh[4 * u + 3] = v.w;
+                }
+                v4f acc[2] = {v4f{0.f, 0.f, 0.f, 0.f}, v4f{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+                for (int kb = 0; kb < NKB; kb++) {
+                    // lane (column n, group q): h K 32kb + 8q..+7 = half q&1 of chunk 2kb + q/2
+                    const uint2 bv = *reinterpret_cast<const uint2 *>(&sb[dl_boff(r, 2 * kb + (q >> 1)) + (q & 1) * 8]);
+                    const long b = (long)(((uint64_t)bv.y << 32) | bv.x);
+#pragma unroll
+                    for (int t = 0; t < 2; t++) {
+                        const u32x4 f = ac[t][kb >> 1];
+                        const long a = (kb & 1) ? (long)(((uint64_t)f[3] << 32) | f[2])
+                                                : (long)(((uint64_t)f[1] << 32) | f[0]);
+                        const v4i ci = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, v4i{0, 0, 0, 0}, 0, 0, 0);
+                        // f16 scales of rows 4q..4q+3 at block kb
+                        const u32x4 sv = as[t][kb >> 1];
+                        const uint32_t s01 = (kb & 1) ? sv[2] : sv[0], s23 = (kb & 1) ? sv[3] : sv[1];
+                        acc[t][0] += (float)ci[0] * (f16lo(s01) * dh[kb]);
+                        acc[t][1] += (float)ci[1] * (f16hi(s01) * dh[kb]);
+                        acc[t][2] += (float)ci[2] * (f16lo(s23) * dh[kb]);
+                        acc[t][3] += (float)ci[3] * (f16hi(s23) * dh[kb]);
+                    }
+                    // two blocks (4 MFMAs) per scheduling group, their scaling
+                    // done in the group: otherwise every block's integer
+                    // result stays live until the end of the column tile
+                    if (kb & 1) {
+                        asm volatile("" : "+v"(acc[0]), "+v"(acc[1]));
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                }
+                if (j * 16 + n < nr) {
+                    const int p = c0 + j * 16 + n;
+                    const float w = ws[j * 16 + n];
+#pragma unroll
+                    for (int t = 0; t < 2; t++) {
+                        const v4f c = acc[t];
+                        *reinterpret_cast<float4 *>(A.dnw + (size_t)p * A.ldo + (mt0 + 2 * ps + t) * 16 + 4 * q) =
+                            make_float4(c[0] * w, c[1] * w, c[2] * w, c[3] * w);
+                    }
+                }
+            }
+        }
+    }
+}
+
+// Q8: routed tiles of a q8_0-split down take down_q8_tile; the shared
+// expert's tiles (MXFP4) and every tile of an MXFP4 layer the body below.
+template <bool Q8>
+__global__ __launch_bounds__(64 * kDlW, Q8 ? 2 : 1) void k_down_lds(GemmArgs A) {
     constexpr int KD = 512, NKT = KD / 128, NRB = 2048 / (16 * kDlRT * kDlW);
     __shared__ __align__(16) uint8_t sb[kDlRows * 512];
     __shared__ uint32_t ss[kDlRows][4];       // B scale dwords: [row][lane group]
     __shared__ float ws[kDlRows];             // routing weight of each row
+    __shared__ __align__(16) float ssf[Q8 ? kDlRows : 1][kDlSfStride];   // int8 h scales
     const int xcd = blockIdx.x & 7, jx = blockIdx.x >> 3;
     const int ti = 8 * (jx / NRB) + xcd, rb = jx % NRB;
     if (ti >= *A.ntiles) return;
     Q36_TRACE_WG(0);
     Q36_TRACE_AT(48);
     const int4 tile = A.tiles[ti];
-    const int e = tile.x, p0 = tile.y, p1 = tile.z;
+    const int e = __builtin_amdgcn_readfirstlane(tile.x), p0 = tile.y, p1 = tile.z;
+    if constexpr (Q8) {
+        if (e < A.E) {
+            down_q8_tile(A, e, p0, p1, rb, sb, ssf, ws);
+            return;
+        }
+    }
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), q = lane >> 4, n = lane & 15;
     const uint8_t *W = e < A.E ? A.wa + (size_t)e * A.wstride : A.sa;
     const size_t nib = (size_t)2048 * KD / 2;
@@ -1265,21 +1414,9 @@ __global__ __launch_bounds__(64 * kDlW) void k_down_lds(GemmArgs A) {
     for (int c0 = p0; c0 < p1; c0 += kDlRows) {
         const int nr = min(kDlRows, p1 - c0);
         if (c0 != p0) __syncthreads();   // previous chunk fully read
-        // stage rows c0 .. c0+nr of h (contiguous in sorted order) with
-        // direct-to-LDS loads, all in flight at once: wave w loads row pairs
-        // w + 4u (1 KiB each, lane-contiguous in LDS), then their
-        // lane-group-major scale dwords and routing weights
-        const int npair = __builtin_amdgcn_readfirstlane((nr + 1) >> 1);
-        const int wv = __builtin_amdgcn_readfirstlane(wave);
-#pragma unroll
-        for (int u = 0; u < kDlRows / 2 / kDlW; u++) {
-            const int pr = wv + kDlW * u;
-            if (pr < npair) {
-                const int r = 2 * pr + (lane >> 5), ph = lane & 31;
-                const int c = (ph & 16) | ((ph ^ r) & 15);       // logical chunk in this slot
-                dma16(A.bq + (size_t)(c0 + min(r, nr - 1)) * KD + c * 16, &sb[pr * 1024]);
-            }
-        }
+        // stage rows c0 .. c0+nr of h (contiguous in sorted order), then
+        // their lane-group-major scale dwords and routing weights
+        stage_h_rows(A.bq, c0, nr, sb);
         for (int c = tid; c < nr; c += 64 * kDlW) {
             *reinterpret_cast<u32x4 *>(&ss[c][0]) = *reinterpret_cast<const u32x4 *>(A.bs2 + (size_t)(c0 + c) * 16);
             ws[c] = A.row_w[c0 + c];
@@ -1345,6 +1482,9 @@ struct DirectArgs {
     // between calls), error flag, and the number of gate/up workgroups
     uint32_t *arrive; uint32_t *depart; uint32_t *err; int n_gateup_wg;
     const uint8_t *xs_in;                       // scales of pre-quantised x (x_fmt kFmtE4M3)
+    size_t dn_wstride;                          // bytes per routed down matrix
+    int dn_q8;                                  // routed down is q8_0-split
+    float *hsf;                                 // int8 h scales (tap, q8_0-split down)
 };
 
 constexpr int kDD = 2048;   // d_model of the instantiated kernels
@@ -1492,52 +1632,104 @@ __global__ __launch_bounds__(256) void k_direct_gateup(DirectArgs A) {
 // Token t x 16 output rows; wave s handles slot s (wave k: shared expert):
 // quantises its SwiGLU row, multiplies by the 16x512 down tile, scales by
 // the routing weight; wave 0 adds the slots in order (k_moe_combine order,
-// q36_engine.cu:784-791) and writes the output rows.
+// q36_engine.cu:784-791) and writes the output rows.  Q8: the routed slots'
+// down matrices are q8_0-split -- h is quantised per 32 to int8 with an fp32
+// scale (k_quant_q8b) and each 32-block is one int8 MFMA scaled by both
+// scales (k_gemm_expert_i8); the shared expert's wave stays MXFP4.
+template <bool Q8>
 __global__ __launch_bounds__(576) void k_direct_down(DirectArgs A) {
     __shared__ __align__(16) uint8_t sh[kMaxTopK + 1][kDF + 32];
     __shared__ uint8_t shs[kMaxTopK + 1][kDF / 32];
+    __shared__ float shf[Q8 ? kMaxTopK + 1 : 1][kDF / 32];
     __shared__ float red[kMaxTopK + 1][16];
     const int rt = blockIdx.x, t = blockIdx.y;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int nslot = blockDim.x >> 6;
     const int nr = A.T * A.k;
     const bool routed = wave < A.k;
+    const bool wq8 = Q8 && routed;   // wave-uniform: selects the MFMA kind
     const int i = routed ? t * A.k + wave : nr + t;
     const int e = routed ? A.idx[i] : A.E;
     const float wgt = routed ? A.wt[i] : 1.0f / (1.0f + expf(-A.shg[t]));
-    const uint8_t *W = (e < A.E) ? A.down + (size_t)e * A.wstride : A.sh_down;
-    const size_t nib = (size_t)kDD * kDF / 2;
-    uint4 a[4];
-#pragma unroll
-    for (int j = 0; j < 4; j++)
-        a[j] = *reinterpret_cast<const uint4 *>(W + ((size_t)rt * 4 + j) * 1024 + (size_t)lane * 16);
-    const int sa = *reinterpret_cast<const int *>(W + nib + ((size_t)rt * 64 + lane) * 4);
-
-    float hv[8];
-    load8(A.hf, Q36MOE_FMT_F32, (size_t)i * kDF + lane * 8, hv);
-    quant8_lane(hv, lane, &sh[wave][lane * 8], &shs[wave][lane >> 2]);
-    if (lane < 8) reinterpret_cast<uint32_t *>(&sh[wave][kDF])[lane] = 0u;
-    if (rt == 0) {   // quantised h (tap)
-        *reinterpret_cast<uint2 *>(A.hq + (size_t)i * kDF + lane * 8) =
-            *reinterpret_cast<const uint2 *>(&sh[wave][lane * 8]);
-        if ((lane & 3) == 0) A.hs[(size_t)i * (kDF / 32) + (lane >> 2)] = shs[wave][lane >> 2];
-    }
-    __syncthreads();
     const int q = lane >> 4;
     const bool col0 = (lane & 15) == 0;
+    constexpr int NKP = kDF / 64, NKB = kDF / 32;
+    float hv[8];
+    load8(A.hf, Q36MOE_FMT_F32, (size_t)i * kDF + lane * 8, hv);
+    // phase 1: this wave's down tile into registers, its h row quantised into LDS
+    u32x4 ac[NKP], as[NKP];   // q8_0-split: codes and f16 scales
+    uint4 a[4];               // MXFP4: E2M1 fragments and the scale dword
+    int sa = 0;
+    if (wq8) {
+        const uint8_t *W = A.down + (size_t)e * A.dn_wstride;
+        const uint8_t *Wsc = W + (size_t)kDD * kDF;
+#pragma unroll
+        for (int kp = 0; kp < NKP; kp++) {
+            ac[kp] = *reinterpret_cast<const u32x4 *>(W + ((size_t)rt * NKP + kp) * 1024 + lane * 16);
+            as[kp] = *reinterpret_cast<const u32x4 *>(Wsc + (((size_t)rt * 4 + q) * NKB + 2 * kp) * 8);
+        }
+        // lanes 4j..4j+3 hold block j
+        float amax = 0.0f;
+#pragma unroll
+        for (int u = 0; u < 8; u++) amax = fmaxf(amax, fabsf(hv[u]));
+        amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+        amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+        const float inv = q8b_inv(amax);
+        const uint2 hc = make_uint2(q8b4(hv[0], hv[1], hv[2], hv[3], inv), q8b4(hv[4], hv[5], hv[6], hv[7], inv));
+        *reinterpret_cast<uint2 *>(&sh[wave][lane * 8]) = hc;
+        if ((lane & 3) == 0) shf[wave][lane >> 2] = amax / 127.0f;
+        if (rt == 0) {   // quantised h (tap)
+            *reinterpret_cast<uint2 *>(A.hq + (size_t)i * kDF + lane * 8) = hc;
+            if ((lane & 3) == 0) A.hsf[(size_t)i * (kDF / 32) + (lane >> 2)] = amax / 127.0f;
+        }
+    } else {
+        const uint8_t *W = (e < A.E) ? A.down + (size_t)e * A.dn_wstride : A.sh_down;
+        const size_t nib = (size_t)kDD * kDF / 2;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            a[j] = *reinterpret_cast<const uint4 *>(W + ((size_t)rt * 4 + j) * 1024 + (size_t)lane * 16);
+        sa = *reinterpret_cast<const int *>(W + nib + ((size_t)rt * 64 + lane) * 4);
+        quant8_lane(hv, lane, &sh[wave][lane * 8], &shs[wave][lane >> 2]);
+        if (rt == 0) {   // quantised h (tap)
+            *reinterpret_cast<uint2 *>(A.hq + (size_t)i * kDF + lane * 8) =
+                *reinterpret_cast<const uint2 *>(&sh[wave][lane * 8]);
+            if ((lane & 3) == 0) A.hs[(size_t)i * (kDF / 32) + (lane >> 2)] = shs[wave][lane >> 2];
+        }
+    }
+    if (lane < 8) reinterpret_cast<uint32_t *>(&sh[wave][kDF])[lane] = 0u;
+    __syncthreads();
+    // phase 2: column 0 is the entry's h row; lanes of other columns read zeros
     v4f c = {0.f, 0.f, 0.f, 0.f};
-    static_for<0, 4>([&](auto J) {
-        constexpr int j = decltype(J)::value;
-        const uint8_t *b0p = col0 ? &sh[wave][j * 128 + 16 * q] : &sh[wave][kDF];
-        const uint8_t *b1p = col0 ? &sh[wave][j * 128 + 64 + 16 * q] : &sh[wave][kDF + 16];
-        const uint4 b0 = *reinterpret_cast<const uint4 *>(b0p);
-        const uint4 b1 = *reinterpret_cast<const uint4 *>(b1p);
-        const v8i b = v8i{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w,
-                          (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
-        const int sb = shs[wave][j * 4 + q];
-        const v8i av = v8i{(int)a[j].x, (int)a[j].y, (int)a[j].z, (int)a[j].w, 0, 0, 0, 0};
-        c = mfma_f4xf8<j>(av, b, c, sa, sb);
-    });
+    if (wq8) {
+#pragma unroll
+        for (int kb = 0; kb < NKB; kb++) {
+            const uint2 bv = *reinterpret_cast<const uint2 *>(col0 ? &sh[wave][kb * 32 + 8 * q] : &sh[wave][kDF]);
+            const long b = (long)(((uint64_t)bv.y << 32) | bv.x);
+            const u32x4 f = ac[kb >> 1];
+            const long av = (kb & 1) ? (long)(((uint64_t)f[3] << 32) | f[2]) : (long)(((uint64_t)f[1] << 32) | f[0]);
+            const v4i ci = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, b, v4i{0, 0, 0, 0}, 0, 0, 0);
+            const float dh = shf[wave][kb];
+            const u32x4 sv = as[kb >> 1];
+            const uint32_t s01 = (kb & 1) ? sv[2] : sv[0], s23 = (kb & 1) ? sv[3] : sv[1];
+            c[0] += (float)ci[0] * (f16lo(s01) * dh);
+            c[1] += (float)ci[1] * (f16hi(s01) * dh);
+            c[2] += (float)ci[2] * (f16lo(s23) * dh);
+            c[3] += (float)ci[3] * (f16hi(s23) * dh);
+        }
+    } else {
+        static_for<0, 4>([&](auto J) {
+            constexpr int j = decltype(J)::value;
+            const uint8_t *b0p = col0 ? &sh[wave][j * 128 + 16 * q] : &sh[wave][kDF];
+            const uint8_t *b1p = col0 ? &sh[wave][j * 128 + 64 + 16 * q] : &sh[wave][kDF + 16];
+            const uint4 b0 = *reinterpret_cast<const uint4 *>(b0p);
+            const uint4 b1 = *reinterpret_cast<const uint4 *>(b1p);
+            const v8i b = v8i{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w,
+                              (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+            const int sb = shs[wave][j * 4 + q];
+            const v8i av = v8i{(int)a[j].x, (int)a[j].y, (int)a[j].z, (int)a[j].w, 0, 0, 0, 0};
+            c = mfma_f4xf8<j>(av, b, c, sa, sb);
+        });
+    }
     if (col0) {
 #pragma unroll
         for (int r = 0; r < 4; r++) red[wave][4 * q + r] = c[r] * wgt;
@@ -1785,6 +1977,7 @@ struct q36moe_weights {
     uint8_t *gate, *up, *down;       // [E][packed matrix]
     uint8_t *sh_gate, *sh_up, *sh_down;
     size_t gu_bytes, dn_bytes;       // one packed matrix
+    int dn_q8;                       // routed down in the packed q8_0-split layout
     void *base;                      // single device allocation
 };
 
@@ -1813,6 +2006,7 @@ struct q36moe_ctx {
     float *row_w;
     int4 *tiles; int32_t *ntiles;
     uint8_t *hq, *hs, *hs2;
+    float *hsf;                     // fp32 scales of int8 h rows (q8_0-split down)
     float *dnw;
     float *hf;                      // direct path: fp32 SwiGLU rows
     uint32_t *sync;                 // fused decode: arrive[16], depart[16], err
@@ -1830,20 +2024,23 @@ namespace {
 
 int hip_rc(hipError_t e) { return e == hipSuccess ? Q36MOE_OK : Q36MOE_EHIP; }
 
+// ggml type ids of the expert formats (q36.h:133-141)
+constexpr int kTypeQ8_0 = 8, kTypeQ5_K = 13, kTypeQ6_K = 14, kTypeMXFP4 = 39;
+
 bool dims_ok(int E, int D, int FF) {
     return E >= 1 && E <= kMaxExperts && D > 0 && FF > 0 && D % 512 == 0 && FF % 512 == 0;
 }
 
-int alloc_weights(int E, int D, int FF, int FFsh, q36moe_weights **out) {
+int alloc_weights(int E, int D, int FF, int FFsh, int dn_q8, q36moe_weights **out) {
     if (!out || !dims_ok(E, D, FF) || !(FFsh == 0 || FFsh == FF)) return Q36MOE_EINVAL;
     q36moe_weights *w = new (std::nothrow) q36moe_weights();
     if (!w) return Q36MOE_ENOMEM;
-    w->E = E; w->D = D; w->FF = FF; w->FFsh = FFsh;
+    w->E = E; w->D = D; w->FF = FF; w->FFsh = FFsh; w->dn_q8 = dn_q8;
     const size_t m = (size_t)D * FF;
     w->gu_bytes = m / 2 + m / 32;
-    w->dn_bytes = w->gu_bytes;
-    const size_t routed = align256(w->gu_bytes * E);
-    const size_t total = 3 * routed + (FFsh ? 3 * align256(w->gu_bytes) : 0);
+    w->dn_bytes = dn_q8 ? m + m / 16 : w->gu_bytes;   // int8 codes + f16 per 32
+    const size_t routed = align256(w->gu_bytes * E), routed_dn = align256(w->dn_bytes * E);
+    const size_t total = 2 * routed + routed_dn + (FFsh ? 3 * align256(w->gu_bytes) : 0);
     if (hipMalloc(&w->base, total) != hipSuccess) {
         delete w;
         return Q36MOE_ENOMEM;
@@ -1851,7 +2048,7 @@ int alloc_weights(int E, int D, int FF, int FFsh, q36moe_weights **out) {
     uint8_t *p = static_cast<uint8_t *>(w->base);
     w->gate = p; w->up = p + routed; w->down = p + 2 * routed;
     if (FFsh) {
-        uint8_t *q = p + 3 * routed;
+        uint8_t *q = p + 2 * routed + routed_dn;
         w->sh_gate = q; w->sh_up = q + align256(w->gu_bytes); w->sh_down = q + 2 * align256(w->gu_bytes);
     } else {
         w->sh_gate = w->sh_up = w->sh_down = nullptr;
@@ -1868,41 +2065,66 @@ extern "C" {
 const char *q36moe_version(void) { return "q36moe 0.1 gfx950"; }
 
 int q36moe_weights_alloc(int n_expert, int d_model, int d_ff, int d_ff_sh, q36moe_weights **out) {
-    return alloc_weights(n_expert, d_model, d_ff, d_ff_sh, out);
+    return alloc_weights(n_expert, d_model, d_ff, d_ff_sh, 0, out);
 }
 
 int q36moe_weights_upload(const void *gate, const void *up, const void *down, const void *sh_gate,
                           const void *sh_up, const void *sh_down, int n_expert, int d_model,
                           int d_ff, int d_ff_sh, q36moe_weights **out) {
+    return q36moe_weights_upload_typed(gate, up, down, kTypeMXFP4, sh_gate, sh_up, sh_down, n_expert, d_model,
+                                       d_ff, d_ff_sh, out);
+}
+
+int q36moe_weights_upload_typed(const void *gate, const void *up, const void *down, int down_type,
+                                const void *sh_gate, const void *sh_up, const void *sh_down, int n_expert,
+                                int d_model, int d_ff, int d_ff_sh, q36moe_weights **out) {
     if (!gate || !up || !down || !out) return Q36MOE_EINVAL;
     if (d_ff_sh && (!sh_gate || !sh_up || !sh_down)) return Q36MOE_EINVAL;
+    // down row bytes per ggml type (blocks of 32, or super-blocks of 256)
+    size_t dn_row;
+    if (down_type == kTypeMXFP4) dn_row = (size_t)(d_ff / 32) * 17;
+    else if (down_type == kTypeQ8_0) dn_row = (size_t)(d_ff / 32) * 34;
+    else if ((down_type == kTypeQ5_K || down_type == kTypeQ6_K) && d_ff % 256 == 0)
+        dn_row = (size_t)(d_ff / 256) * (down_type == kTypeQ5_K ? 176 : 210);
+    else return Q36MOE_EINVAL;
+    const int dn_q8 = down_type != kTypeMXFP4;
     q36moe_weights *w = nullptr;
-    int rc = alloc_weights(n_expert, d_model, d_ff, d_ff_sh, &w);
+    int rc = alloc_weights(n_expert, d_model, d_ff, d_ff_sh, dn_q8, &w);
     if (rc) return rc;
     const size_t gu_src = (size_t)d_ff * (d_model / 32) * 17;
-    const size_t dn_src = (size_t)d_model * (d_ff / 32) * 17;
-    uint8_t *host = static_cast<uint8_t *>(malloc(w->gu_bytes));
-    if (!host) {
+    const size_t dn_src = (size_t)d_model * dn_row;
+    const size_t m = (size_t)d_model * d_ff;
+    uint8_t *host = static_cast<uint8_t *>(malloc(w->gu_bytes > w->dn_bytes ? w->gu_bytes : w->dn_bytes));
+    int8_t *codes = dn_q8 ? static_cast<int8_t *>(malloc(m)) : nullptr;
+    uint16_t *scales = dn_q8 ? static_cast<uint16_t *>(malloc(m / 32 * 2)) : nullptr;
+    if (!host || (dn_q8 && (!codes || !scales))) {
+        free(host); free(codes); free(scales);
         q36moe_weights_free(w);
         return Q36MOE_ENOMEM;
     }
-    struct Job { const uint8_t *src; size_t src_stride; uint8_t *dst; int M, K, n; };
+    struct Job { const uint8_t *src; size_t src_stride; uint8_t *dst; size_t dst_stride; int M, K, n, q8; };
     const Job jobs[6] = {
-        {static_cast<const uint8_t *>(gate), gu_src, w->gate, d_ff, d_model, n_expert},
-        {static_cast<const uint8_t *>(up), gu_src, w->up, d_ff, d_model, n_expert},
-        {static_cast<const uint8_t *>(down), dn_src, w->down, d_model, d_ff, n_expert},
-        {static_cast<const uint8_t *>(sh_gate), gu_src, w->sh_gate, d_ff, d_model, d_ff_sh ? 1 : 0},
-        {static_cast<const uint8_t *>(sh_up), gu_src, w->sh_up, d_ff, d_model, d_ff_sh ? 1 : 0},
-        {static_cast<const uint8_t *>(sh_down), dn_src, w->sh_down, d_model, d_ff, d_ff_sh ? 1 : 0},
+        {static_cast<const uint8_t *>(gate), gu_src, w->gate, w->gu_bytes, d_ff, d_model, n_expert, 0},
+        {static_cast<const uint8_t *>(up), gu_src, w->up, w->gu_bytes, d_ff, d_model, n_expert, 0},
+        {static_cast<const uint8_t *>(down), dn_src, w->down, w->dn_bytes, d_model, d_ff, n_expert, dn_q8},
+        {static_cast<const uint8_t *>(sh_gate), gu_src, w->sh_gate, w->gu_bytes, d_ff, d_model, d_ff_sh ? 1 : 0, 0},
+        {static_cast<const uint8_t *>(sh_up), gu_src, w->sh_up, w->gu_bytes, d_ff, d_model, d_ff_sh ? 1 : 0, 0},
+        {static_cast<const uint8_t *>(sh_down), (size_t)d_model * (d_ff / 32) * 17, w->sh_down, w->gu_bytes,
+         d_model, d_ff, d_ff_sh ? 1 : 0, 0},
     };
     for (const Job &j : jobs) {
         for (int e = 0; e < j.n && rc == 0; e++) {
-            rc = q36moe_pack_mxfp4(j.src + j.src_stride * e, j.M, j.K, host);
+            if (j.q8) {
+                rc = q36moe_requant_q8(down_type, j.src + j.src_stride * e, j.M, j.K, codes, scales);
+                if (rc == 0) rc = q36moe_pack_q8(codes, scales, j.M, j.K, host);
+            } else {
+                rc = q36moe_pack_mxfp4(j.src + j.src_stride * e, j.M, j.K, host);
+            }
             if (rc == 0)
-                rc = hip_rc(hipMemcpy(j.dst + w->gu_bytes * e, host, w->gu_bytes, hipMemcpyHostToDevice));
+                rc = hip_rc(hipMemcpy(j.dst + j.dst_stride * e, host, j.dst_stride, hipMemcpyHostToDevice));
         }
     }
-    free(host);
+    free(host); free(codes); free(scales);
     if (rc) {
         q36moe_weights_free(w);
         return rc;
@@ -1914,6 +2136,7 @@ int q36moe_weights_upload(const void *gate, const void *up, const void *down, co
 int q36moe_weights_fill_synthetic(q36moe_weights *w, uint64_t seed, int exp_lo, int exp_hi,
                                   void *stream) {
     if (!w || exp_lo > exp_hi || exp_lo < -127 || exp_hi > 127) return Q36MOE_EINVAL;
+    if (w->dn_q8) return Q36MOE_EINVAL;   // MXFP4 sets only
     hipStream_t s = static_cast<hipStream_t>(stream);
     const size_t m = (size_t)w->D * w->FF, nib = m / 2, scl = m / 32;
     uint8_t *mats[3] = {w->gate, w->up, w->down};
@@ -1947,6 +2170,11 @@ int q36moe_weights_device_ptrs(const q36moe_weights *w, void **gate, void **up, 
     if (gate_bytes) *gate_bytes = w->gu_bytes;
     if (down_bytes) *down_bytes = w->dn_bytes;
     return Q36MOE_OK;
+}
+
+int q36moe_weights_down_type(const q36moe_weights *w) {
+    if (!w) return Q36MOE_EINVAL;
+    return w->dn_q8 ? kTypeQ8_0 : kTypeMXFP4;
 }
 
 void q36moe_weights_free(q36moe_weights *w) {
@@ -1988,6 +2216,7 @@ int q36moe_ctx_create(int max_tokens, int n_expert, int d_model, int d_ff, int t
     const size_t o_rt = take(rows * 4), o_rw = take(rows * 4);
     const size_t o_tiles = take(c->tile_cap * 16), o_nt = take(4);
     const size_t o_hq = take(rows * d_ff), o_hs = take(rows * d_ff / 32), o_hs2 = take(rows * d_ff / 32);
+    const size_t o_hsf = take(rows * d_ff / 32 * 4);
     const size_t o_dnw = take(rows * d_model * 4);
     const size_t direct_rows = (size_t)(max_tokens < kDirectMaxT ? max_tokens : kDirectMaxT) * (top_k + 1);
     const size_t o_hf = take(direct_rows * d_ff * 4);
@@ -2013,6 +2242,7 @@ int q36moe_ctx_create(int max_tokens, int n_expert, int d_model, int d_ff, int t
     c->tiles = reinterpret_cast<int4 *>(b + o_tiles);
     c->ntiles = reinterpret_cast<int32_t *>(b + o_nt);
     c->hq = b + o_hq; c->hs = b + o_hs; c->hs2 = b + o_hs2;
+    c->hsf = reinterpret_cast<float *>(b + o_hsf);
     c->dnw = reinterpret_cast<float *>(b + o_dnw);
     c->hf = reinterpret_cast<float *>(b + o_hf);
     c->sync = reinterpret_cast<uint32_t *>(b + o_sync);
@@ -2051,9 +2281,12 @@ static void bind_weights(Plan &P, const q36moe_weights *w) {
     P.ga.wstride = w->gu_bytes;
     P.da.wa = w->down; P.da.wb = nullptr; P.da.sa = w->sh_down; P.da.sb = nullptr;
     P.da.wstride = w->dn_bytes;
+    P.ga.hq8 = P.da.hq8 = w->dn_q8;
     P.di.gate = w->gate; P.di.up = w->up; P.di.down = w->down;
     P.di.sh_gate = w->sh_gate; P.di.sh_up = w->sh_up; P.di.sh_down = P.has_sh ? w->sh_down : nullptr;
     P.di.wstride = w->gu_bytes;
+    P.di.dn_wstride = w->dn_bytes;
+    P.di.dn_q8 = w->dn_q8;
 }
 
 // Launches the kernels of one stage (direct path: ST_GATEUP is the routing +
@@ -2069,7 +2302,10 @@ static void launch_stage(const q36moe_ctx *c, const Plan &P, int st, hipStream_t
         } else if (st == ST_GATEUP) {
             hipLaunchKernelGGL(k_direct_gateup, dim3(n, FF / 16), dim3(256), 0, s, P.di);
         } else if (st == ST_DOWN) {
-            hipLaunchKernelGGL(k_direct_down, dim3(D / 16, T), dim3(64 * (K + P.has_sh)), 0, s, P.di);
+            if (P.di.dn_q8)
+                hipLaunchKernelGGL(k_direct_down<true>, dim3(D / 16, T), dim3(64 * (K + P.has_sh)), 0, s, P.di);
+            else
+                hipLaunchKernelGGL(k_direct_down<false>, dim3(D / 16, T), dim3(64 * (K + P.has_sh)), 0, s, P.di);
         }
         return;
     }
@@ -2093,7 +2329,12 @@ static void launch_stage(const q36moe_ctx *c, const Plan &P, int st, hipStream_t
                                    P.ga);
             break;
         case ST_DOWN:
-            hipLaunchKernelGGL(k_down_lds, dim3(P.tiles * (D / (16 * kDlRT * kDlW))), dim3(64 * kDlW), 0, s, P.da);
+            if (P.da.hq8)
+                hipLaunchKernelGGL(k_down_lds<true>, dim3(P.tiles * (D / (16 * kDlRT * kDlW))), dim3(64 * kDlW), 0, s,
+                                   P.da);
+            else
+                hipLaunchKernelGGL(k_down_lds<false>, dim3(P.tiles * (D / (16 * kDlRT * kDlW))), dim3(64 * kDlW), 0,
+                                   s, P.da);
             break;
         case ST_COMBINE:
             hipLaunchKernelGGL(k_combine, dim3(T), dim3(256), 0, s, c->dnw, c->pos, T, K, D, P.has_sh,
@@ -2108,6 +2349,8 @@ int q36moe_ctx_replay(q36moe_ctx *c, const q36moe_weights *w, int stage) {
     if (c->last_T <= 0) return Q36MOE_EINVAL;
     if (w->E != c->E || w->D != c->D || w->FF != c->FF) return Q36MOE_EINVAL;
     if (c->plan->has_sh && !w->sh_gate) return Q36MOE_EINVAL;
+    // the plan's h quantisation matches the down format it was made for
+    if ((c->plan->direct ? c->plan->di.dn_q8 : c->plan->da.hq8) != w->dn_q8) return Q36MOE_EINVAL;
     Plan P = *c->plan;
     bind_weights(P, w);
     launch_stage(c, P, stage, c->stream);
@@ -2139,6 +2382,7 @@ static int forward_impl(q36moe_ctx *c, const q36moe_weights *w, const void *x, i
     const bool direct = (pm == 2 || pm == 3) ? (T <= kDirectMaxT) : (pm == 1 || pm == 4) ? false
                                                                                       : (T <= kDirectMaxT);
     if ((pm == 2 || pm == 3) && !direct) return Q36MOE_EINVAL;
+    if (pm == 3 && w->dn_q8) return Q36MOE_EINVAL;   // the one-kernel decode is MXFP4-only
     // sorted path: skinny tiles (<= 32 rows) while the average expert has at
     // most kSkinnyRows rows, else fat tiles of up to kGdTok rows
     const bool skinny = pm == 4 || (pm == 0 && (size_t)n <= (size_t)kSkinnyRows * E);
@@ -2156,7 +2400,7 @@ static int forward_impl(q36moe_ctx *c, const q36moe_weights *w, const void *x, i
                           nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0,
                           c->topk_idx, c->topk_w, c->pos, c->perm, c->xq, c->xs, c->hf,
                           c->hq, c->hs, out, out_fmt, c->sync, c->sync + kDirectMaxT,
-                          c->sync + 2 * kDirectMaxT, ngu, xs_in};
+                          c->sync + 2 * kDirectMaxT, ngu, xs_in, 0, 0, c->hsf};
     } else {
         P.ra = RouteArgs{logits, ld_logits, T, E, K, scale, x, x_fmt, D, nb,
                          c->topk_idx, c->topk_w, c->xq, c->xs, c->xs2, c->blk_cnt, c->rank, xs_in};
@@ -2170,10 +2414,12 @@ static int forward_impl(q36moe_ctx *c, const q36moe_weights *w, const void *x, i
         ga.bq = x_fmt == kFmtE4M3 ? static_cast<const uint8_t *>(x) : c->xq;
         ga.bs2 = c->xs2; ga.row_tok = c->row_tok; ga.row_w = c->row_w;
         ga.hq = c->hq; ga.hs = c->hs; ga.hs2 = c->hs2; ga.ldo = FF;
+        ga.hsf = c->hsf;
         GemmArgs &da = P.da;
         da = ga;
         da.M = D;
         da.bq = c->hq; da.bs2 = c->hs2; da.dnw = c->dnw; da.ldo = D;
+        da.bsf = c->hsf;
     }
     bind_weights(P, w);
     for (int st = 0; st < ST_COUNT; st++) {
@@ -2285,6 +2531,7 @@ int q36moe_ctx_copy_tap(q36moe_ctx *c, int tap, void *dst, size_t bytes, size_t 
         case Q36MOE_TAP_POS: src = c->pos; sz = n * 4; break;
         case Q36MOE_TAP_HQ: src = c->hq; sz = rows * c->FF; break;
         case Q36MOE_TAP_HS: src = c->hs; sz = rows * c->FF / 32; break;
+        case Q36MOE_TAP_HSF: src = c->hsf; sz = rows * c->FF / 32 * 4; break;
         case Q36MOE_TAP_DNW:
             if (c->last_path == 1) return Q36MOE_EINVAL;   // combined in registers
             src = c->dnw; sz = rows * c->D * 4; break;

@@ -281,9 +281,11 @@ int q36moe_weights_from_gguf(const q36moe_gguf *g, int layer, int with_shared, q
     const Tensor *ut = find(g, blk(layer, "ffn_up_exps.weight"));
     const Tensor *dt = find(g, blk(layer, "ffn_down_exps.weight"));
     if (!gt || !ut || !dt) return Q36MOE_ENOENT;
-    // MXFP4 only: the reference's other expert types (Q5_K/Q6_K/Q8_0 down
-    // fallbacks of real files) have no kernel here
-    if (gt->type != T_MXFP4 || ut->type != T_MXFP4 || dt->type != T_MXFP4) return Q36MOE_EINVAL;
+    // gate/up MXFP4; down MXFP4 or one of the reference's requantised
+    // fallback types (Q5_K / Q6_K experts of real files, and Q8_0)
+    if (gt->type != T_MXFP4 || ut->type != T_MXFP4) return Q36MOE_EINVAL;
+    if (dt->type != T_MXFP4 && dt->type != T_Q5_K && dt->type != T_Q6_K && dt->type != T_Q8_0)
+        return Q36MOE_EINVAL;
     // ggml order: gate/up [d_model][d_ff][E], down [d_ff][d_model][E]
     if (gt->n_dims != 3 || ut->n_dims != 3 || dt->n_dims != 3) return Q36MOE_EINVAL;
     const uint64_t D = gt->dims[0], FF = gt->dims[1], E = gt->dims[2];
@@ -306,8 +308,8 @@ int q36moe_weights_from_gguf(const q36moe_gguf *g, int layer, int with_shared, q
         sd = data_of(g, c);
         ff_sh = (int)FF;
     }
-    return q36moe_weights_upload(data_of(g, gt), data_of(g, ut), data_of(g, dt), sg, su, sd, (int)E, (int)D,
-                                 (int)FF, ff_sh, out);
+    return q36moe_weights_upload_typed(data_of(g, gt), data_of(g, ut), data_of(g, dt), (int)dt->type, sg, su,
+                                       sd, (int)E, (int)D, (int)FF, ff_sh, out);
 }
 
 int q36moe_router_from_gguf(const q36moe_gguf *g, int layer, float *dst, size_t dst_floats, int *n_rows,

@@ -20,6 +20,8 @@ FMT_F32 = 0
 FMT_BF16 = 1
 
 TAP_TOPK_IDX, TAP_TOPK_W, TAP_XQ, TAP_XS, TAP_EOFF, TAP_PERM, TAP_POS, TAP_HQ, TAP_HS, TAP_DNW = range(10)
+TAP_HSF = 10
+GGML_Q8_0, GGML_Q5_K, GGML_Q6_K, GGML_MXFP4 = 8, 13, 14, 39
 
 _ERRORS = {-22: "EINVAL", -12: "ENOMEM", -1000: "EHIP"}
 
@@ -44,6 +46,11 @@ def lib():
     L.q36moe_expert_bytes.argtypes = [i, i]
     L.q36moe_expert_bytes.restype = sz
     L.q36moe_weights_upload.argtypes = [vp] * 6 + [i] * 4 + [pp]
+    L.q36moe_weights_upload_typed.argtypes = [vp] * 3 + [i] + [vp] * 3 + [i] * 4 + [pp]
+    L.q36moe_weights_down_type.argtypes = [vp]
+    L.q36moe_requant_q8.argtypes = [i, vp, i, i, vp, vp]
+    L.q36moe_pack_q8.argtypes = [vp, vp, i, i, vp]
+    L.q36moe_unpack_q8.argtypes = [vp, i, i, vp, vp]
     L.q36moe_weights_alloc.argtypes = [i] * 4 + [pp]
     L.q36moe_weights_device_ptrs.argtypes = [vp] + [pp] * 6 + [ctypes.POINTER(sz)] * 2
     L.q36moe_weights_fill_synthetic.argtypes = [vp, ctypes.c_uint64, i, i, vp]
@@ -124,9 +131,12 @@ class MoEWeights:
         self.n_expert, self.d_model, self.d_ff, self.d_ff_sh = n_expert, d_model, d_ff, d_ff_sh
 
     @classmethod
-    def upload(cls, gate, up, down, sh_gate=None, sh_up=None, sh_down=None):
-        """gate/up [E, d_ff, d_model/32, 17], down [E, d_model, d_ff/32, 17]
-        GGUF block_mxfp4 bytes (numpy uint8)."""
+    def upload(cls, gate, up, down, sh_gate=None, sh_up=None, sh_down=None, down_type=GGML_MXFP4):
+        """gate/up [E, d_ff, d_model/32, 17] GGUF block_mxfp4 bytes (numpy
+        uint8); down [E, d_model, row bytes] blocks of ggml type down_type
+        (GGML_MXFP4 [.., d_ff/32, 17], or GGML_Q8_0 / GGML_Q5_K / GGML_Q6_K,
+        requantised to the q8_0-split layout as upload() does for k-quant
+        experts, q36_engine.cu:229-252)."""
         E, d_ff, nbk, _ = gate.shape
         d_model = nbk * 32
         keep = []
@@ -145,9 +155,16 @@ class MoEWeights:
         else:
             ptrs += [None, None, None]
         h = ctypes.c_void_p()
-        check(lib().q36moe_weights_upload(*ptrs, E, d_model, d_ff, d_ff_sh, ctypes.byref(h)),
-              "q36moe_weights_upload")
+        check(lib().q36moe_weights_upload_typed(*ptrs[:3], down_type, *ptrs[3:], E, d_model, d_ff, d_ff_sh,
+                                                ctypes.byref(h)),
+              "q36moe_weights_upload_typed")
         return cls(h, E, d_model, d_ff, d_ff_sh)
+
+    @property
+    def down_type(self):
+        """ggml type of the routed down on the device: GGML_MXFP4 or GGML_Q8_0
+        (the q8_0-split layout, whatever type it was uploaded from)."""
+        return lib().q36moe_weights_down_type(self._h)
 
     @classmethod
     def from_gguf(cls, gguf, layer, with_shared=False):
@@ -207,6 +224,36 @@ def pack_mxfp4(blocks):
     out = np.empty(M * K // 2 + M * K // 32, dtype=np.uint8)
     check(lib().q36moe_pack_mxfp4(p, M, K, ctypes.c_void_p(out.ctypes.data)), "q36moe_pack_mxfp4")
     return out
+
+
+def requant_q8(ggml_type, blocks, M, K):
+    """Host: one [M][K] matrix of GGUF Q8_0 / Q5_K / Q6_K blocks -> (int8 codes
+    [M, K], f16 scale bits [M, K/32]) in the q8_0-split layout."""
+    src, p = _host_u8(blocks)
+    codes = np.empty((M, K), dtype=np.int8)
+    scales = np.empty((M, K // 32), dtype=np.uint16)
+    check(lib().q36moe_requant_q8(ggml_type, p, M, K, ctypes.c_void_p(codes.ctypes.data),
+                                  ctypes.c_void_p(scales.ctypes.data)), "q36moe_requant_q8")
+    return codes, scales
+
+
+def pack_q8(codes, scales):
+    M, K = codes.shape
+    codes = np.ascontiguousarray(codes, dtype=np.int8)
+    scales = np.ascontiguousarray(scales, dtype=np.uint16)
+    out = np.empty(M * K + M * K // 16, dtype=np.uint8)
+    check(lib().q36moe_pack_q8(ctypes.c_void_p(codes.ctypes.data), ctypes.c_void_p(scales.ctypes.data), M, K,
+                               ctypes.c_void_p(out.ctypes.data)), "q36moe_pack_q8")
+    return out
+
+
+def unpack_q8(packed, M, K):
+    src, p = _host_u8(packed)
+    codes = np.empty((M, K), dtype=np.int8)
+    scales = np.empty((M, K // 32), dtype=np.uint16)
+    check(lib().q36moe_unpack_q8(p, M, K, ctypes.c_void_p(codes.ctypes.data), ctypes.c_void_p(scales.ctypes.data)),
+          "q36moe_unpack_q8")
+    return codes, scales
 
 
 def unpack_mxfp4(packed, M, K):
@@ -293,6 +340,7 @@ class MoELayer:
             TAP_EOFF: ((E + 1,), torch.int32), TAP_PERM: ((T * k,), torch.int32),
             TAP_POS: ((T * k,), torch.int32), TAP_HQ: ((rows, FF), torch.uint8),
             TAP_HS: ((rows, FF // 32), torch.uint8), TAP_DNW: ((rows, D), torch.float32),
+            TAP_HSF: ((rows, FF // 32), torch.float32),
         }
         shape, dt = shapes[which]
         dst = torch.empty(shape, dtype=dt, device="cuda")

@@ -41,6 +41,32 @@ def expert_weights(seed, n_expert=N_EXPERT, d_model=D_MODEL, d_ff=D_FF, shared=F
     return w
 
 
+GGML_Q8_0, GGML_Q5_K, GGML_Q6_K = 8, 13, 14
+KQUANT_BLOCK = {GGML_Q8_0: (32, 34), GGML_Q5_K: (256, 176), GGML_Q6_K: (256, 210)}
+
+
+def _f16_bytes(rng, n, lo, hi):
+    return np.frombuffer(rng.uniform(lo, hi, size=n).astype(np.float16).tobytes(), dtype=np.uint8).reshape(n, 2)
+
+
+def kquant_blocks(rng, rows, k, ggml_type):
+    """[rows, row bytes] uint8 GGUF blocks of a Q8_0 / Q5_K / Q6_K matrix with
+    random codes and finite f16 super-block scales (the formats of the
+    reference's fallback expert tensors, q36.h:109-131), sized so values
+    span roughly the MXFP4 experts' range."""
+    elems, size = KQUANT_BLOCK[ggml_type]
+    nb = rows * (k // elems)
+    blk = np.frombuffer(rng.bytes(nb * size), dtype=np.uint8).reshape(nb, size).copy()
+    if ggml_type == GGML_Q8_0:
+        blk[:, 0:2] = _f16_bytes(rng, nb, 0.005, 0.05)
+    elif ggml_type == GGML_Q5_K:
+        blk[:, 0:2] = _f16_bytes(rng, nb, 5e-4, 3e-3)      # d
+        blk[:, 2:4] = _f16_bytes(rng, nb, 5e-4, 3e-3)      # dmin
+    else:
+        blk[:, 208:210] = _f16_bytes(rng, nb, 5e-4, 3e-3)  # d
+    return blk.reshape(rows, -1)
+
+
 def hidden(rng, T, d_model=D_MODEL):
     return rng.standard_normal((T, d_model), dtype=np.float32)
 

@@ -5,7 +5,7 @@ import struct
 import numpy as np
 
 U8, I8, U16, I16, U32, I32, F32, BOOL, STR, ARR, U64, I64, F64 = range(13)
-T_F32, T_F16, T_Q8_0, T_BF16, T_MXFP4 = 0, 1, 8, 30, 39
+T_F32, T_F16, T_Q8_0, T_Q5_K, T_Q6_K, T_BF16, T_MXFP4 = 0, 1, 8, 13, 14, 30, 39
 _SCALAR = {U8: "<B", I8: "<b", U16: "<H", I16: "<h", U32: "<I", I32: "<i", F32: "<f", BOOL: "<?",
            U64: "<Q", I64: "<q", F64: "<d"}
 

@@ -18,11 +18,17 @@ REF_GGUF = os.path.join(ROOT, "oracle", "_ref", "libref_gguf.so")
 D, FF = 2048, 512
 
 
-def _layer_file(path, E=16, layer=0, router_bf16=False, shared="mxfp4", seed=5, alignment=64):
+def _layer_file(path, E=16, layer=0, router_bf16=False, shared="mxfp4", seed=5, alignment=64,
+                down_type=gf.T_MXFP4, gate_type=gf.T_MXFP4):
     """One MoE block of a q36-style file with E experts, plus unrelated
-    metadata and tensors; returns the arrays written."""
+    metadata and tensors; returns the arrays written.  down_type 13 / 14 / 8
+    writes a Q5_K / Q6_K / Q8_0 down (the k-quant experts of real files);
+    gate_type other than MXFP4 only relabels the gate bytes (for rejection
+    tests)."""
     rng = np.random.default_rng(seed)
     w = synth.expert_weights(seed, n_expert=E, shared=True)
+    if down_type != gf.T_MXFP4:
+        w["down"] = synth.kquant_blocks(rng, E * D, FF, down_type).reshape(E, D, -1)
     router = (rng.standard_normal((E, D)) * 0.02).astype(np.float32)
     shg_row = (rng.standard_normal(D) * 0.02).astype(np.float32)
     norm = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
@@ -39,9 +45,9 @@ def _layer_file(path, E=16, layer=0, router_bf16=False, shared="mxfp4", seed=5, 
                (p + "ffn_gate_inp.weight", [D, E], gf.T_BF16 if router_bf16 else gf.T_F32,
                 gf.bf16_bytes(router) if router_bf16 else router.tobytes()),
                (p + "ffn_gate_inp_shexp.weight", [D], gf.T_BF16, gf.bf16_bytes(shg_row)),
-               (p + "ffn_gate_exps.weight", [D, FF, E], gf.T_MXFP4, w["gate"].tobytes()),
+               (p + "ffn_gate_exps.weight", [D, FF, E], gate_type, w["gate"].tobytes()),
                (p + "ffn_up_exps.weight", [D, FF, E], gf.T_MXFP4, w["up"].tobytes()),
-               (p + "ffn_down_exps.weight", [FF, D, E], gf.T_MXFP4, w["down"].tobytes()),
+               (p + "ffn_down_exps.weight", [FF, D, E], down_type, w["down"].tobytes()),
                ("token_embd.weight", [64, 8], gf.T_Q8_0, bytes(8 * 2 * 34))]
     if shared == "mxfp4":
         tensors += [(p + "ffn_gate_shexp.weight", [D, FF], gf.T_MXFP4, w["sh_gate"].tobytes()),
@@ -197,6 +203,41 @@ def test_weights_from_gguf_rejects_before_upload(tmp_path):
         assert L.q36moe_weights_from_gguf(g._h, 0, 1, ctypes.byref(h)) == -22   # Q8_0 shared expert
         assert L.q36moe_weights_from_gguf(g._h, 3, 0, ctypes.byref(h)) == -2    # no block 3
         assert L.q36moe_weights_from_gguf(g._h, -1, 0, ctypes.byref(h)) == -22
+    # routed gate/up must be MXFP4 (the bytes are relabelled Q8_0 here: a
+    # type error, caught before the size of the data matters)
+    _layer_file(path, E=2, gate_type=gf.T_Q8_0)
+    with moe.GGUF(path) as g:
+        assert L.q36moe_weights_from_gguf(g._h, 0, 0, ctypes.byref(h)) == -22
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("down_type", [gf.T_Q5_K, gf.T_Q6_K])
+def test_weights_from_gguf_kquant_down(tmp_path, down_type):
+    """A k-quant down projection (blk.0.ffn_down_exps of the real file is
+    Q5_K) ingested from the file gives bit-identical outputs to
+    q36moe_weights_upload_typed of the same blocks, on the direct and the
+    sorted path, with the MXFP4 shared expert."""
+    dev = torch.device("cuda:0")
+    path = str(tmp_path / "l.gguf")
+    spec = _layer_file(path, E=16, down_type=down_type)
+    w = spec["w"]
+    with moe.GGUF(path) as g:
+        wg = moe.MoEWeights.from_gguf(g, 0, with_shared=True)
+    assert wg.down_type == gf.T_Q8_0
+    wu = moe.MoEWeights.upload(w["gate"], w["up"], w["down"], w["sh_gate"], w["sh_up"], w["sh_down"],
+                               down_type=down_type)
+    for T in (3, 40):
+        rng = np.random.default_rng(80 + T)
+        x = torch.from_numpy(synth.hidden(rng, T)).to(dev)
+        lg = torch.from_numpy(rng.standard_normal((T, 16)).astype(np.float32)).to(dev)
+        shg = torch.from_numpy(rng.standard_normal(T).astype(np.float32)).to(dev)
+        outs = []
+        for wt in (wg, wu):
+            layer = moe.MoELayer(T, n_expert=16)
+            outs.append(layer.forward(wt, x, lg, shg, out_dtype=torch.float32).cpu().numpy())
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(outs[0], outs[1])
+        assert np.abs(outs[0]).max() > 0
 
 
 @pytest.mark.gpu
