@@ -16,6 +16,12 @@ expert FF 512, MXFP4 weights, e4m3 activations with per-32 E8M0 scales):
   prefill4096  T=4096, N(0,1) logits
   mixed        T=4006 (6x1 decode + 3000 + 1000 prefill) + shared expert
 
+--down-type q5_k runs the same configuration with the routed down
+projection uploaded as Q5_K blocks (the k-quant experts of real files,
+requantised on upload to int8 + f16 per 32, h quantised to int8 + fp32 per
+32, down on int8 MFMA); its weights are host-generated and uploaded, so it
+rotates fewer layers (--layers defaults to 16, 9 GB) and has no CPU leg.
+
 The roofline object is for the dominant kernel of the configuration, timed
 with HIP events around that kernel on the stream it runs on; cpu_baseline is
 the C oracle's fp32 layer forward (oracle/liboracle.so) on host cores.
@@ -36,6 +42,7 @@ MFMA_FP8_PEAK_TFS = 5000.0   # dense FP8 MFMA (scaled f8f6f4 with an e4m3 operan
 D, E, FF, K = 2048, 256, 512, 8
 MAT_BYTES = D * FF // 2 + D * FF // 32         # one packed expert matrix, 557,056 B
 EXPERT_BYTES = 3 * MAT_BYTES                   # gate + up + down, 1,671,168 B
+Q8_MAT_BYTES = D * FF + D * FF // 16           # q8_0-split down matrix, 1,114,112 B
 
 CONFIGS = {
     "decode1": dict(T=1, shared=False, steps=2000, warmup=200),
@@ -53,7 +60,9 @@ def parse():
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--config", default="decode1", choices=sorted(CONFIGS))
-    ap.add_argument("--layers", type=int, default=40)
+    ap.add_argument("--layers", type=int, default=None, help="weight layers rotated (40; 16 for q5_k)")
+    ap.add_argument("--down-type", default="mxfp4", choices=["mxfp4", "q5_k"],
+                    help="format of the routed down projection")
     ap.add_argument("--inputs", type=int, default=16, help="distinct input batches cycled")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -89,19 +98,22 @@ def distinct_experts(layer, moe):
     return int(np.unique(idx).size)
 
 
-def kernel_bytes(stage, T, U, shared):
+def kernel_bytes(stage, T, U, shared, dn_q8=False):
     """Algorithmic HBM bytes of one launch of a stage.  U = distinct routed
-    experts hit; P = routed (token, slot) rows, plus T shared rows."""
+    experts hit; P = routed (token, slot) rows, plus T shared rows.  With a
+    q8_0-split down the routed h rows carry an fp32 scale per 32 and the
+    routed down matrices are int8 + f16 per 32."""
     P = T * K + (T if shared else 0)
     Ue = U + (1 if shared else 0)
     xq = T * D + T * D // 32
-    hq = P * FF + P * FF // 32
+    hq = P * FF + P * FF // 32 * (4 if dn_q8 else 1)
     if stage == "gateup":
         # gate+up weights of the hit experts, the e4m3 activations, h out
         return Ue * 2 * MAT_BYTES + xq + hq
     if stage == "down":
         # down weights, h in, weighted f32 rows out
-        return Ue * MAT_BYTES + hq + P * D * 4
+        dn = U * (Q8_MAT_BYTES if dn_q8 else MAT_BYTES) + (MAT_BYTES if shared else 0)
+        return dn + hq + P * D * 4
     raise ValueError(stage)
 
 
@@ -182,10 +194,22 @@ def main():
     torch.cuda.set_device(dev)
     stream = torch.cuda.current_stream()
 
+    dn_q8 = args.down_type == "q5_k"
+    if args.layers is None:
+        args.layers = 16 if dn_q8 else 40
     layers = []
     for l in range(args.layers):
-        w = moe.MoEWeights.alloc(E, D, FF, FF if shared else 0)
-        w.fill_synthetic(args.seed * 1000 + l)
+        if dn_q8:
+            from q36_amd import synth
+            sw = synth.expert_weights(args.seed * 1000 + l, shared=shared)
+            rng = np.random.default_rng(args.seed * 1000 + l)
+            dn = synth.kquant_blocks(rng, E * D, FF, synth.GGML_Q5_K).reshape(E, D, -1)
+            w = moe.MoEWeights.upload(sw["gate"], sw["up"], dn, sw.get("sh_gate"), sw.get("sh_up"),
+                                      sw.get("sh_down"), down_type=synth.GGML_Q5_K)
+            del sw, dn
+        else:
+            w = moe.MoEWeights.alloc(E, D, FF, FF if shared else 0)
+            w.fill_synthetic(args.seed * 1000 + l)
         layers.append(w)
     xs, ls, ss = make_inputs(args.config, T, args.inputs, args.seed, dev)
     layer = moe.MoELayer(T, stream=stream)
@@ -270,18 +294,18 @@ def main():
         roof = {"bound": "mfma", "achieved": ach, "peak": MFMA_FP8_PEAK_TFS, "unit": "TFLOP/s",
                 "frac": ach / MFMA_FP8_PEAK_TFS, "traffic": None, "kernel": dom,
                 "kernel_us": st_us[dom], "flops_per_launch": fl,
-                "hbm_gbs": kernel_bytes(dom, T, U, shared) / (st_us[dom] * 1e-6) / 1e9}
+                "hbm_gbs": kernel_bytes(dom, T, U, shared, dn_q8) / (st_us[dom] * 1e-6) / 1e9}
     else:
-        by = kernel_bytes(dom, T, U, shared)
+        by = kernel_bytes(dom, T, U, shared, dn_q8)
         ach = by / (st_us[dom] * 1e-6) / 1e9
         roof = {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": ach / HBM_PEAK_GBS, "traffic": None, "kernel": dom,
                 "kernel_us": st_us[dom], "bytes_per_launch": by}
-    roof["traffic"] = measured_traffic(args.config, dom)
+    roof["traffic"] = None if dn_q8 else measured_traffic(args.config, dom)
     # both grouped GEMMs against both ceilings (the dominant one is `roof`)
     gemm = {}
     for st in ("gateup", "down"):
-        fl, by = kernel_flops(st, T, shared), kernel_bytes(st, T, U, shared)
+        fl, by = kernel_flops(st, T, shared), kernel_bytes(st, T, U, shared, dn_q8)
         gemm[st] = {"us": st_us[st], "tflops": fl / (st_us[st] * 1e-6) / 1e12,
                     "mfma_frac": fl / (st_us[st] * 1e-6) / 1e12 / MFMA_FP8_PEAK_TFS,
                     "gbs": by / (st_us[st] * 1e-6) / 1e9,
@@ -291,6 +315,8 @@ def main():
     torch.cuda.synchronize()
 
     layer_bytes = (U + (1 if shared else 0)) * EXPERT_BYTES + T * (D * 4 + E * 4 + D * 2)
+    if dn_q8:
+        layer_bytes += U * (Q8_MAT_BYTES - MAT_BYTES)
     res = {
         "metric": "MoE layer tokens/s (W4A8, 1 GPU)",
         "value": T / (ms * 1e-3),
@@ -305,8 +331,10 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp8e4m3 x mxfp4 (fp32 accumulate, bf16 out)",
-        "data": "synthetic (seeded MXFP4 weights filled on device, N(0,1) x and logits)",
-        "config": {"workload": args.config, "tokens": T, "d_model": D, "n_expert": E,
+        "data": ("synthetic (seeded MXFP4 gate/up and Q5_K down blocks uploaded from the host, N(0,1) x and logits)"
+                 if dn_q8 else "synthetic (seeded MXFP4 weights filled on device, N(0,1) x and logits)"),
+        "config": {"workload": args.config + ("_q5k_down" if dn_q8 else ""), "tokens": T, "d_model": D,
+                   "n_expert": E, "down_type": args.down_type,
                    "top_k": K, "d_ff": FF, "shared_expert": shared,
                    "weight_layers_rotated": args.layers,
                    "launch": (f"HIP graph of {graph_layers} layer forwards, replayed"
@@ -317,7 +345,7 @@ def main():
         "roofline": roof,
         "grouped_gemms": gemm,
     }
-    if not args.no_cpu:
+    if not args.no_cpu and not dn_q8:
         res["cpu_baseline"] = cpu_baseline(args.config, T, args.cpu_seconds, shared)
     print(json.dumps(res))
 

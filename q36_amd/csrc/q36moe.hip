@@ -23,8 +23,11 @@
 #include <cstdint>
 #include <cstdlib>
 #include <cstring>
+#include <atomic>
 #include <new>
+#include <thread>
 #include <type_traits>
+#include <vector>
 
 #include "q36moe.h"
 
@@ -2093,15 +2096,6 @@ int q36moe_weights_upload_typed(const void *gate, const void *up, const void *do
     if (rc) return rc;
     const size_t gu_src = (size_t)d_ff * (d_model / 32) * 17;
     const size_t dn_src = (size_t)d_model * dn_row;
-    const size_t m = (size_t)d_model * d_ff;
-    uint8_t *host = static_cast<uint8_t *>(malloc(w->gu_bytes > w->dn_bytes ? w->gu_bytes : w->dn_bytes));
-    int8_t *codes = dn_q8 ? static_cast<int8_t *>(malloc(m)) : nullptr;
-    uint16_t *scales = dn_q8 ? static_cast<uint16_t *>(malloc(m / 32 * 2)) : nullptr;
-    if (!host || (dn_q8 && (!codes || !scales))) {
-        free(host); free(codes); free(scales);
-        q36moe_weights_free(w);
-        return Q36MOE_ENOMEM;
-    }
     struct Job { const uint8_t *src; size_t src_stride; uint8_t *dst; size_t dst_stride; int M, K, n, q8; };
     const Job jobs[6] = {
         {static_cast<const uint8_t *>(gate), gu_src, w->gate, w->gu_bytes, d_ff, d_model, n_expert, 0},
@@ -2112,19 +2106,51 @@ int q36moe_weights_upload_typed(const void *gate, const void *up, const void *do
         {static_cast<const uint8_t *>(sh_down), (size_t)d_model * (d_ff / 32) * 17, w->sh_down, w->gu_bytes,
          d_model, d_ff, d_ff_sh ? 1 : 0, 0},
     };
+    // each matrix set is repacked on host threads (experts split across
+    // them, as the reference's upload does with OpenMP) into one staging
+    // buffer, then copied in one transfer
+    const unsigned hw = std::thread::hardware_concurrency();
+    const int nth = (int)(hw == 0 ? 1 : hw > 16 ? 16 : hw);
     for (const Job &j : jobs) {
-        for (int e = 0; e < j.n && rc == 0; e++) {
-            if (j.q8) {
-                rc = q36moe_requant_q8(down_type, j.src + j.src_stride * e, j.M, j.K, codes, scales);
-                if (rc == 0) rc = q36moe_pack_q8(codes, scales, j.M, j.K, host);
-            } else {
-                rc = q36moe_pack_mxfp4(j.src + j.src_stride * e, j.M, j.K, host);
+        if (rc || j.n == 0) continue;
+        uint8_t *stage = static_cast<uint8_t *>(malloc(j.dst_stride * j.n));
+        if (!stage) { rc = Q36MOE_ENOMEM; break; }
+        std::atomic<int> err{0};
+        auto work = [&](int tid) noexcept {
+            std::vector<int8_t> codes;
+            std::vector<uint16_t> scales;
+            try {
+                codes.resize(j.q8 ? (size_t)j.M * j.K : 0);
+                scales.resize(j.q8 ? (size_t)j.M * j.K / 32 : 0);
+            } catch (...) {
+                err.store(Q36MOE_ENOMEM);
+                return;
             }
-            if (rc == 0)
-                rc = hip_rc(hipMemcpy(j.dst + j.dst_stride * e, host, j.dst_stride, hipMemcpyHostToDevice));
+            for (int e = tid; e < j.n; e += nth) {
+                int r;
+                if (j.q8) {
+                    r = q36moe_requant_q8(down_type, j.src + j.src_stride * e, j.M, j.K, codes.data(), scales.data());
+                    if (r == 0) r = q36moe_pack_q8(codes.data(), scales.data(), j.M, j.K, stage + j.dst_stride * e);
+                } else {
+                    r = q36moe_pack_mxfp4(j.src + j.src_stride * e, j.M, j.K, stage + j.dst_stride * e);
+                }
+                if (r) err.store(r);
+            }
+        };
+        const int nt = j.n < nth ? j.n : nth;
+        std::vector<std::thread> pool;
+        try {
+            for (int t = 1; t < nt; t++) pool.emplace_back(work, t);
+        } catch (...) {
+            // threads that could not be started: their share runs here
+            for (int t = (int)pool.size() + 1; t < nt; t++) work(t);
         }
+        work(0);
+        for (auto &t : pool) t.join();
+        rc = err.load();
+        if (rc == 0) rc = hip_rc(hipMemcpy(j.dst, stage, j.dst_stride * j.n, hipMemcpyHostToDevice));
+        free(stage);
     }
-    free(host); free(codes); free(scales);
     if (rc) {
         q36moe_weights_free(w);
         return rc;
