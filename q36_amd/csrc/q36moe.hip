@@ -1291,9 +1291,11 @@ constexpr int kDlSfStride = 20;
 // scales against int8 weights with f16 scales.  Each 32-block is one
 // v_mfma_i32_16x16x32_i8 whose exact integer result is scaled by the
 // weight row's f16 scale times the h row's fp32 scale and accumulated in
-// fp32.  The wave's 4 row tiles run as two passes of 2 (codes and scales of
-// 2 row tiles are 128 VGPRs); B is staged once per chunk, as in the MXFP4
-// body.
+// fp32.  The wave's 4 row tiles run as 4 passes over the staged B (codes
+// and fp32 scales of one row tile are 96 VGPRs); B is staged once per chunk,
+// as in the MXFP4 body.  The kernel is VALU-bound (per block and output a
+// convert, a scale product and an fma), so every pass is software-pipelined
+// by one block.
 __device__ __forceinline__ void down_q8_tile(const GemmArgs &A, int e, int p0, int p1, int rb, uint8_t *sb,
                                              float (*ssf)[kDlSfStride], float *ws) {
     constexpr int KD = 512, NKP = KD / 64, NKB = KD / 32;
@@ -1315,15 +1317,20 @@ __device__ __forceinline__ void down_q8_tile(const GemmArgs &A, int e, int p0, i
         __syncthreads();
         const int ntt = (nr + 15) >> 4;
 #pragma unroll 1
-        for (int ps = 0; ps < kDlRT / 2; ps++) {
-            u32x4 ac[2][NKP], as[2][NKP];
+        for (int ps = 0; ps < kDlRT; ps++) {
+            const int mt = mt0 + ps;
+            u32x4 ac[NKP];
+            float dw[NKB][4];   // f16 scales of rows 4q..4q+3, widened once per pass
 #pragma unroll
-            for (int t = 0; t < 2; t++) {
-                const int mt = mt0 + 2 * ps + t;
+            for (int kp = 0; kp < NKP; kp++) {
+                ac[kp] = *reinterpret_cast<const u32x4 *>(W + ((size_t)mt * NKP + kp) * 1024 + lane * 16);
+                const u32x4 sv = *reinterpret_cast<const u32x4 *>(Wsc + (((size_t)mt * 4 + q) * NKB + 2 * kp) * 8);
 #pragma unroll
-                for (int kp = 0; kp < NKP; kp++) {
-                    ac[t][kp] = *reinterpret_cast<const u32x4 *>(W + ((size_t)mt * NKP + kp) * 1024 + lane * 16);
-                    as[t][kp] = *reinterpret_cast<const u32x4 *>(Wsc + (((size_t)mt * 4 + q) * NKB + 2 * kp) * 8);
+                for (int h = 0; h < 2; h++) {
+                    dw[2 * kp + h][0] = f16lo(sv[2 * h]);
+                    dw[2 * kp + h][1] = f16hi(sv[2 * h]);
+                    dw[2 * kp + h][2] = f16lo(sv[2 * h + 1]);
+                    dw[2 * kp + h][3] = f16hi(sv[2 * h + 1]);
                 }
             }
             for (int j = 0; j < ntt; j++) {
@@ -1335,43 +1342,38 @@ __device__ __forceinline__ void down_q8_tile(const GemmArgs &A, int e, int p0, i
                     const float4 v = *reinterpret_cast<const float4 *>(&ssf[r][4 * u]);
                     dh[4 * u] = v.x; dh[4 * u + 1] = v.y; dh[4 * u + 2] = v.z; dh[4 * u + 3] = v.w;
                 }
-                v4f acc[2] = {v4f{0.f, 0.f, 0.f, 0.f}, v4f{0.f, 0.f, 0.f, 0.f}};
+                // all 16 B fragments read up front (one LDS latency per column
+                // tile): lane (column n, group q) holds h K 32kb + 8q..+7 =
+                // half q&1 of chunk 2kb + q/2
+                uint2 bv[NKB];
+#pragma unroll
+                for (int kb = 0; kb < NKB; kb++)
+                    bv[kb] = *reinterpret_cast<const uint2 *>(&sb[dl_boff(r, 2 * kb + (q >> 1)) + (q & 1) * 8]);
+                v4f acc = {0.f, 0.f, 0.f, 0.f};
+                v4i prev;
 #pragma unroll
                 for (int kb = 0; kb < NKB; kb++) {
-                    // lane (column n, group q): h K 32kb + 8q..+7 = half q&1 of chunk 2kb + q/2
-                    const uint2 bv = *reinterpret_cast<const uint2 *>(&sb[dl_boff(r, 2 * kb + (q >> 1)) + (q & 1) * 8]);
-                    const long b = (long)(((uint64_t)bv.y << 32) | bv.x);
+                    const long b = (long)(((uint64_t)bv[kb].y << 32) | bv[kb].x);
+                    const u32x4 f = ac[kb >> 1];
+                    const long a = (kb & 1) ? (long)(((uint64_t)f[3] << 32) | f[2]) : (long)(((uint64_t)f[1] << 32) | f[0]);
+                    const v4i ci = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, v4i{0, 0, 0, 0}, 0, 0, 0);
+                    if (kb > 0) {   // the previous block, while this one's MFMA runs
 #pragma unroll
-                    for (int t = 0; t < 2; t++) {
-                        const u32x4 f = ac[t][kb >> 1];
-                        const long a = (kb & 1) ? (long)(((uint64_t)f[3] << 32) | f[2])
-                                                : (long)(((uint64_t)f[1] << 32) | f[0]);
-                        const v4i ci = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, v4i{0, 0, 0, 0}, 0, 0, 0);
-                        // f16 scales of rows 4q..4q+3 at block kb
-                        const u32x4 sv = as[t][kb >> 1];
-                        const uint32_t s01 = (kb & 1) ? sv[2] : sv[0], s23 = (kb & 1) ? sv[3] : sv[1];
-                        acc[t][0] += (float)ci[0] * (f16lo(s01) * dh[kb]);
-                        acc[t][1] += (float)ci[1] * (f16hi(s01) * dh[kb]);
-                        acc[t][2] += (float)ci[2] * (f16lo(s23) * dh[kb]);
-                        acc[t][3] += (float)ci[3] * (f16hi(s23) * dh[kb]);
+                        for (int i = 0; i < 4; i++) acc[i] += (float)prev[i] * (dw[kb - 1][i] * dh[kb - 1]);
                     }
-                    // two blocks (4 MFMAs) per scheduling group, their scaling
-                    // done in the group: otherwise every block's integer
-                    // result stays live until the end of the column tile
-                    if (kb & 1) {
-                        asm volatile("" : "+v"(acc[0]), "+v"(acc[1]));
-                        __builtin_amdgcn_sched_barrier(0);
-                    }
+                    prev = ci;
+                    // one block per scheduling group: left alone, the compiler
+                    // issues every block's MFMA first and holds all the results
+                    asm volatile("" : "+v"(acc));
+                    __builtin_amdgcn_sched_barrier(0);
                 }
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[i] += (float)prev[i] * (dw[NKB - 1][i] * dh[NKB - 1]);
                 if (j * 16 + n < nr) {
                     const int p = c0 + j * 16 + n;
                     const float w = ws[j * 16 + n];
-#pragma unroll
-                    for (int t = 0; t < 2; t++) {
-                        const v4f c = acc[t];
-                        *reinterpret_cast<float4 *>(A.dnw + (size_t)p * A.ldo + (mt0 + 2 * ps + t) * 16 + 4 * q) =
-                            make_float4(c[0] * w, c[1] * w, c[2] * w, c[3] * w);
-                    }
+                    *reinterpret_cast<float4 *>(A.dnw + (size_t)p * A.ldo + mt * 16 + 4 * q) =
+                        make_float4(acc[0] * w, acc[1] * w, acc[2] * w, acc[3] * w);
                 }
             }
         }
