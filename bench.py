@@ -19,8 +19,10 @@ expert FF 512, MXFP4 weights, e4m3 activations with per-32 E8M0 scales):
 --down-type q5_k runs the same configuration with the routed down
 projection uploaded as Q5_K blocks (the k-quant experts of real files,
 requantised on upload to int8 + f16 per 32, h quantised to int8 + fp32 per
-32, down on int8 MFMA); its weights are host-generated and uploaded, so it
-rotates fewer layers (--layers defaults to 16, 9 GB) and has no CPU leg.
+32, down on int8 MFMA); --shared-type q8_0 (configurations with a shared
+expert) uploads the shared expert as Q8_0 blocks, as the release file has it
+(int8 x and h, int8 MFMA).  These weights are host-generated and uploaded, so
+such runs rotate fewer layers (--layers defaults to 16) and have no CPU leg.
 
 The roofline object is for the dominant kernel of the configuration, timed
 with HIP events around that kernel on the stream it runs on; cpu_baseline is
@@ -63,6 +65,8 @@ def parse():
     ap.add_argument("--layers", type=int, default=None, help="weight layers rotated (40; 16 for q5_k)")
     ap.add_argument("--down-type", default="mxfp4", choices=["mxfp4", "q5_k"],
                     help="format of the routed down projection")
+    ap.add_argument("--shared-type", default="mxfp4", choices=["mxfp4", "q8_0"],
+                    help="format of the shared expert (configurations with one)")
     ap.add_argument("--inputs", type=int, default=16, help="distinct input batches cycled")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -98,21 +102,24 @@ def distinct_experts(layer, moe):
     return int(np.unique(idx).size)
 
 
-def kernel_bytes(stage, T, U, shared, dn_q8=False):
+def kernel_bytes(stage, T, U, shared, dn_q8=False, sh_q8=False):
     """Algorithmic HBM bytes of one launch of a stage.  U = distinct routed
-    experts hit; P = routed (token, slot) rows, plus T shared rows.  With a
-    q8_0-split down the routed h rows carry an fp32 scale per 32 and the
-    routed down matrices are int8 + f16 per 32."""
+    experts hit; P = routed (token, slot) rows, plus T shared rows.  A
+    q8_0-split matrix is int8 + f16 per 32; int8 activations carry an fp32
+    scale per 32 (h rows of a q8_0-split down; x of a q8_0-split shared
+    expert, read besides the e4m3 x)."""
     P = T * K + (T if shared else 0)
-    Ue = U + (1 if shared else 0)
-    xq = T * D + T * D // 32
-    hq = P * FF + P * FF // 32 * (4 if dn_q8 else 1)
+    sh_mat = Q8_MAT_BYTES if sh_q8 else MAT_BYTES
+    xq = T * D + T * D // 32 + (T * D + T * D // 8 if sh_q8 else 0)
+    hq = T * K * FF + T * K * FF // 32 * (4 if dn_q8 else 1)
+    if shared:
+        hq += T * FF + T * FF // 32 * (4 if sh_q8 else 1)
     if stage == "gateup":
-        # gate+up weights of the hit experts, the e4m3 activations, h out
-        return Ue * 2 * MAT_BYTES + xq + hq
+        # gate+up weights of the hit experts, the activations, h out
+        return U * 2 * MAT_BYTES + (2 * sh_mat if shared else 0) + xq + hq
     if stage == "down":
         # down weights, h in, weighted f32 rows out
-        dn = U * (Q8_MAT_BYTES if dn_q8 else MAT_BYTES) + (MAT_BYTES if shared else 0)
+        dn = U * (Q8_MAT_BYTES if dn_q8 else MAT_BYTES) + (sh_mat if shared else 0)
         return dn + hq + P * D * 4
     raise ValueError(stage)
 
@@ -195,17 +202,27 @@ def main():
     stream = torch.cuda.current_stream()
 
     dn_q8 = args.down_type == "q5_k"
+    sh_q8 = shared and args.shared_type == "q8_0"
+    host_up = dn_q8 or sh_q8
     if args.layers is None:
-        args.layers = 16 if dn_q8 else 40
+        args.layers = 16 if host_up else 40
     layers = []
     for l in range(args.layers):
-        if dn_q8:
+        if host_up:
             from q36_amd import synth
             sw = synth.expert_weights(args.seed * 1000 + l, shared=shared)
             rng = np.random.default_rng(args.seed * 1000 + l)
-            dn = synth.kquant_blocks(rng, E * D, FF, synth.GGML_Q5_K).reshape(E, D, -1)
+            dn, dn_t = sw["down"], 39   # MXFP4
+            if dn_q8:
+                dn, dn_t = synth.kquant_blocks(rng, E * D, FF, synth.GGML_Q5_K).reshape(E, D, -1), synth.GGML_Q5_K
+            sh_t = 39
+            if sh_q8:
+                sh_t = synth.GGML_Q8_0
+                sw["sh_gate"] = synth.kquant_blocks(rng, FF, D, sh_t)
+                sw["sh_up"] = synth.kquant_blocks(rng, FF, D, sh_t)
+                sw["sh_down"] = synth.kquant_blocks(rng, D, FF, sh_t)
             w = moe.MoEWeights.upload(sw["gate"], sw["up"], dn, sw.get("sh_gate"), sw.get("sh_up"),
-                                      sw.get("sh_down"), down_type=synth.GGML_Q5_K)
+                                      sw.get("sh_down"), down_type=dn_t, sh_type=sh_t)
             del sw, dn
         else:
             w = moe.MoEWeights.alloc(E, D, FF, FF if shared else 0)
@@ -294,18 +311,18 @@ def main():
         roof = {"bound": "mfma", "achieved": ach, "peak": MFMA_FP8_PEAK_TFS, "unit": "TFLOP/s",
                 "frac": ach / MFMA_FP8_PEAK_TFS, "traffic": None, "kernel": dom,
                 "kernel_us": st_us[dom], "flops_per_launch": fl,
-                "hbm_gbs": kernel_bytes(dom, T, U, shared, dn_q8) / (st_us[dom] * 1e-6) / 1e9}
+                "hbm_gbs": kernel_bytes(dom, T, U, shared, dn_q8, sh_q8) / (st_us[dom] * 1e-6) / 1e9}
     else:
-        by = kernel_bytes(dom, T, U, shared, dn_q8)
+        by = kernel_bytes(dom, T, U, shared, dn_q8, sh_q8)
         ach = by / (st_us[dom] * 1e-6) / 1e9
         roof = {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": ach / HBM_PEAK_GBS, "traffic": None, "kernel": dom,
                 "kernel_us": st_us[dom], "bytes_per_launch": by}
-    roof["traffic"] = None if dn_q8 else measured_traffic(args.config, dom)
+    roof["traffic"] = None if host_up else measured_traffic(args.config, dom)
     # both grouped GEMMs against both ceilings (the dominant one is `roof`)
     gemm = {}
     for st in ("gateup", "down"):
-        fl, by = kernel_flops(st, T, shared), kernel_bytes(st, T, U, shared, dn_q8)
+        fl, by = kernel_flops(st, T, shared), kernel_bytes(st, T, U, shared, dn_q8, sh_q8)
         gemm[st] = {"us": st_us[st], "tflops": fl / (st_us[st] * 1e-6) / 1e12,
                     "mfma_frac": fl / (st_us[st] * 1e-6) / 1e12 / MFMA_FP8_PEAK_TFS,
                     "gbs": by / (st_us[st] * 1e-6) / 1e9,
@@ -317,6 +334,8 @@ def main():
     layer_bytes = (U + (1 if shared else 0)) * EXPERT_BYTES + T * (D * 4 + E * 4 + D * 2)
     if dn_q8:
         layer_bytes += U * (Q8_MAT_BYTES - MAT_BYTES)
+    if sh_q8:
+        layer_bytes += 3 * (Q8_MAT_BYTES - MAT_BYTES)
     res = {
         "metric": "MoE layer tokens/s (W4A8, 1 GPU)",
         "value": T / (ms * 1e-3),
@@ -331,10 +350,12 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp8e4m3 x mxfp4 (fp32 accumulate, bf16 out)",
-        "data": ("synthetic (seeded MXFP4 gate/up and Q5_K down blocks uploaded from the host, N(0,1) x and logits)"
-                 if dn_q8 else "synthetic (seeded MXFP4 weights filled on device, N(0,1) x and logits)"),
-        "config": {"workload": args.config + ("_q5k_down" if dn_q8 else ""), "tokens": T, "d_model": D,
-                   "n_expert": E, "down_type": args.down_type,
+        "data": (f"synthetic (seeded MXFP4 gate/up, {args.down_type} down, {args.shared_type if shared else 'no'} "
+                 "shared expert, blocks uploaded from the host; N(0,1) x and logits)"
+                 if host_up else "synthetic (seeded MXFP4 weights filled on device, N(0,1) x and logits)"),
+        "config": {"workload": args.config + ("_q5k_down" if dn_q8 else "") + ("_q8_0_shared" if sh_q8 else ""),
+                   "tokens": T, "d_model": D, "n_expert": E, "down_type": args.down_type,
+                   "shared_type": args.shared_type if shared else None,
                    "top_k": K, "d_ff": FF, "shared_expert": shared,
                    "weight_layers_rotated": args.layers,
                    "launch": (f"HIP graph of {graph_layers} layer forwards, replayed"
@@ -345,7 +366,7 @@ def main():
         "roofline": roof,
         "grouped_gemms": gemm,
     }
-    if not args.no_cpu and not dn_q8:
+    if not args.no_cpu and not host_up:
         res["cpu_baseline"] = cpu_baseline(args.config, T, args.cpu_seconds, shared)
     print(json.dumps(res))
 

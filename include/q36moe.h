@@ -68,6 +68,9 @@ extern "C" {
 #define Q36MOE_TAP_DNW       9  /* f32   [T*k+T][d_model] w * down rows */
 #define Q36MOE_TAP_HSF      10  /* f32   [T*k+T][d_ff/32] int8 h scales
                                    (q8_0-split down; HQ then holds int8) */
+#define Q36MOE_TAP_XQ8      11  /* i8    [T][d_model] int8 x of a q8_0-split
+                                   shared expert (sorted path)           */
+#define Q36MOE_TAP_XSF      12  /* f32   [T][d_model/32] its scales      */
 
 typedef struct q36moe_weights q36moe_weights;
 typedef struct q36moe_ctx q36moe_ctx;
@@ -89,23 +92,28 @@ int q36moe_weights_upload(const void *gate, const void *up, const void *down,
                           int n_expert, int d_model, int d_ff, int d_ff_sh,
                           q36moe_weights **out);
 
-/* As q36moe_weights_upload, with the routed down projection in any of the
- * reference's expert types: down_type is the ggml type of `down` --
- * 39 MXFP4 (the call above), 13 Q5_K, 14 Q6_K (super-blocks of 256, so
- * d_ff % 256 == 0) or 8 Q8_0 -- as [n_expert][d_model][row blocks].  A
- * Q5_K / Q6_K down is dequantised and requantised on the host to int8 codes
- * with one f16 scale per 32 (the reference's q8_0-split layout), a Q8_0 one
- * is split as it is.  Such a layer quantises h per 32 to int8 with an fp32
- * scale (d = amax/127) and runs the down projection on int8 MFMA, each
- * 32-block's integer dot product scaled by both f16 and fp32 scales.  The
- * shared expert (sh_*) stays MXFP4.  Decode path 3 (the one-kernel variant)
- * is MXFP4-only: forward with it on such weights is EINVAL. */
+/* As q36moe_weights_upload, with the routed down projection and the shared
+ * expert in any of the reference's expert types.  down_type is the ggml type
+ * of `down` -- 39 MXFP4 (the call above), 13 Q5_K, 14 Q6_K (super-blocks of
+ * 256, so d_ff % 256 == 0) or 8 Q8_0 -- as [n_expert][d_model][row blocks];
+ * sh_type the type of all three shared matrices (the release file's are
+ * Q8_0).  A Q5_K / Q6_K matrix is dequantised and requantised on the host to
+ * int8 codes with one f16 scale per 32 (the reference's q8_0-split layout),
+ * a Q8_0 one is split as it is.  Activations feeding such a matrix are
+ * quantised per 32 to int8 with an fp32 scale (d = amax/127; h for a
+ * q8_0-split down, and x for a q8_0-split shared expert) and the product runs
+ * on int8 MFMA, each 32-block's integer dot product scaled by both scales.
+ * A q8_0-split layer refuses decode path 3 (the one-kernel variant), and a
+ * q8_0-split shared expert refuses q36moe_forward_q8 (its x must be the
+ * unquantised input): EINVAL. */
 int q36moe_weights_upload_typed(const void *gate, const void *up, const void *down, int down_type,
-                                const void *sh_gate, const void *sh_up, const void *sh_down,
+                                const void *sh_gate, const void *sh_up, const void *sh_down, int sh_type,
                                 int n_expert, int d_model, int d_ff, int d_ff_sh,
                                 q36moe_weights **out);
-/* ggml type of the routed down projection of w as uploaded (39 or 8). */
+/* ggml type of the routed down projection of w as uploaded (39 or 8), and
+ * of its shared expert (39, 8, or 0 without one). */
 int q36moe_weights_down_type(const q36moe_weights *w);
+int q36moe_weights_shared_type(const q36moe_weights *w);
 
 /* Allocate a weight set on the device without filling it; the caller fills
  * the packed buffers returned by q36moe_weights_device_ptrs (e.g. with
@@ -263,8 +271,8 @@ int q36moe_gguf_u32(const q36moe_gguf *g, const char *key, uint32_t *out);
  * ggml dims [d_model][d_ff][E] / [d_ff][d_model][E]; gate and up MXFP4
  * (ggml type 39), down MXFP4, Q5_K, Q6_K or Q8_0 (as
  * q36moe_weights_upload_typed); with with_shared, also
- * blk.N.ffn_{gate,up,down}_shexp.weight (MXFP4 only: a Q8_0 shared expert
- * is EINVAL here). */
+ * blk.N.ffn_{gate,up,down}_shexp.weight, all three of one type: MXFP4,
+ * Q8_0 (the release file's), Q5_K or Q6_K. */
 int q36moe_weights_from_gguf(const q36moe_gguf *g, int layer, int with_shared, q36moe_weights **out);
 /* The router rows of block `layer` as host f32 for q36moe_router_logits:
  * blk.N.ffn_gate_inp.weight [n_expert][d_model] (F32 or BF16, widened

@@ -57,6 +57,7 @@ def lib():
         L.or_requant_q8.argtypes = [ctypes.c_uint32, vp, i, i, vp, vp]
         L.or_quant_q8b.argtypes = [vp, i, vp, vp]
         L.or_expert_down_q8.argtypes = [vp, vp, i, i, vp, vp]
+        L.or_expert_h_q8.argtypes = [vp, vp, vp, vp, i, i, vp, vp]
         _lib = L
     return _lib
 
@@ -69,24 +70,30 @@ class _W(ctypes.Structure):
     _fields_ = [("gate", ctypes.c_void_p), ("up", ctypes.c_void_p), ("down", ctypes.c_void_p),
                 ("sh_gate", ctypes.c_void_p), ("sh_up", ctypes.c_void_p), ("sh_down", ctypes.c_void_p),
                 ("n_expert", ctypes.c_int), ("d_model", ctypes.c_int), ("d_ff", ctypes.c_int),
-                ("d_ff_sh", ctypes.c_int), ("down_q8", ctypes.c_void_p), ("down_q8d", ctypes.c_void_p)]
+                ("d_ff_sh", ctypes.c_int), ("down_q8", ctypes.c_void_p), ("down_q8d", ctypes.c_void_p),
+                ("sh_gate_q8", ctypes.c_void_p), ("sh_up_q8", ctypes.c_void_p), ("sh_down_q8", ctypes.c_void_p),
+                ("sh_gate_q8d", ctypes.c_void_p), ("sh_up_q8d", ctypes.c_void_p), ("sh_down_q8d", ctypes.c_void_p)]
 
 
 def _wstruct(w):
     """w: gate/up (/down) GGUF MXFP4 blocks [E][M][K/32][17], optional
     sh_*; or down_q8 (int8 [E][D][FF]) + down_q8d (f16 bits [E][D][FF/32])
-    for the q8_0-split routed down."""
+    for the q8_0-split routed down; sh_{gate,up,down}_q8 (int8) + _q8d (f16
+    bits) for a q8_0-split shared expert."""
     keep = {}
     for k, v in w.items():
         if v is None:
             continue
-        dt = {"down_q8": np.int8, "down_q8d": np.uint16}.get(k, np.uint8)
+        dt = np.int8 if k.endswith("_q8") else np.uint16 if k.endswith("_q8d") else np.uint8
         keep[k] = np.ascontiguousarray(v, dtype=dt)
     E, FF, nb, _ = keep["gate"].shape
+    ffsh = keep["sh_gate"].shape[0] if "sh_gate" in keep else keep["sh_gate_q8"].shape[0] if "sh_gate_q8" in keep else 0
     s = _W(_p(keep["gate"]), _p(keep["up"]), _p(keep.get("down")),
            _p(keep.get("sh_gate")), _p(keep.get("sh_up")), _p(keep.get("sh_down")),
-           E, nb * 32, FF, keep["sh_gate"].shape[0] if "sh_gate" in keep else 0,
-           _p(keep.get("down_q8")), _p(keep.get("down_q8d")))
+           E, nb * 32, FF, ffsh,
+           _p(keep.get("down_q8")), _p(keep.get("down_q8d")),
+           *[_p(keep.get(f"sh_{m}_q8")) for m in ("gate", "up", "down")],
+           *[_p(keep.get(f"sh_{m}_q8d")) for m in ("gate", "up", "down")])
     return s, keep
 
 
@@ -251,6 +258,18 @@ def expert_down_q8(qs, ds, hd):
     y = np.empty(D, dtype=np.float64)
     lib().or_expert_down_q8(_p(qs), _p(ds), D, FF, _p(hd), _p(y))
     return y
+
+
+def expert_h_q8(gq, gd, uq, ud, xd):
+    gq = np.ascontiguousarray(gq, dtype=np.int8)
+    uq = np.ascontiguousarray(uq, dtype=np.int8)
+    gd = np.ascontiguousarray(gd, dtype=np.uint16)
+    ud = np.ascontiguousarray(ud, dtype=np.uint16)
+    xd = np.ascontiguousarray(xd, dtype=np.float64)
+    FF, D = gq.shape
+    h = np.empty(FF, dtype=np.float64)
+    lib().or_expert_h_q8(_p(gq), _p(gd), _p(uq), _p(ud), D, FF, _p(xd), _p(h))
+    return h
 
 
 def moe_forward(w, x, logits, shg=None, k=8, scale=1.0, act_mode=0, tokens=None):

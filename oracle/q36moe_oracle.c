@@ -518,6 +518,48 @@ static void expert_d(const uint8_t *g, const uint8_t *u, const uint8_t *d,
     free(gv); free(uv); free(hd); free(hf);
 }
 
+/* Shared expert of split-Q8 matrices (pf_gemm wtype 0, q36_engine.cu:
+ * 3403-3406, used for the shared expert at :3464-3469): x quantised per 32
+ * by k_quant_q8b, int8 gate/up, SwiGLU in fp32, h quantised the same way,
+ * int8 down; act_mode 1 keeps x and h unquantised (the decode matvecs,
+ * :1627-1629). */
+static void expert_q8_d(const or_weights *w, int D, int FF, const float *x, int act_mode, double *out) {
+    double *xd = (double *)malloc(sizeof(double) * (size_t)D);
+    double *g = (double *)malloc(sizeof(double) * (size_t)FF);
+    double *u = (double *)malloc(sizeof(double) * (size_t)FF);
+    double *hd = (double *)malloc(sizeof(double) * (size_t)FF);
+    float *hf = (float *)malloc(sizeof(float) * (size_t)FF);
+    int K = D > FF ? D : FF;
+    int8_t *q = (int8_t *)malloc((size_t)K);
+    float *sc = (float *)malloc(sizeof(float) * (size_t)K / 32);
+    if (act_mode == 0) {
+        or_quant_q8b(x, D, q, sc);
+        for (int j = 0; j < D; j++) xd[j] = (double)q[j] * (double)sc[j / 32];
+    } else {
+        for (int j = 0; j < D; j++) xd[j] = x[j];
+    }
+    mv_q8_d(w->sh_gate_q8, w->sh_gate_q8d, FF, D, xd, g);
+    mv_q8_d(w->sh_up_q8, w->sh_up_q8d, FF, D, xd, u);
+    for (int f = 0; f < FF; f++) hf[f] = (float)(silu_d(g[f]) * u[f]);
+    if (act_mode == 0) {
+        or_quant_q8b(hf, FF, q, sc);
+        for (int f = 0; f < FF; f++) hd[f] = (double)q[f] * (double)sc[f / 32];
+    } else {
+        for (int f = 0; f < FF; f++) hd[f] = hf[f];
+    }
+    mv_q8_d(w->sh_down_q8, w->sh_down_q8d, D, FF, hd, out);
+    free(xd); free(g); free(u); free(hd); free(hf); free(q); free(sc);
+}
+
+void or_expert_h_q8(const int8_t *gq, const uint16_t *gd, const int8_t *uq, const uint16_t *ud, int D, int FF,
+                    const double *x, double *h) {
+    double *u = (double *)malloc(sizeof(double) * (size_t)FF);
+    mv_q8_d(gq, gd, FF, D, x, h);
+    mv_q8_d(uq, ud, FF, D, x, u);
+    for (int f = 0; f < FF; f++) h[f] = silu_d(h[f]) * u[f];
+    free(u);
+}
+
 void or_expert_h(const uint8_t *gate, const uint8_t *up, int D, int FF,
                  const double *x, double *h) {
     double *u = (double *)malloc(sizeof(double) * (size_t)FF);
@@ -562,7 +604,11 @@ void or_moe_forward(const or_weights *w, const float *x, const float *logits,
                      w->down_q8 ? w->down_q8d + (size_t)D * (FF / 32) * e : 0, D, FF, xd, act_mode, y);
             for (int j = 0; j < D; j++) o[j] += wt[s] * y[j];
         }
-        if (shg && w->sh_gate) {
+        if (shg && w->sh_gate_q8) {
+            expert_q8_d(w, D, w->d_ff_sh, xt, act_mode, y);
+            double gsh = sigm_d((double)shg[t]);
+            for (int j = 0; j < D; j++) o[j] += gsh * y[j];
+        } else if (shg && w->sh_gate) {
             expert_d(w->sh_gate, w->sh_up, w->sh_down, 0, 0, D, w->d_ff_sh, xd, act_mode, y);
             double gsh = sigm_d((double)shg[t]);
             for (int j = 0; j < D; j++) o[j] += gsh * y[j];

@@ -68,6 +68,9 @@ void or_requant_q8_row(const float *x, int K, int8_t *qs, uint16_t *ds);
 int  or_requant_q8(uint32_t type, const void *src, int M, int K, int8_t *qs, uint16_t *ds);
 void or_quant_q8b(const float *x, int K, int8_t *q, float *d);
 void or_expert_down_q8(const int8_t *qs, const uint16_t *ds, int D, int FF, const double *h, double *y);
+/* h = silu(gate . x) * (up . x) in double over q8_0-split gate/up [FF][D] */
+void or_expert_h_q8(const int8_t *gq, const uint16_t *gd, const int8_t *uq, const uint16_t *ud, int D, int FF,
+                    const double *x, double *h);
 
 /* ---- the whole layer --------------------------------------------------- */
 typedef struct {
@@ -78,6 +81,14 @@ typedef struct {
      * codes [E][d_model][d_ff] int8, f16 scales [E][d_model][d_ff/32] */
     const int8_t *down_q8;
     const uint16_t *down_q8d;
+    /* shared expert in the q8_0-split layout instead of sh_* (NULL = MXFP4,
+     * the release file's Q8_0 _shexp tensors): codes gate/up
+     * [d_ff_sh][d_model], down [d_model][d_ff_sh], f16 scales per 32.  Its
+     * activations are quantised per 32 to int8 + fp32 scale (k_quant_q8b),
+     * x and h alike, as pf_gemm does for split-Q8 weights
+     * (q36_engine.cu:3403-3406, :3464-3469). */
+    const int8_t *sh_gate_q8, *sh_up_q8, *sh_down_q8;
+    const uint16_t *sh_gate_q8d, *sh_up_q8d, *sh_down_q8d;
 } or_weights;
 
 /* act_mode 0: W4A8 -- x and h quantised exactly as the product does

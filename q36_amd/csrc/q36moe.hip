@@ -428,12 +428,29 @@ __device__ __forceinline__ void load8(const void *x, int fmt, size_t off, float 
     cvt8(load8_raw(x, fmt, off), fmt, v);
 }
 
+// The per-32 int8 quantiser of h for a q8_0-split down (k_quant_q8b,
+// q36_engine.cu:2627-2640): d = amax/127, code = rint(v * 127/amax) clamped
+// to [-127, 127], all zero for an all-zero block.
+__device__ __forceinline__ float q8b_inv(float amax) { return amax > 0.0f ? 127.0f / amax : 0.0f; }
+__device__ __forceinline__ uint32_t q8b4(float a, float b, float c, float d, float inv) {
+    auto one = [inv](float v) {
+        const float r = fminf(fmaxf(__builtin_rintf(v * inv), -127.0f), 127.0f);
+        return (uint32_t)((int)r & 255);
+    };
+    return one(a) | (one(b) << 8) | (one(c) << 16) | (one(d) << 24);
+}
+
+// f16 bit patterns (low / high half of a dword) to float
+__device__ __forceinline__ float f16lo(uint32_t d) { return (float)__builtin_bit_cast(_Float16, (uint16_t)d); }
+__device__ __forceinline__ float f16hi(uint32_t d) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(d >> 16)); }
+
 struct RouteArgs {
     const float *logits; int ld; int T; int E; int k; float scale;
     const void *x; int x_fmt; int D; int nb;
     int32_t *idx; float *wt; uint8_t *xq; uint8_t *xs; uint8_t *xs2;
     int32_t *blk_cnt; int32_t *rank;
     const uint8_t *xs_in;     // scales of pre-quantised x (x_fmt kFmtE4M3)
+    int8_t *xq8; float *xsf;  // int8 x + fp32 scales per 32 for a q8_0-split shared expert, or null
 };
 
 // One wavefront per token, TPB tokens per workgroup: top-k routing,
@@ -488,6 +505,17 @@ __global__ __launch_bounds__(64 * TPB) void k_route(RouteArgs A) {
             const uint8_t sb = quant8_lane(v, lane, A.xq + o, A.xs + (size_t)t * nb32 + b);
             // lane-group-major copy for the grouped GEMM: [t][b % 4][b / 4]
             if ((lane & 3) == 0) A.xs2[(size_t)t * nb32 + (b & 3) * (nb32 / 4) + (b >> 2)] = sb;
+            if (A.xq8) {   // the q8_0-split shared expert's int8 x (k_quant_q8b)
+                float a = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 8; i++) a = fmaxf(a, fabsf(v[i]));
+                a = fmaxf(a, __shfl_xor(a, 1, 64));
+                a = fmaxf(a, __shfl_xor(a, 2, 64));
+                const float inv = q8b_inv(a);
+                *reinterpret_cast<uint2 *>(A.xq8 + o) =
+                    make_uint2(q8b4(v[0], v[1], v[2], v[3], inv), q8b4(v[4], v[5], v[6], v[7], inv));
+                if ((lane & 3) == 0) A.xsf[(size_t)t * nb32 + b] = a / 127.0f;
+            }
         }
         }
     }
@@ -528,7 +556,8 @@ __global__ __launch_bounds__(256) void k_quant(const void *x, int x_fmt, int T, 
 struct ScanArgs {
     const int32_t *blk_cnt; int nb; int tpb; int inline_cols; int E; int T; int k;
     const int32_t *idx; const float *wt; const int32_t *rank; const float *shg;
-    int tn;
+    int tn;      // rows per routed tile
+    int tn_sh;   // rows per shared-expert tile
     int32_t *blk_off; int32_t *tot; int32_t *e_off; int32_t *perm; int32_t *pos;
     int32_t *row_tok; float *row_w; int4 *tiles; int32_t *ntiles;
 };
@@ -652,10 +681,10 @@ __global__ __launch_bounds__(256) void k_scatter(ScanArgs A) {
                 const int p0 = off[e] + j * A.tn;
                 A.tiles[toff[e] + j] = make_int4(e, p0, min(p0 + A.tn, off[e] + tot[e]), 0);
             }
-        const int nsh = A.shg ? (A.T + A.tn - 1) / A.tn : 0;
+        const int nsh = A.shg ? (A.T + A.tn_sh - 1) / A.tn_sh : 0;
         for (int j = tid; j < nsh; j += 256) {
-            const int p0 = n + j * A.tn;
-            A.tiles[toff[A.E] + j] = make_int4(A.E, p0, min(p0 + A.tn, n + A.T), 0);
+            const int p0 = n + j * A.tn_sh;
+            A.tiles[toff[A.E] + j] = make_int4(A.E, p0, min(p0 + A.tn_sh, n + A.T), 0);
         }
         if (tid == 0) *A.ntiles = toff[A.E] + nsh;
     }
@@ -681,19 +710,14 @@ struct GemmArgs {
     // with fp32 scales (hsf [row][ldo/32]); DOWN reads them from bsf
     int hq8;
     float *hsf; const float *bsf;
+    // q8_0-split shared expert: its tiles are skipped by the MXFP4 gate/up
+    // kernels (k_shared_gateup_q8 computes its rows from the int8 x) and run
+    // down_q8_tile in DOWN
+    int shq8;
+    const int8_t *xq8; const float *xsf;   // int8 x [T][K] + fp32 scales [T][K/32]
+    int T, nrouted;                        // tokens; routed rows (shared row of token t = nrouted + t)
+    int sh_wgs;                            // k_gateup_dma: leading workgroups that run the shared body
 };
-
-// The per-32 int8 quantiser of h for a q8_0-split down (k_quant_q8b,
-// q36_engine.cu:2627-2640): d = amax/127, code = rint(v * 127/amax) clamped
-// to [-127, 127], all zero for an all-zero block.
-__device__ __forceinline__ float q8b_inv(float amax) { return amax > 0.0f ? 127.0f / amax : 0.0f; }
-__device__ __forceinline__ uint32_t q8b4(float a, float b, float c, float d, float inv) {
-    auto one = [inv](float v) {
-        const float r = fminf(fmaxf(__builtin_rintf(v * inv), -127.0f), 127.0f);
-        return (uint32_t)((int)r & 255);
-    };
-    return one(a) | (one(b) << 8) | (one(c) << 16) | (one(d) << 24);
-}
 
 // Quantise and store one lane's share of a 32-row block of h for sorted row
 // p: h[r][i] is row ffb + 16r + 4q + i (the MFMA result layout of two row
@@ -937,10 +961,122 @@ __device__ __forceinline__ void body(const GemmArgs &A, Lds &L, const uint8_t *W
 }
 }  // namespace gdma
 
+// ---------------------------------------------------------------------------
+// shared expert gate/up with q8_0-split matrices (sorted path)
+// ---------------------------------------------------------------------------
+// The reference runs a split-Q8 shared expert through pf_gemm's int8 path
+// (q36_engine.cu:3403-3406, :3464-3469): x quantised per 32 to int8 with an
+// fp32 scale, int8 MMA per 32-block with both scales applied.  Workgroup =
+// (256 tokens, a 32-row block of gate and the same 32 rows of up); wave w
+// takes tokens 64w..64w+63 (4 column tiles) against the 4 row tiles over all
+// of K = 2048, so each weight fragment loaded feeds 4 MFMAs (the weights,
+// 2 MiB for gate + up, stay in L2).  Each block's integer result is scaled
+// and added in fp32.  The epilogue is the routed kernels': SwiGLU and the
+// int8 quantisation of h into the token's shared row.
+constexpr int kShCt = 4;                 // column tiles per wave
+constexpr int kShTok = 4 * 16 * kShCt;   // tokens per workgroup
+constexpr int kShRb = 512 / 32;          // 32-row blocks of d_ff
+
+// Operands of one K-pair (two 32-blocks) of the shared gate/up body.
+struct ShKp {
+    u32x4 af[4], sf[4];      // weight codes and f16 scales of the 4 row tiles
+    uint2 bx[kShCt][2];      // x codes of the column tiles, both blocks
+    float2 dh[kShCt];        // their fp32 scales
+};
+
+// Workgroup (token block tb, 32-row block rb) of the shared gate/up.
+__device__ __forceinline__ void shared_gateup_q8_body(const GemmArgs &A, int tb, int rb) {
+    constexpr int KD = 2048, NKP = KD / 64, NKB = KD / 32, MF = 512;
+    const int tid = threadIdx.x, lane = tid & 63, q = lane >> 4, n = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int t0 = tb * kShTok + wave * 16 * kShCt;   // this wave's first token
+    const int mt0 = rb * 2;                            // first row tile of the 32-row block
+    if (t0 >= A.T) return;                             // wave-uniform; no barrier follows
+    const int8_t *xr[kShCt];
+    const float *xs[kShCt];
+#pragma unroll
+    for (int j = 0; j < kShCt; j++) {
+        // padding columns repeat the last token; never stored
+        const int t = min(t0 + 16 * j + n, A.T - 1);
+        xr[j] = A.xq8 + (size_t)t * KD;
+        xs[j] = A.xsf + (size_t)t * NKB;
+    }
+    auto load = [&](int kp, ShKp &o) {
+#pragma unroll
+        for (int a = 0; a < 4; a++) {
+            const uint8_t *W = a < 2 ? A.sa : A.sb;
+            const int mt = mt0 + (a & 1);
+            o.af[a] = *reinterpret_cast<const u32x4 *>(W + ((size_t)mt * NKP + kp) * 1024 + lane * 16);
+            o.sf[a] = *reinterpret_cast<const u32x4 *>(W + (size_t)MF * KD + (((size_t)mt * 4 + q) * NKB + 2 * kp) * 8);
+        }
+        // x K 64kp + 8q..+7 (block 2kp) and 64kp + 32 + 8q..+7 (block 2kp+1)
+#pragma unroll
+        for (int j = 0; j < kShCt; j++) {
+            o.bx[j][0] = *reinterpret_cast<const uint2 *>(xr[j] + 64 * kp + 8 * q);
+            o.bx[j][1] = *reinterpret_cast<const uint2 *>(xr[j] + 64 * kp + 32 + 8 * q);
+            o.dh[j] = *reinterpret_cast<const float2 *>(xs[j] + 2 * kp);
+        }
+    };
+    v4f acc[4][kShCt];   // gate mt0, mt0+1, up mt0, mt0+1 x column tiles
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int j = 0; j < kShCt; j++) acc[a][j] = v4f{0.f, 0.f, 0.f, 0.f};
+    ShKp cur, nxt;
+    load(0, cur);
+#pragma unroll 1
+    for (int kp = 0; kp < NKP; kp++) {
+        if (kp + 1 < NKP) load(kp + 1, nxt);   // in flight while this pair computes
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int a = 0; a < 4; a++) {
+                const long av = (long)(((uint64_t)cur.af[a][2 * h + 1] << 32) | cur.af[a][2 * h]);
+                const uint32_t s01 = cur.sf[a][2 * h], s23 = cur.sf[a][2 * h + 1];
+                const float w0 = f16lo(s01), w1 = f16hi(s01), w2 = f16lo(s23), w3 = f16hi(s23);
+#pragma unroll
+                for (int j = 0; j < kShCt; j++) {
+                    const long b = (long)(((uint64_t)cur.bx[j][h].y << 32) | cur.bx[j][h].x);
+                    const v4i ci = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, b, v4i{0, 0, 0, 0}, 0, 0, 0);
+                    const float dhh = h ? cur.dh[j].y : cur.dh[j].x;
+                    acc[a][j][0] += (float)ci[0] * (w0 * dhh);
+                    acc[a][j][1] += (float)ci[1] * (w1 * dhh);
+                    acc[a][j][2] += (float)ci[2] * (w2 * dhh);
+                    acc[a][j][3] += (float)ci[3] * (w3 * dhh);
+                }
+            }
+        cur = nxt;
+    }
+#pragma unroll
+    for (int j = 0; j < kShCt; j++) {
+        float h[2][4];
+#pragma unroll
+        for (int r = 0; r < 2; r++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) h[r][i] = silu(acc[r][j][i]) * acc[2 + r][j][i];
+        const int t = t0 + 16 * j + n;
+        store_h_block(A, true, A.nrouted + t, t < A.T, mt0 * 16, q, lane, h);
+    }
+}
+
+// Stand-alone launch (skinny-tile layers); fat-tile layers run the same
+// body in k_gateup_dma's first workgroups, beside the routed tiles.
+__global__ __launch_bounds__(256) void k_shared_gateup_q8(GemmArgs A) {
+    shared_gateup_q8_body(A, blockIdx.x, blockIdx.y);
+}
+
 __global__ __launch_bounds__(256, 2) void k_gateup_dma(GemmArgs A) {
     __shared__ gdma::Lds L;
     constexpr int NRB = 512 / (16 * gdma::RT);
-    const int xcd = blockIdx.x & 7, jx = blockIdx.x >> 3;
+    // a q8_0-split shared expert's workgroups come first (a multiple of 8,
+    // so the XCD of each routed workgroup is unchanged) and run beside the
+    // routed tiles
+    const int bid = (int)blockIdx.x - A.sh_wgs;
+    if (bid < 0) {
+        shared_gateup_q8_body(A, (int)blockIdx.x / kShRb, (int)blockIdx.x % kShRb);
+        return;
+    }
+    const int xcd = bid & 7, jx = bid >> 3;
     const int ti = 8 * (jx / NRB) + xcd;
     const int mt0 = (jx % NRB) * gdma::RT;
     if (ti >= *A.ntiles) return;
@@ -948,6 +1084,7 @@ __global__ __launch_bounds__(256, 2) void k_gateup_dma(GemmArgs A) {
     Q36_TRACE_AT(28);
     const int4 tile = A.tiles[ti];
     const int e = tile.x, p0 = tile.y, p1 = tile.z;
+    if (e == A.E && A.shq8) return;      // k_shared_gateup_q8's rows
     const uint8_t *Wg = e < A.E ? A.wa + (size_t)e * A.wstride : A.sa;
     const uint8_t *Wu = e < A.E ? A.wb + (size_t)e * A.wstride : A.sb;
     const int ntt = (p1 - p0 + 15) >> 4;
@@ -1234,7 +1371,8 @@ __global__ __launch_bounds__(64 * kSkW) void k_skinny_gateup(GemmArgs A) {
     const int nj = (p1 - p0 + 15) >> 4;
     const uint8_t *Wg = e < A.E ? A.wa + (size_t)e * A.wstride : A.sa;
     const uint8_t *Wu = e < A.E ? A.wb + (size_t)e * A.wstride : A.sb;
-    const bool hq8 = A.hq8 && e < A.E;   // the shared expert's down stays MXFP4
+    if (e == A.E && A.shq8) return;      // k_shared_gateup_q8's rows
+    const bool hq8 = A.hq8 && e < A.E;   // shared rows: an MXFP4 down
     if (nj <= 1) skinny_gateup<1>(A, Wg, Wu, rb * 2, p0, p1, red, hq8);
     else skinny_gateup<2>(A, Wg, Wu, rb * 2, p0, p1, red, hq8);
 }
@@ -1258,10 +1396,6 @@ constexpr int kDlRows = 128;             // B rows staged per chunk
 // chunk index XORed (low 4 bits) with the row, so the 16 rows of a fragment
 // read fall in 16 distinct bank groups
 __device__ __forceinline__ int dl_boff(int r, int c) { return r * 512 + ((c & 16) | ((c ^ r) & 15)) * 16; }
-
-// f16 bit patterns (low / high half of a dword) to float
-__device__ __forceinline__ float f16lo(uint32_t d) { return (float)__builtin_bit_cast(_Float16, (uint16_t)d); }
-__device__ __forceinline__ float f16hi(uint32_t d) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(d >> 16)); }
 
 // Stage h rows c0 .. c0+nr (sorted order, 512 B each) into sb with
 // direct-to-LDS loads, all in flight at once: wave w loads row pairs w + 4u
@@ -1296,12 +1430,11 @@ constexpr int kDlSfStride = 20;
 // as in the MXFP4 body.  The kernel is VALU-bound (per block and output a
 // convert, a scale product and an fma), so every pass is software-pipelined
 // by one block.
-__device__ __forceinline__ void down_q8_tile(const GemmArgs &A, int e, int p0, int p1, int rb, uint8_t *sb,
+__device__ __forceinline__ void down_q8_tile(const GemmArgs &A, const uint8_t *W, int p0, int p1, int rb, uint8_t *sb,
                                              float (*ssf)[kDlSfStride], float *ws) {
     constexpr int KD = 512, NKP = KD / 64, NKB = KD / 32;
     const int tid = threadIdx.x, lane = tid & 63, q = lane >> 4, n = lane & 15;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint8_t *W = A.wa + (size_t)e * A.wstride;
     const uint8_t *Wsc = W + (size_t)2048 * KD;   // f16 scales after the codes
     const int mt0 = (rb * kDlW + wave) * kDlRT;
     for (int c0 = p0; c0 < p1; c0 += kDlRows) {
@@ -1380,8 +1513,9 @@ __device__ __forceinline__ void down_q8_tile(const GemmArgs &A, int e, int p0, i
     }
 }
 
-// Q8: routed tiles of a q8_0-split down take down_q8_tile; the shared
-// expert's tiles (MXFP4) and every tile of an MXFP4 layer the body below.
+// Q8: tiles whose down matrix is q8_0-split (routed: hq8, shared: shq8)
+// take down_q8_tile; the others, and every tile of an MXFP4 layer, the
+// body below.
 template <bool Q8>
 __global__ __launch_bounds__(64 * kDlW, Q8 ? 2 : 1) void k_down_lds(GemmArgs A) {
     constexpr int KD = 512, NKT = KD / 128, NRB = 2048 / (16 * kDlRT * kDlW);
@@ -1397,8 +1531,8 @@ __global__ __launch_bounds__(64 * kDlW, Q8 ? 2 : 1) void k_down_lds(GemmArgs A) 
     const int4 tile = A.tiles[ti];
     const int e = __builtin_amdgcn_readfirstlane(tile.x), p0 = tile.y, p1 = tile.z;
     if constexpr (Q8) {
-        if (e < A.E) {
-            down_q8_tile(A, e, p0, p1, rb, sb, ssf, ws);
+        if (e < A.E ? A.hq8 : A.shq8) {
+            down_q8_tile(A, e < A.E ? A.wa + (size_t)e * A.wstride : A.sa, p0, p1, rb, sb, ssf, ws);
             return;
         }
     }
@@ -1490,6 +1624,7 @@ struct DirectArgs {
     size_t dn_wstride;                          // bytes per routed down matrix
     int dn_q8;                                  // routed down is q8_0-split
     float *hsf;                                 // int8 h scales (tap, q8_0-split down)
+    int sh_q8;                                  // shared expert is q8_0-split
 };
 
 constexpr int kDD = 2048;   // d_model of the instantiated kernels
@@ -1502,13 +1637,98 @@ constexpr int kDF = 512;    // d_ff
 struct DirectGateupLds {
     __align__(16) uint8_t sx[kDD + 32];   // + 32 zero bytes
     uint8_t sxs[kDD / 32];
+    float sxf[kDD / 32];                  // int8 x scales (q8_0-split shared expert)
     float red[4][2][16];
     uint32_t rlds[4][kRouteLds];
 };
 
-template <bool FUSED>
+// Shared-expert entry of the direct path when its matrices are q8_0-split
+// (pf_gemm's int8 path, q36_engine.cu:3403-3406): wave w quantises x K
+// [512w, 512w+512) per 32 to int8 + fp32 scale into LDS and runs its 16
+// blocks against 16 rows of gate and up (int8 MFMA, each block scaled by
+// both scales); partial sums meet in LDS in wave order as in the MXFP4 body.
+__device__ __forceinline__ void direct_shared_q8(const DirectArgs &A, int t, int i, int ft, DirectGateupLds &L_) {
+    constexpr int NKP = kDD / 64, NKB = kDD / 32;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int q = lane >> 4;
+    const bool col0 = (lane & 15) == 0;
+    int8_t *sx = reinterpret_cast<int8_t *>(L_.sx);
+    float *sxf = L_.sxf;
+    const X8 xr = load8_raw(A.x, A.x_fmt, (size_t)t * kDD + wave * 512 + lane * 8);
+    // this wave's 8 K-pairs of the gate and up row tile ft
+    u32x4 ag[8], au[8], sg[8], su[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+        const int kp = wave * 8 + u;
+        ag[u] = *reinterpret_cast<const u32x4 *>(A.sh_gate + ((size_t)ft * NKP + kp) * 1024 + lane * 16);
+        au[u] = *reinterpret_cast<const u32x4 *>(A.sh_up + ((size_t)ft * NKP + kp) * 1024 + lane * 16);
+        const size_t so = (size_t)kDF * kDD + (((size_t)ft * 4 + q) * NKB + 2 * kp) * 8;
+        sg[u] = *reinterpret_cast<const u32x4 *>(A.sh_gate + so);
+        su[u] = *reinterpret_cast<const u32x4 *>(A.sh_up + so);
+    }
+    float v[8];
+    cvt8(xr, A.x_fmt, v);
+    float amax = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 8; u++) amax = fmaxf(amax, fabsf(v[u]));
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+    const float inv = q8b_inv(amax);
+    *reinterpret_cast<uint2 *>(sx + wave * 512 + lane * 8) =
+        make_uint2(q8b4(v[0], v[1], v[2], v[3], inv), q8b4(v[4], v[5], v[6], v[7], inv));
+    if ((lane & 3) == 0) sxf[wave * 16 + (lane >> 2)] = amax / 127.0f;
+    if (threadIdx.x < 8) reinterpret_cast<uint32_t *>(L_.sx + kDD)[threadIdx.x] = 0u;
+    __syncthreads();
+    v4f cg = {0.f, 0.f, 0.f, 0.f}, cu = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < 8; u++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int kb = 2 * (wave * 8 + u) + h;
+            // column 0 is the token; lanes of other columns read zeros
+            const uint2 bv = *reinterpret_cast<const uint2 *>(col0 ? sx + kb * 32 + 8 * q : sx + kDD);
+            const long b = (long)(((uint64_t)bv.y << 32) | bv.x);
+            const float dh = sxf[kb];
+            const long a0 = (long)(((uint64_t)ag[u][2 * h + 1] << 32) | ag[u][2 * h]);
+            const long a1 = (long)(((uint64_t)au[u][2 * h + 1] << 32) | au[u][2 * h]);
+            const v4i gi = __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, b, v4i{0, 0, 0, 0}, 0, 0, 0);
+            const v4i ui = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, b, v4i{0, 0, 0, 0}, 0, 0, 0);
+            const uint32_t g01 = sg[u][2 * h], g23 = sg[u][2 * h + 1];
+            const uint32_t u01 = su[u][2 * h], u23 = su[u][2 * h + 1];
+            cg[0] += (float)gi[0] * (f16lo(g01) * dh); cg[1] += (float)gi[1] * (f16hi(g01) * dh);
+            cg[2] += (float)gi[2] * (f16lo(g23) * dh); cg[3] += (float)gi[3] * (f16hi(g23) * dh);
+            cu[0] += (float)ui[0] * (f16lo(u01) * dh); cu[1] += (float)ui[1] * (f16hi(u01) * dh);
+            cu[2] += (float)ui[2] * (f16lo(u23) * dh); cu[3] += (float)ui[3] * (f16hi(u23) * dh);
+            // one block per scheduling group (otherwise all 32 MFMA results
+            // are held at once)
+            asm volatile("" : "+v"(cg), "+v"(cu));
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    if (col0) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            L_.red[wave][0][4 * q + r] = cg[r];
+            L_.red[wave][1][4 * q + r] = cu[r];
+        }
+    }
+    __syncthreads();
+    if (wave == 0 && lane < 16) {
+        const float g = L_.red[0][0][lane] + L_.red[1][0][lane] + L_.red[2][0][lane] + L_.red[3][0][lane];
+        const float u = L_.red[0][1][lane] + L_.red[1][1][lane] + L_.red[2][1][lane] + L_.red[3][1][lane];
+        A.hf[(size_t)i * kDF + ft * 16 + lane] = silu(g) * u;
+    }
+}
+
+template <bool FUSED, bool SHQ8 = false>
 __device__ __forceinline__ void direct_gateup_body(const DirectArgs &A, int i, int ft,
                                                    DirectGateupLds &L_) {
+    if constexpr (SHQ8) {   // workgroup-uniform: the shared expert's entries
+        const int nr0 = A.T * A.k;
+        if (i >= nr0) {
+            direct_shared_q8(A, i - nr0, i, ft, L_);
+            return;
+        }
+    }
     uint8_t *sx = L_.sx;
     uint8_t *sxs = L_.sxs;
     auto &red = L_.red;
@@ -1629,18 +1849,19 @@ __device__ __forceinline__ void direct_gateup_body(const DirectArgs &A, int i, i
     }
 }
 
+template <bool SHQ8>
 __global__ __launch_bounds__(256) void k_direct_gateup(DirectArgs A) {
     __shared__ DirectGateupLds L_;
-    direct_gateup_body<false>(A, blockIdx.x, blockIdx.y, L_);
+    direct_gateup_body<false, SHQ8>(A, blockIdx.x, blockIdx.y, L_);
 }
 
 // Token t x 16 output rows; wave s handles slot s (wave k: shared expert):
 // quantises its SwiGLU row, multiplies by the 16x512 down tile, scales by
 // the routing weight; wave 0 adds the slots in order (k_moe_combine order,
-// q36_engine.cu:784-791) and writes the output rows.  Q8: the routed slots'
-// down matrices are q8_0-split -- h is quantised per 32 to int8 with an fp32
-// scale (k_quant_q8b) and each 32-block is one int8 MFMA scaled by both
-// scales (k_gemm_expert_i8); the shared expert's wave stays MXFP4.
+// q36_engine.cu:784-791) and writes the output rows.  Q8: waves whose down
+// matrix is q8_0-split (the routed slots with dn_q8, the shared expert with
+// sh_q8) quantise h per 32 to int8 with an fp32 scale (k_quant_q8b) and run
+// each 32-block as one int8 MFMA scaled by both scales (k_gemm_expert_i8).
 template <bool Q8>
 __global__ __launch_bounds__(576) void k_direct_down(DirectArgs A) {
     __shared__ __align__(16) uint8_t sh[kMaxTopK + 1][kDF + 32];
@@ -1652,7 +1873,7 @@ __global__ __launch_bounds__(576) void k_direct_down(DirectArgs A) {
     const int nslot = blockDim.x >> 6;
     const int nr = A.T * A.k;
     const bool routed = wave < A.k;
-    const bool wq8 = Q8 && routed;   // wave-uniform: selects the MFMA kind
+    const bool wq8 = Q8 && (routed ? A.dn_q8 : A.sh_q8);   // wave-uniform: selects the MFMA kind
     const int i = routed ? t * A.k + wave : nr + t;
     const int e = routed ? A.idx[i] : A.E;
     const float wgt = routed ? A.wt[i] : 1.0f / (1.0f + expf(-A.shg[t]));
@@ -1666,7 +1887,7 @@ __global__ __launch_bounds__(576) void k_direct_down(DirectArgs A) {
     uint4 a[4];               // MXFP4: E2M1 fragments and the scale dword
     int sa = 0;
     if (wq8) {
-        const uint8_t *W = A.down + (size_t)e * A.dn_wstride;
+        const uint8_t *W = routed ? A.down + (size_t)e * A.dn_wstride : A.sh_down;
         const uint8_t *Wsc = W + (size_t)kDD * kDF;
 #pragma unroll
         for (int kp = 0; kp < NKP; kp++) {
@@ -1983,6 +2204,8 @@ struct q36moe_weights {
     uint8_t *sh_gate, *sh_up, *sh_down;
     size_t gu_bytes, dn_bytes;       // one packed matrix
     int dn_q8;                       // routed down in the packed q8_0-split layout
+    int sh_q8;                       // shared expert (all three matrices) q8_0-split
+    size_t sh_gu_bytes, sh_dn_bytes; // one packed shared matrix
     void *base;                      // single device allocation
 };
 
@@ -2012,6 +2235,7 @@ struct q36moe_ctx {
     int4 *tiles; int32_t *ntiles;
     uint8_t *hq, *hs, *hs2;
     float *hsf;                     // fp32 scales of int8 h rows (q8_0-split down)
+    int8_t *xq8; float *xsf;        // int8 x + fp32 scales (q8_0-split shared expert, sorted path)
     float *dnw;
     float *hf;                      // direct path: fp32 SwiGLU rows
     uint32_t *sync;                 // fused decode: arrive[16], depart[16], err
@@ -2036,16 +2260,19 @@ bool dims_ok(int E, int D, int FF) {
     return E >= 1 && E <= kMaxExperts && D > 0 && FF > 0 && D % 512 == 0 && FF % 512 == 0;
 }
 
-int alloc_weights(int E, int D, int FF, int FFsh, int dn_q8, q36moe_weights **out) {
+int alloc_weights(int E, int D, int FF, int FFsh, int dn_q8, int sh_q8, q36moe_weights **out) {
     if (!out || !dims_ok(E, D, FF) || !(FFsh == 0 || FFsh == FF)) return Q36MOE_EINVAL;
     q36moe_weights *w = new (std::nothrow) q36moe_weights();
     if (!w) return Q36MOE_ENOMEM;
-    w->E = E; w->D = D; w->FF = FF; w->FFsh = FFsh; w->dn_q8 = dn_q8;
+    w->E = E; w->D = D; w->FF = FF; w->FFsh = FFsh; w->dn_q8 = dn_q8; w->sh_q8 = FFsh ? sh_q8 : 0;
     const size_t m = (size_t)D * FF;
     w->gu_bytes = m / 2 + m / 32;
-    w->dn_bytes = dn_q8 ? m + m / 16 : w->gu_bytes;   // int8 codes + f16 per 32
+    const size_t q8_bytes = m + m / 16;               // int8 codes + f16 per 32
+    w->dn_bytes = dn_q8 ? q8_bytes : w->gu_bytes;
+    w->sh_gu_bytes = w->sh_dn_bytes = w->sh_q8 ? q8_bytes : w->gu_bytes;
     const size_t routed = align256(w->gu_bytes * E), routed_dn = align256(w->dn_bytes * E);
-    const size_t total = 2 * routed + routed_dn + (FFsh ? 3 * align256(w->gu_bytes) : 0);
+    const size_t sh_gu = align256(w->sh_gu_bytes), sh_dn = align256(w->sh_dn_bytes);
+    const size_t total = 2 * routed + routed_dn + (FFsh ? 2 * sh_gu + sh_dn : 0);
     if (hipMalloc(&w->base, total) != hipSuccess) {
         delete w;
         return Q36MOE_ENOMEM;
@@ -2054,12 +2281,22 @@ int alloc_weights(int E, int D, int FF, int FFsh, int dn_q8, q36moe_weights **ou
     w->gate = p; w->up = p + routed; w->down = p + 2 * routed;
     if (FFsh) {
         uint8_t *q = p + 2 * routed + routed_dn;
-        w->sh_gate = q; w->sh_up = q + align256(w->gu_bytes); w->sh_down = q + 2 * align256(w->gu_bytes);
+        w->sh_gate = q; w->sh_up = q + sh_gu; w->sh_down = q + 2 * sh_gu;
     } else {
         w->sh_gate = w->sh_up = w->sh_down = nullptr;
     }
     *out = w;
     return Q36MOE_OK;
+}
+
+// Bytes per row of a matrix of row length K in ggml type t (blocks of 32,
+// super-blocks of 256); 0 for a type no expert matrix may have here.
+size_t type_row_bytes(int t, int K) {
+    if (t == kTypeMXFP4 && K % 32 == 0) return (size_t)(K / 32) * 17;
+    if (t == kTypeQ8_0 && K % 32 == 0) return (size_t)(K / 32) * 34;
+    if (t == kTypeQ5_K && K % 256 == 0) return (size_t)(K / 256) * 176;
+    if (t == kTypeQ6_K && K % 256 == 0) return (size_t)(K / 256) * 210;
+    return 0;
 }
 
 
@@ -2070,43 +2307,40 @@ extern "C" {
 const char *q36moe_version(void) { return "q36moe 0.1 gfx950"; }
 
 int q36moe_weights_alloc(int n_expert, int d_model, int d_ff, int d_ff_sh, q36moe_weights **out) {
-    return alloc_weights(n_expert, d_model, d_ff, d_ff_sh, 0, out);
+    return alloc_weights(n_expert, d_model, d_ff, d_ff_sh, 0, 0, out);
 }
 
 int q36moe_weights_upload(const void *gate, const void *up, const void *down, const void *sh_gate,
                           const void *sh_up, const void *sh_down, int n_expert, int d_model,
                           int d_ff, int d_ff_sh, q36moe_weights **out) {
-    return q36moe_weights_upload_typed(gate, up, down, kTypeMXFP4, sh_gate, sh_up, sh_down, n_expert, d_model,
-                                       d_ff, d_ff_sh, out);
+    return q36moe_weights_upload_typed(gate, up, down, kTypeMXFP4, sh_gate, sh_up, sh_down, kTypeMXFP4, n_expert,
+                                       d_model, d_ff, d_ff_sh, out);
 }
 
 int q36moe_weights_upload_typed(const void *gate, const void *up, const void *down, int down_type,
-                                const void *sh_gate, const void *sh_up, const void *sh_down, int n_expert,
-                                int d_model, int d_ff, int d_ff_sh, q36moe_weights **out) {
+                                const void *sh_gate, const void *sh_up, const void *sh_down, int sh_type,
+                                int n_expert, int d_model, int d_ff, int d_ff_sh, q36moe_weights **out) {
     if (!gate || !up || !down || !out) return Q36MOE_EINVAL;
     if (d_ff_sh && (!sh_gate || !sh_up || !sh_down)) return Q36MOE_EINVAL;
-    // down row bytes per ggml type (blocks of 32, or super-blocks of 256)
-    size_t dn_row;
-    if (down_type == kTypeMXFP4) dn_row = (size_t)(d_ff / 32) * 17;
-    else if (down_type == kTypeQ8_0) dn_row = (size_t)(d_ff / 32) * 34;
-    else if ((down_type == kTypeQ5_K || down_type == kTypeQ6_K) && d_ff % 256 == 0)
-        dn_row = (size_t)(d_ff / 256) * (down_type == kTypeQ5_K ? 176 : 210);
-    else return Q36MOE_EINVAL;
-    const int dn_q8 = down_type != kTypeMXFP4;
+    const size_t dn_row = type_row_bytes(down_type, d_ff);
+    if (!dn_row) return Q36MOE_EINVAL;
+    if (d_ff_sh && (!type_row_bytes(sh_type, d_model) || !type_row_bytes(sh_type, d_ff))) return Q36MOE_EINVAL;
+    const int dn_q8 = down_type != kTypeMXFP4, sh_q8 = d_ff_sh && sh_type != kTypeMXFP4;
     q36moe_weights *w = nullptr;
-    int rc = alloc_weights(n_expert, d_model, d_ff, d_ff_sh, dn_q8, &w);
+    int rc = alloc_weights(n_expert, d_model, d_ff, d_ff_sh, dn_q8, sh_q8, &w);
     if (rc) return rc;
     const size_t gu_src = (size_t)d_ff * (d_model / 32) * 17;
     const size_t dn_src = (size_t)d_model * dn_row;
-    struct Job { const uint8_t *src; size_t src_stride; uint8_t *dst; size_t dst_stride; int M, K, n, q8; };
+    const int sh_t = d_ff_sh ? sh_type : kTypeMXFP4;
+    // (src, src stride, dst, dst stride, M, K, count, ggml type)
+    struct Job { const uint8_t *src; size_t src_stride; uint8_t *dst; size_t dst_stride; int M, K, n, type; };
     const Job jobs[6] = {
-        {static_cast<const uint8_t *>(gate), gu_src, w->gate, w->gu_bytes, d_ff, d_model, n_expert, 0},
-        {static_cast<const uint8_t *>(up), gu_src, w->up, w->gu_bytes, d_ff, d_model, n_expert, 0},
-        {static_cast<const uint8_t *>(down), dn_src, w->down, w->dn_bytes, d_model, d_ff, n_expert, dn_q8},
-        {static_cast<const uint8_t *>(sh_gate), gu_src, w->sh_gate, w->gu_bytes, d_ff, d_model, d_ff_sh ? 1 : 0, 0},
-        {static_cast<const uint8_t *>(sh_up), gu_src, w->sh_up, w->gu_bytes, d_ff, d_model, d_ff_sh ? 1 : 0, 0},
-        {static_cast<const uint8_t *>(sh_down), (size_t)d_model * (d_ff / 32) * 17, w->sh_down, w->gu_bytes,
-         d_model, d_ff, d_ff_sh ? 1 : 0, 0},
+        {static_cast<const uint8_t *>(gate), gu_src, w->gate, w->gu_bytes, d_ff, d_model, n_expert, kTypeMXFP4},
+        {static_cast<const uint8_t *>(up), gu_src, w->up, w->gu_bytes, d_ff, d_model, n_expert, kTypeMXFP4},
+        {static_cast<const uint8_t *>(down), dn_src, w->down, w->dn_bytes, d_model, d_ff, n_expert, down_type},
+        {static_cast<const uint8_t *>(sh_gate), 0, w->sh_gate, w->sh_gu_bytes, d_ff, d_model, d_ff_sh ? 1 : 0, sh_t},
+        {static_cast<const uint8_t *>(sh_up), 0, w->sh_up, w->sh_gu_bytes, d_ff, d_model, d_ff_sh ? 1 : 0, sh_t},
+        {static_cast<const uint8_t *>(sh_down), 0, w->sh_down, w->sh_dn_bytes, d_model, d_ff, d_ff_sh ? 1 : 0, sh_t},
     };
     // each matrix set is repacked on host threads (experts split across
     // them, as the reference's upload does with OpenMP) into one staging
@@ -2119,19 +2353,20 @@ int q36moe_weights_upload_typed(const void *gate, const void *up, const void *do
         if (!stage) { rc = Q36MOE_ENOMEM; break; }
         std::atomic<int> err{0};
         auto work = [&](int tid) noexcept {
+            const bool q8 = j.type != kTypeMXFP4;
             std::vector<int8_t> codes;
             std::vector<uint16_t> scales;
             try {
-                codes.resize(j.q8 ? (size_t)j.M * j.K : 0);
-                scales.resize(j.q8 ? (size_t)j.M * j.K / 32 : 0);
+                codes.resize(q8 ? (size_t)j.M * j.K : 0);
+                scales.resize(q8 ? (size_t)j.M * j.K / 32 : 0);
             } catch (...) {
                 err.store(Q36MOE_ENOMEM);
                 return;
             }
             for (int e = tid; e < j.n; e += nth) {
                 int r;
-                if (j.q8) {
-                    r = q36moe_requant_q8(down_type, j.src + j.src_stride * e, j.M, j.K, codes.data(), scales.data());
+                if (q8) {
+                    r = q36moe_requant_q8(j.type, j.src + j.src_stride * e, j.M, j.K, codes.data(), scales.data());
                     if (r == 0) r = q36moe_pack_q8(codes.data(), scales.data(), j.M, j.K, stage + j.dst_stride * e);
                 } else {
                     r = q36moe_pack_mxfp4(j.src + j.src_stride * e, j.M, j.K, stage + j.dst_stride * e);
@@ -2164,7 +2399,7 @@ int q36moe_weights_upload_typed(const void *gate, const void *up, const void *do
 int q36moe_weights_fill_synthetic(q36moe_weights *w, uint64_t seed, int exp_lo, int exp_hi,
                                   void *stream) {
     if (!w || exp_lo > exp_hi || exp_lo < -127 || exp_hi > 127) return Q36MOE_EINVAL;
-    if (w->dn_q8) return Q36MOE_EINVAL;   // MXFP4 sets only
+    if (w->dn_q8 || w->sh_q8) return Q36MOE_EINVAL;   // MXFP4 sets only
     hipStream_t s = static_cast<hipStream_t>(stream);
     const size_t m = (size_t)w->D * w->FF, nib = m / 2, scl = m / 32;
     uint8_t *mats[3] = {w->gate, w->up, w->down};
@@ -2203,6 +2438,12 @@ int q36moe_weights_device_ptrs(const q36moe_weights *w, void **gate, void **up, 
 int q36moe_weights_down_type(const q36moe_weights *w) {
     if (!w) return Q36MOE_EINVAL;
     return w->dn_q8 ? kTypeQ8_0 : kTypeMXFP4;
+}
+
+int q36moe_weights_shared_type(const q36moe_weights *w) {
+    if (!w) return Q36MOE_EINVAL;
+    if (!w->FFsh) return 0;
+    return w->sh_q8 ? kTypeQ8_0 : kTypeMXFP4;
 }
 
 void q36moe_weights_free(q36moe_weights *w) {
@@ -2245,6 +2486,7 @@ int q36moe_ctx_create(int max_tokens, int n_expert, int d_model, int d_ff, int t
     const size_t o_tiles = take(c->tile_cap * 16), o_nt = take(4);
     const size_t o_hq = take(rows * d_ff), o_hs = take(rows * d_ff / 32), o_hs2 = take(rows * d_ff / 32);
     const size_t o_hsf = take(rows * d_ff / 32 * 4);
+    const size_t o_xq8 = take((size_t)max_tokens * d_model), o_xsf = take((size_t)max_tokens * d_model / 32 * 4);
     const size_t o_dnw = take(rows * d_model * 4);
     const size_t direct_rows = (size_t)(max_tokens < kDirectMaxT ? max_tokens : kDirectMaxT) * (top_k + 1);
     const size_t o_hf = take(direct_rows * d_ff * 4);
@@ -2271,6 +2513,8 @@ int q36moe_ctx_create(int max_tokens, int n_expert, int d_model, int d_ff, int t
     c->ntiles = reinterpret_cast<int32_t *>(b + o_nt);
     c->hq = b + o_hq; c->hs = b + o_hs; c->hs2 = b + o_hs2;
     c->hsf = reinterpret_cast<float *>(b + o_hsf);
+    c->xq8 = reinterpret_cast<int8_t *>(b + o_xq8);
+    c->xsf = reinterpret_cast<float *>(b + o_xsf);
     c->dnw = reinterpret_cast<float *>(b + o_dnw);
     c->hf = reinterpret_cast<float *>(b + o_hf);
     c->sync = reinterpret_cast<uint32_t *>(b + o_sync);
@@ -2310,11 +2554,13 @@ static void bind_weights(Plan &P, const q36moe_weights *w) {
     P.da.wa = w->down; P.da.wb = nullptr; P.da.sa = w->sh_down; P.da.sb = nullptr;
     P.da.wstride = w->dn_bytes;
     P.ga.hq8 = P.da.hq8 = w->dn_q8;
+    P.ga.shq8 = P.da.shq8 = P.has_sh && w->sh_q8;
     P.di.gate = w->gate; P.di.up = w->up; P.di.down = w->down;
     P.di.sh_gate = w->sh_gate; P.di.sh_up = w->sh_up; P.di.sh_down = P.has_sh ? w->sh_down : nullptr;
     P.di.wstride = w->gu_bytes;
     P.di.dn_wstride = w->dn_bytes;
     P.di.dn_q8 = w->dn_q8;
+    P.di.sh_q8 = P.has_sh && w->sh_q8;
 }
 
 // Launches the kernels of one stage (direct path: ST_GATEUP is the routing +
@@ -2328,9 +2574,12 @@ static void launch_stage(const q36moe_ctx *c, const Plan &P, int st, hipStream_t
             if (st == ST_GATEUP)
                 hipLaunchKernelGGL(k_decode_fused, dim3(P.di.n_gateup_wg + T * (D / 16)), dim3(256), 0, s, P.di);
         } else if (st == ST_GATEUP) {
-            hipLaunchKernelGGL(k_direct_gateup, dim3(n, FF / 16), dim3(256), 0, s, P.di);
+            if (P.di.sh_q8)
+                hipLaunchKernelGGL(k_direct_gateup<true>, dim3(n, FF / 16), dim3(256), 0, s, P.di);
+            else
+                hipLaunchKernelGGL(k_direct_gateup<false>, dim3(n, FF / 16), dim3(256), 0, s, P.di);
         } else if (st == ST_DOWN) {
-            if (P.di.dn_q8)
+            if (P.di.dn_q8 || P.di.sh_q8)
                 hipLaunchKernelGGL(k_direct_down<true>, dim3(D / 16, T), dim3(64 * (K + P.has_sh)), 0, s, P.di);
             else
                 hipLaunchKernelGGL(k_direct_down<false>, dim3(D / 16, T), dim3(64 * (K + P.has_sh)), 0, s, P.di);
@@ -2350,14 +2599,17 @@ static void launch_stage(const q36moe_ctx *c, const Plan &P, int st, hipStream_t
             hipLaunchKernelGGL(k_scatter, dim3(P.nb), dim3(256), 0, s, P.sa);
             break;
         case ST_GATEUP:
-            if (P.skinny)
+            if (P.skinny) {
                 hipLaunchKernelGGL(k_skinny_gateup, dim3(P.tiles * 16), dim3(64 * kSkW), 0, s, P.ga);
-            else
-                hipLaunchKernelGGL(k_gateup_dma, dim3(P.tiles * (FF / (16 * gdma::RT))), dim3(64 * gdma::W), 0, s,
-                                   P.ga);
+                if (P.ga.shq8)
+                    hipLaunchKernelGGL(k_shared_gateup_q8, dim3((T + kShTok - 1) / kShTok, kShRb), dim3(256), 0, s,
+                                       P.ga);
+            } else
+                hipLaunchKernelGGL(k_gateup_dma, dim3(P.tiles * (FF / (16 * gdma::RT)) + P.ga.sh_wgs),
+                                   dim3(64 * gdma::W), 0, s, P.ga);
             break;
         case ST_DOWN:
-            if (P.da.hq8)
+            if (P.da.hq8 || P.da.shq8)
                 hipLaunchKernelGGL(k_down_lds<true>, dim3(P.tiles * (D / (16 * kDlRT * kDlW))), dim3(64 * kDlW), 0, s,
                                    P.da);
             else
@@ -2379,6 +2631,8 @@ int q36moe_ctx_replay(q36moe_ctx *c, const q36moe_weights *w, int stage) {
     if (c->plan->has_sh && !w->sh_gate) return Q36MOE_EINVAL;
     // the plan's h quantisation matches the down format it was made for
     if ((c->plan->direct ? c->plan->di.dn_q8 : c->plan->da.hq8) != w->dn_q8) return Q36MOE_EINVAL;
+    if ((c->plan->direct ? c->plan->di.sh_q8 : c->plan->da.shq8) != (c->plan->has_sh && w->sh_q8))
+        return Q36MOE_EINVAL;
     Plan P = *c->plan;
     bind_weights(P, w);
     launch_stage(c, P, stage, c->stream);
@@ -2410,12 +2664,19 @@ static int forward_impl(q36moe_ctx *c, const q36moe_weights *w, const void *x, i
     const bool direct = (pm == 2 || pm == 3) ? (T <= kDirectMaxT) : (pm == 1 || pm == 4) ? false
                                                                                       : (T <= kDirectMaxT);
     if ((pm == 2 || pm == 3) && !direct) return Q36MOE_EINVAL;
-    if (pm == 3 && w->dn_q8) return Q36MOE_EINVAL;   // the one-kernel decode is MXFP4-only
+    const bool shq8 = has_sh && w->sh_q8;
+    if (pm == 3 && (w->dn_q8 || shq8)) return Q36MOE_EINVAL;   // the one-kernel decode is MXFP4-only
+    // a q8_0-split shared expert quantises x itself (int8 + fp32 per 32):
+    // pre-quantised e4m3 input cannot feed it
+    if (shq8 && x_fmt == kFmtE4M3) return Q36MOE_EINVAL;
     // sorted path: skinny tiles (<= 32 rows) while the average expert has at
     // most kSkinnyRows rows, else fat tiles of up to kGdTok rows
     const bool skinny = pm == 4 || (pm == 0 && (size_t)n <= (size_t)kSkinnyRows * E);
     const int tn = skinny ? kSkTok : kGdTok;
-    int tiles = n / tn + (n < E ? n : E) + (has_sh ? (T + tn - 1) / tn : 0);
+    // a q8_0-split shared expert's down is VALU-heavy: its rows go in small
+    // tiles so the work spreads over many workgroups instead of trailing
+    const int tn_sh = shq8 ? kSkTok : tn;
+    int tiles = n / tn + (n < E ? n : E) + (has_sh ? (T + tn_sh - 1) / tn_sh : 0);
     tiles = (tiles + 7) & ~7;   // whole groups of 8 for the XCD-major tile order
 
     Plan &P = *c->plan;
@@ -2432,7 +2693,7 @@ static int forward_impl(q36moe_ctx *c, const q36moe_weights *w, const void *x, i
     } else {
         P.ra = RouteArgs{logits, ld_logits, T, E, K, scale, x, x_fmt, D, nb,
                          c->topk_idx, c->topk_w, c->xq, c->xs, c->xs2, c->blk_cnt, c->rank, xs_in};
-        P.sa = ScanArgs{c->blk_cnt, nb, tpb, nb <= kScanInlineBlocks ? 1 : 0, E, T, K, c->topk_idx, c->topk_w, c->rank, shg, tn,
+        P.sa = ScanArgs{c->blk_cnt, nb, tpb, nb <= kScanInlineBlocks ? 1 : 0, E, T, K, c->topk_idx, c->topk_w, c->rank, shg, tn, tn_sh,
                         c->blk_off, c->tot, c->e_off, c->perm, c->pos, c->row_tok, c->row_w, c->tiles,
                         c->ntiles};
         GemmArgs &ga = P.ga;
@@ -2443,6 +2704,8 @@ static int forward_impl(q36moe_ctx *c, const q36moe_weights *w, const void *x, i
         ga.bs2 = c->xs2; ga.row_tok = c->row_tok; ga.row_w = c->row_w;
         ga.hq = c->hq; ga.hs = c->hs; ga.hs2 = c->hs2; ga.ldo = FF;
         ga.hsf = c->hsf;
+        ga.xq8 = c->xq8; ga.xsf = c->xsf; ga.T = T; ga.nrouted = n;
+        ga.sh_wgs = shq8 && !skinny ? (T + kShTok - 1) / kShTok * kShRb : 0;
         GemmArgs &da = P.da;
         da = ga;
         da.M = D;
@@ -2450,6 +2713,10 @@ static int forward_impl(q36moe_ctx *c, const q36moe_weights *w, const void *x, i
         da.bsf = c->hsf;
     }
     bind_weights(P, w);
+    if (!direct && shq8) {   // k_route also writes the int8 x the shared expert reads
+        P.ra.xq8 = c->xq8;
+        P.ra.xsf = c->xsf;
+    }
     for (int st = 0; st < ST_COUNT; st++) {
         if (c->timing) (void)hipEventRecord(c->ev[st], s);
         launch_stage(c, P, st, s);
@@ -2560,6 +2827,12 @@ int q36moe_ctx_copy_tap(q36moe_ctx *c, int tap, void *dst, size_t bytes, size_t 
         case Q36MOE_TAP_HQ: src = c->hq; sz = rows * c->FF; break;
         case Q36MOE_TAP_HS: src = c->hs; sz = rows * c->FF / 32; break;
         case Q36MOE_TAP_HSF: src = c->hsf; sz = rows * c->FF / 32 * 4; break;
+        case Q36MOE_TAP_XQ8:
+            if (c->last_path == 1) return Q36MOE_EINVAL;   // quantised in LDS only
+            src = c->xq8; sz = T * c->D; break;
+        case Q36MOE_TAP_XSF:
+            if (c->last_path == 1) return Q36MOE_EINVAL;
+            src = c->xsf; sz = T * c->D / 32 * 4; break;
         case Q36MOE_TAP_DNW:
             if (c->last_path == 1) return Q36MOE_EINVAL;   // combined in registers
             src = c->dnw; sz = rows * c->D * 4; break;

@@ -293,13 +293,17 @@ int q36moe_weights_from_gguf(const q36moe_gguf *g, int layer, int with_shared, q
         dt->dims[1] != D || dt->dims[2] != E || D > (1u << 20) || FF > (1u << 20) || E > (1u << 20))
         return Q36MOE_EINVAL;
     const uint8_t *sg = nullptr, *su = nullptr, *sd = nullptr;
-    int ff_sh = 0;
+    int ff_sh = 0, sh_type = (int)T_MXFP4;
     if (with_shared) {
         const Tensor *a = find(g, blk(layer, "ffn_gate_shexp.weight"));
         const Tensor *b = find(g, blk(layer, "ffn_up_shexp.weight"));
         const Tensor *c = find(g, blk(layer, "ffn_down_shexp.weight"));
         if (!a || !b || !c) return Q36MOE_ENOENT;
-        if (a->type != T_MXFP4 || b->type != T_MXFP4 || c->type != T_MXFP4) return Q36MOE_EINVAL;
+        // one type for all three; MXFP4 or one of the split-Q8 sources
+        if (a->type != b->type || a->type != c->type) return Q36MOE_EINVAL;
+        if (a->type != T_MXFP4 && a->type != T_Q8_0 && a->type != T_Q5_K && a->type != T_Q6_K)
+            return Q36MOE_EINVAL;
+        sh_type = (int)a->type;
         if (a->dims[0] != D || a->dims[1] != FF || b->dims[0] != D || b->dims[1] != FF || c->dims[0] != FF ||
             c->dims[1] != D || a->dims[2] != 1 || b->dims[2] != 1 || c->dims[2] != 1)
             return Q36MOE_EINVAL;
@@ -309,7 +313,7 @@ int q36moe_weights_from_gguf(const q36moe_gguf *g, int layer, int with_shared, q
         ff_sh = (int)FF;
     }
     return q36moe_weights_upload_typed(data_of(g, gt), data_of(g, ut), data_of(g, dt), (int)dt->type, sg, su,
-                                       sd, (int)E, (int)D, (int)FF, ff_sh, out);
+                                       sd, sh_type, (int)E, (int)D, (int)FF, ff_sh, out);
 }
 
 int q36moe_router_from_gguf(const q36moe_gguf *g, int layer, float *dst, size_t dst_floats, int *n_rows,

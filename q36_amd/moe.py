@@ -20,7 +20,7 @@ FMT_F32 = 0
 FMT_BF16 = 1
 
 TAP_TOPK_IDX, TAP_TOPK_W, TAP_XQ, TAP_XS, TAP_EOFF, TAP_PERM, TAP_POS, TAP_HQ, TAP_HS, TAP_DNW = range(10)
-TAP_HSF = 10
+TAP_HSF, TAP_XQ8, TAP_XSF = 10, 11, 12
 GGML_Q8_0, GGML_Q5_K, GGML_Q6_K, GGML_MXFP4 = 8, 13, 14, 39
 
 _ERRORS = {-22: "EINVAL", -12: "ENOMEM", -1000: "EHIP"}
@@ -46,8 +46,9 @@ def lib():
     L.q36moe_expert_bytes.argtypes = [i, i]
     L.q36moe_expert_bytes.restype = sz
     L.q36moe_weights_upload.argtypes = [vp] * 6 + [i] * 4 + [pp]
-    L.q36moe_weights_upload_typed.argtypes = [vp] * 3 + [i] + [vp] * 3 + [i] * 4 + [pp]
+    L.q36moe_weights_upload_typed.argtypes = [vp] * 3 + [i] + [vp] * 3 + [i] * 5 + [pp]
     L.q36moe_weights_down_type.argtypes = [vp]
+    L.q36moe_weights_shared_type.argtypes = [vp]
     L.q36moe_requant_q8.argtypes = [i, vp, i, i, vp, vp]
     L.q36moe_pack_q8.argtypes = [vp, vp, i, i, vp]
     L.q36moe_unpack_q8.argtypes = [vp, i, i, vp, vp]
@@ -131,12 +132,15 @@ class MoEWeights:
         self.n_expert, self.d_model, self.d_ff, self.d_ff_sh = n_expert, d_model, d_ff, d_ff_sh
 
     @classmethod
-    def upload(cls, gate, up, down, sh_gate=None, sh_up=None, sh_down=None, down_type=GGML_MXFP4):
+    def upload(cls, gate, up, down, sh_gate=None, sh_up=None, sh_down=None, down_type=GGML_MXFP4,
+               sh_type=GGML_MXFP4):
         """gate/up [E, d_ff, d_model/32, 17] GGUF block_mxfp4 bytes (numpy
         uint8); down [E, d_model, row bytes] blocks of ggml type down_type
         (GGML_MXFP4 [.., d_ff/32, 17], or GGML_Q8_0 / GGML_Q5_K / GGML_Q6_K,
         requantised to the q8_0-split layout as upload() does for k-quant
-        experts, q36_engine.cu:229-252)."""
+        experts, q36_engine.cu:229-252).  sh_* are the shared expert's three
+        matrices, all of ggml type sh_type ([rows, row bytes] blocks; the
+        release file's are GGML_Q8_0)."""
         E, d_ff, nbk, _ = gate.shape
         d_model = nbk * 32
         keep = []
@@ -147,7 +151,7 @@ class MoEWeights:
             ptrs.append(p)
         d_ff_sh = 0
         if sh_gate is not None:
-            d_ff_sh = sh_gate.shape[0]
+            d_ff_sh = d_ff
             for a in (sh_gate, sh_up, sh_down):
                 a, p = _host_u8(a)
                 keep.append(a)
@@ -155,8 +159,8 @@ class MoEWeights:
         else:
             ptrs += [None, None, None]
         h = ctypes.c_void_p()
-        check(lib().q36moe_weights_upload_typed(*ptrs[:3], down_type, *ptrs[3:], E, d_model, d_ff, d_ff_sh,
-                                                ctypes.byref(h)),
+        check(lib().q36moe_weights_upload_typed(*ptrs[:3], down_type, *ptrs[3:], sh_type, E, d_model, d_ff,
+                                                d_ff_sh, ctypes.byref(h)),
               "q36moe_weights_upload_typed")
         return cls(h, E, d_model, d_ff, d_ff_sh)
 
@@ -165,6 +169,11 @@ class MoEWeights:
         """ggml type of the routed down on the device: GGML_MXFP4 or GGML_Q8_0
         (the q8_0-split layout, whatever type it was uploaded from)."""
         return lib().q36moe_weights_down_type(self._h)
+
+    @property
+    def shared_type(self):
+        """GGML_MXFP4 or GGML_Q8_0 (q8_0-split) for the shared expert, 0 without one."""
+        return lib().q36moe_weights_shared_type(self._h)
 
     @classmethod
     def from_gguf(cls, gguf, layer, with_shared=False):
@@ -341,6 +350,7 @@ class MoELayer:
             TAP_POS: ((T * k,), torch.int32), TAP_HQ: ((rows, FF), torch.uint8),
             TAP_HS: ((rows, FF // 32), torch.uint8), TAP_DNW: ((rows, D), torch.float32),
             TAP_HSF: ((rows, FF // 32), torch.float32),
+            TAP_XQ8: ((T, D), torch.int8), TAP_XSF: ((T, D // 32), torch.float32),
         }
         shape, dt = shapes[which]
         dst = torch.empty(shape, dtype=dt, device="cuda")

@@ -53,10 +53,15 @@ def _layer_file(path, E=16, layer=0, router_bf16=False, shared="mxfp4", seed=5, 
         tensors += [(p + "ffn_gate_shexp.weight", [D, FF], gf.T_MXFP4, w["sh_gate"].tobytes()),
                     (p + "ffn_up_shexp.weight", [D, FF], gf.T_MXFP4, w["sh_up"].tobytes()),
                     (p + "ffn_down_shexp.weight", [FF, D], gf.T_MXFP4, w["sh_down"].tobytes())]
-    elif shared == "q8_0":   # the reference model's shared expert type
-        tensors += [(p + n, dims, gf.T_Q8_0, bytes(dims[0] * dims[1] // 32 * 34))
-                    for n, dims in (("ffn_gate_shexp.weight", [D, FF]), ("ffn_up_shexp.weight", [D, FF]),
-                                    ("ffn_down_shexp.weight", [FF, D]))]
+    elif shared in ("q8_0", "mixed"):   # the release file's shared expert type
+        for n, dims in (("sh_gate", [D, FF]), ("sh_up", [D, FF]), ("sh_down", [FF, D])):
+            w[n] = synth.kquant_blocks(rng, dims[1], dims[0], gf.T_Q8_0)
+        # "mixed": the down relabelled MXFP4 (one type is required for all three)
+        sh_down_t = gf.T_MXFP4 if shared == "mixed" else gf.T_Q8_0
+        tensors += [(p + "ffn_gate_shexp.weight", [D, FF], gf.T_Q8_0, w["sh_gate"].tobytes()),
+                    (p + "ffn_up_shexp.weight", [D, FF], gf.T_Q8_0, w["sh_up"].tobytes()),
+                    (p + "ffn_down_shexp.weight", [FF, D], sh_down_t,
+                     w["sh_down"].tobytes()[:FF * D // 32 * 17] if shared == "mixed" else w["sh_down"].tobytes())]
     gf.write(path, kvs, tensors, alignment=alignment)
     return {"w": w, "router": router, "shg_row": shg_row, "tensors": tensors, "n_kv": len(kvs)}
 
@@ -196,11 +201,11 @@ def test_router_from_gguf(tmp_path, router_bf16):
 def test_weights_from_gguf_rejects_before_upload(tmp_path):
     """Type and name checks run before any device call."""
     path = str(tmp_path / "l.gguf")
-    _layer_file(path, E=2, shared="q8_0")
+    _layer_file(path, E=2, shared="mixed")
     L = moe.lib()
     with moe.GGUF(path) as g:
         h = ctypes.c_void_p()
-        assert L.q36moe_weights_from_gguf(g._h, 0, 1, ctypes.byref(h)) == -22   # Q8_0 shared expert
+        assert L.q36moe_weights_from_gguf(g._h, 0, 1, ctypes.byref(h)) == -22   # shared tensors of two types
         assert L.q36moe_weights_from_gguf(g._h, 3, 0, ctypes.byref(h)) == -2    # no block 3
         assert L.q36moe_weights_from_gguf(g._h, -1, 0, ctypes.byref(h)) == -22
     # routed gate/up must be MXFP4 (the bytes are relabelled Q8_0 here: a
@@ -228,6 +233,34 @@ def test_weights_from_gguf_kquant_down(tmp_path, down_type):
                                down_type=down_type)
     for T in (3, 40):
         rng = np.random.default_rng(80 + T)
+        x = torch.from_numpy(synth.hidden(rng, T)).to(dev)
+        lg = torch.from_numpy(rng.standard_normal((T, 16)).astype(np.float32)).to(dev)
+        shg = torch.from_numpy(rng.standard_normal(T).astype(np.float32)).to(dev)
+        outs = []
+        for wt in (wg, wu):
+            layer = moe.MoELayer(T, n_expert=16)
+            outs.append(layer.forward(wt, x, lg, shg, out_dtype=torch.float32).cpu().numpy())
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(outs[0], outs[1])
+        assert np.abs(outs[0]).max() > 0
+
+
+@pytest.mark.gpu
+def test_weights_from_gguf_q8_0_shared(tmp_path):
+    """The release file's layout: MXFP4 experts with a Q5_K down and a Q8_0
+    shared expert, ingested from the file, give bit-identical outputs to the
+    typed upload of the same blocks (direct and sorted paths)."""
+    dev = torch.device("cuda:0")
+    path = str(tmp_path / "l.gguf")
+    spec = _layer_file(path, E=16, shared="q8_0", down_type=gf.T_Q5_K)
+    w = spec["w"]
+    with moe.GGUF(path) as g:
+        wg = moe.MoEWeights.from_gguf(g, 0, with_shared=True)
+    assert wg.shared_type == gf.T_Q8_0 and wg.down_type == gf.T_Q8_0
+    wu = moe.MoEWeights.upload(w["gate"], w["up"], w["down"], w["sh_gate"], w["sh_up"], w["sh_down"],
+                               down_type=gf.T_Q5_K, sh_type=gf.T_Q8_0)
+    for T in (3, 40):
+        rng = np.random.default_rng(90 + T)
         x = torch.from_numpy(synth.hidden(rng, T)).to(dev)
         lg = torch.from_numpy(rng.standard_normal((T, 16)).astype(np.float32)).to(dev)
         shg = torch.from_numpy(rng.standard_normal(T).astype(np.float32)).to(dev)

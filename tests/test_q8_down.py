@@ -243,8 +243,9 @@ def test_upload_typed_rejects_bad_args_without_gpu():
     out = ctypes.c_void_p()
     # unknown down type; a k-quant with d_ff not a multiple of 256 cannot occur
     # at d_ff % 512 == 0, so an unknown type and null pointers are the cases
-    assert L.q36moe_weights_upload_typed(p, p, p, 2, None, None, None, 4, 512, 512, 0, ctypes.byref(out)) == -22
-    assert L.q36moe_weights_upload_typed(p, p, None, Q5_K, None, None, None, 4, 512, 512, 0, ctypes.byref(out)) == -22
+    assert L.q36moe_weights_upload_typed(p, p, p, 2, None, None, None, 39, 4, 512, 512, 0, ctypes.byref(out)) == -22
+    assert L.q36moe_weights_upload_typed(p, p, None, Q5_K, None, None, None, 39, 4, 512, 512, 0,
+                                         ctypes.byref(out)) == -22
     assert L.q36moe_requant_q8(Q5_K, p, 4, 100, p, p) == -22      # K % 256
     assert L.q36moe_requant_q8(30, p, 4, 512, p, p) == -22        # not a k-quant / Q8_0
     assert L.q36moe_weights_down_type(None) == -22
@@ -437,4 +438,165 @@ def test_q8_down_path3_and_replay_format_checks(q8_layer):
     with pytest.raises(moe.Q36MoEError):
         layer.replay(mx, 3)
     layer.replay(dw, 3)
+    torch.cuda.synchronize()
+
+
+# ---------------------------------------------------------------------------
+# q8_0-split shared expert (the release file's Q8_0 _shexp tensors)
+# ---------------------------------------------------------------------------
+def _shared_q8(oracle, rng, D=2048, FF=512, src_type=Q8_0):
+    """Shared gate/up/down as GGUF blocks of src_type and their q8_0-split form."""
+    blocks = {"sh_gate": synth.kquant_blocks(rng, FF, D, src_type),
+              "sh_up": synth.kquant_blocks(rng, FF, D, src_type),
+              "sh_down": synth.kquant_blocks(rng, D, FF, src_type)}
+    split = {}
+    for k, (M, K) in (("sh_gate", (FF, D)), ("sh_up", (FF, D)), ("sh_down", (D, FF))):
+        split[k + "_q8"], split[k + "_q8d"] = oracle.requant_q8(src_type, blocks[k], M, K)
+    return blocks, split
+
+
+def test_oracle_shared_q8_composition(oracle):
+    rng = np.random.default_rng(21)
+    E, Dm, F, T, k = 4, 512, 512, 3, 2
+    w = synth.expert_weights(22, n_expert=E, d_model=Dm, d_ff=F)
+    _, sq = _shared_q8(oracle, rng, Dm, F)
+    wq = {"gate": w["gate"], "up": w["up"], "down": w["down"], **sq}
+    x = rng.standard_normal((T, Dm)).astype(np.float32)
+    lg = rng.standard_normal((T, E)).astype(np.float32)
+    shg = rng.standard_normal(T).astype(np.float32)
+    got = oracle.moe_forward(wq, x, lg, shg, k=k)
+    routed = oracle.moe_forward({"gate": w["gate"], "up": w["up"], "down": w["down"]}, x, lg, k=k)
+    for t in range(T):
+        q, s = oracle.quant_q8b(x[t])
+        xd = q.astype(np.float64) * np.repeat(s.astype(np.float64), 32)
+        hf = oracle.expert_h_q8(sq["sh_gate_q8"], sq["sh_gate_q8d"], sq["sh_up_q8"], sq["sh_up_q8d"],
+                                xd).astype(np.float32)
+        hq, hs = oracle.quant_q8b(hf)
+        hd = hq.astype(np.float64) * np.repeat(hs.astype(np.float64), 32)
+        ysh = oracle.expert_down_q8(sq["sh_down_q8"], sq["sh_down_q8d"], hd)
+        ref = routed[t] + ysh / (1 + np.exp(-float(shg[t])))
+        np.testing.assert_allclose(got[t], ref, rtol=1e-12, atol=1e-12 * np.abs(ref).max())
+
+
+def test_upload_typed_rejects_bad_shared_type_without_gpu():
+    from q36_amd import moe
+    L = moe.lib()
+    buf = np.zeros(4096, dtype=np.uint8)
+    p = ctypes.c_void_p(buf.ctypes.data)
+    out = ctypes.c_void_p()
+    assert L.q36moe_weights_upload_typed(p, p, p, 39, p, p, p, 30, 4, 512, 512, 512, ctypes.byref(out)) == -22
+    assert L.q36moe_weights_upload_typed(p, p, p, 39, p, None, p, 8, 4, 512, 512, 512, ctypes.byref(out)) == -22
+    assert L.q36moe_weights_shared_type(None) == -22
+
+
+@pytest.fixture(scope="module")
+def q8_shared_layer(oracle):
+    import torch
+    from q36_amd import moe
+    assert torch.cuda.is_available(), "GPU tests need a GPU"
+    w = synth.expert_weights(2031)
+    rng = np.random.default_rng(2032)
+    blocks, sq = _shared_q8(oracle, rng)
+    E, D, FF = synth.N_EXPERT, synth.D_MODEL, synth.D_FF
+    down = synth.kquant_blocks(rng, E * D, FF, Q6_K).reshape(E, D, -1)
+    dq = np.empty((E, D, FF), dtype=np.int8)
+    dd = np.empty((E, D, FF // 32), dtype=np.uint16)
+    for e in range(E):
+        dq[e], dd[e] = oracle.requant_q8(Q6_K, down[e], D, FF)
+    # the same routed experts with an MXFP4 down (shared Q8 alone) and with a Q6_K down (both)
+    dw_mx = moe.MoEWeights.upload(w["gate"], w["up"], w["down"], blocks["sh_gate"], blocks["sh_up"],
+                                  blocks["sh_down"], sh_type=Q8_0)
+    dw_both = moe.MoEWeights.upload(w["gate"], w["up"], down, blocks["sh_gate"], blocks["sh_up"],
+                                    blocks["sh_down"], down_type=Q6_K, sh_type=Q8_0)
+    assert dw_mx.shared_type == Q8_0 and dw_mx.down_type == 39
+    assert dw_both.shared_type == Q8_0 and dw_both.down_type == Q8_0
+    return {"w": w, "sq": sq, "dq": dq, "dd": dd, "mx": dw_mx, "both": dw_both}
+
+
+def _check_shared_q8(oracle, L, which, T, path, seed):
+    import torch
+    from q36_amd import moe
+    w, sq = L["w"], L["sq"]
+    dw = L[which]
+    k = 8
+    rng = np.random.default_rng(seed)
+    x = synth.hidden(rng, T)
+    lg = synth.normal_logits(rng, T)
+    shg = rng.standard_normal(T).astype(np.float32)
+    layer, y32, y16 = _run(dw, x, lg, shg, path)
+    np.testing.assert_array_equal(y16, torch.from_numpy(y32).to(torch.bfloat16).float().numpy())
+    gi, ow = oracle.router_topk(lg, k)
+    np.testing.assert_array_equal(layer.tap(moe.TAP_TOPK_IDX).cpu().numpy(), gi)
+    if layer.last_path != 1:   # sorted path: the int8 x the shared expert reads, bit-exact
+        q, s = zip(*[oracle.quant_q8b(x[t]) for t in range(T)])
+        np.testing.assert_array_equal(layer.tap(moe.TAP_XQ8).cpu().numpy(), np.stack(q))
+        np.testing.assert_array_equal(layer.tap(moe.TAP_XSF).cpu().numpy(), np.stack(s))
+    toks = np.arange(T) if T <= 40 else rng.choice(T, 24, replace=False)
+    pos = layer.tap(moe.TAP_POS).cpu().numpy()
+    hq = layer.tap(moe.TAP_HQ).cpu().numpy()
+    hs = layer.tap(moe.TAP_HS).cpu().numpy()
+    hsf = layer.tap(moe.TAP_HSF).cpu().numpy()
+    ref_h = np.zeros((toks.size, x.shape[1]))
+    flips = 0
+    for j, t in enumerate(toks):
+        for s in range(k):
+            p, e = int(pos[t * k + s]), int(gi[t, s])
+            if which == "both":
+                hd = hq[p].view(np.int8).astype(np.float64) * np.repeat(hsf[p].astype(np.float64), 32)
+                y = oracle.expert_down_q8(L["dq"][e], L["dd"][e], hd)
+            else:
+                hd = oracle.dequant_e4m3(hq[p:p + 1], hs[p:p + 1])[0]
+                y = oracle.expert_down(w["down"][e], hd)
+            ref_h[j] += ow[t, s] * y
+        # the shared row: int8 h vs the oracle's q8b of fp32(h), then its down
+        p = T * k + int(t)
+        qx, sx = oracle.quant_q8b(x[t])
+        xd = qx.astype(np.float64) * np.repeat(sx.astype(np.float64), 32)
+        hg = oracle.expert_h_q8(sq["sh_gate_q8"], sq["sh_gate_q8d"], sq["sh_up_q8"], sq["sh_up_q8d"], xd)
+        oq, od = oracle.quant_q8b(hg.astype(np.float32))
+        np.testing.assert_allclose(hsf[p], od, rtol=1e-4, atol=0)
+        bad = np.nonzero(hq[p].view(np.int8).astype(np.int64) != oq.astype(np.int64))[0]
+        if bad.size:
+            v = hg[bad] * 127.0 / np.repeat(np.abs(hg).reshape(-1, 32).max(axis=1), 32)[bad]
+            assert np.all(np.abs(np.abs(v - np.floor(v)) - 0.5) <= 127e-4), f"token {t}: shared codes {bad}"
+            flips += bad.size
+        hd = hq[p].view(np.int8).astype(np.float64) * np.repeat(hsf[p].astype(np.float64), 32)
+        ref_h[j] += oracle.expert_down_q8(sq["sh_down_q8"], sq["sh_down_q8d"], hd) / (1 + np.exp(-float(shg[t])))
+    el_h, norm_h = _row_err(y32[toks], ref_h)
+    ow_ = {"gate": w["gate"], "up": w["up"], **sq}
+    if which == "both":
+        ow_.update(down_q8=L["dq"], down_q8d=L["dd"])
+    else:
+        ow_["down"] = w["down"]
+    ref = oracle.moe_forward(ow_, x, lg, shg, tokens=toks.astype(np.int32))
+    _, e2e = _row_err(y32[toks], ref)
+    assert flips <= 0.01 * toks.size * 512
+    assert norm_h <= TOL and el_h <= TOL, f"down/combine error {norm_h:.3g} / {el_h:.3g}"
+    assert e2e <= 1e-2, f"end-to-end max relative error {e2e:.3g}"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("which", ["mx", "both"])
+@pytest.mark.parametrize("T,path", [(1, 0), (5, 2), (40, 4), (40, 1), (600, 0)])
+def test_forward_q8_shared(oracle, q8_shared_layer, which, T, path):
+    _check_shared_q8(oracle, q8_shared_layer, which, T, path, 500 + T + path)
+
+
+@pytest.mark.gpu
+def test_q8_shared_refusals(q8_shared_layer):
+    import torch
+    from q36_amd import moe
+    dw = q8_shared_layer["mx"]
+    rng = np.random.default_rng(510)
+    x = torch.from_numpy(synth.hidden(rng, 2)).cuda()
+    lg = torch.from_numpy(synth.normal_logits(rng, 2)).cuda()
+    shg = torch.from_numpy(rng.standard_normal(2).astype(np.float32)).cuda()
+    layer = moe.MoELayer(4)
+    xq, xs = moe.quant_e4m3(x)
+    with pytest.raises(moe.Q36MoEError):     # int8 x needs the unquantised input
+        layer.forward_q8(dw, xq, xs, lg, shg)
+    layer.forward_q8(dw, xq, xs, lg)          # without the shared expert it is fine
+    layer.set_path(3)
+    with pytest.raises(moe.Q36MoEError):
+        layer.forward(dw, x, lg, shg)
     torch.cuda.synchronize()
