@@ -600,3 +600,42 @@ def test_q8_shared_refusals(q8_shared_layer):
     with pytest.raises(moe.Q36MoEError):
         layer.forward(dw, x, lg, shg)
     torch.cuda.synchronize()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("T", [1, 40, 600])
+def test_q8_layer_in_hip_graph(q8_shared_layer, T):
+    """The release-file layout (Q6_K routed down, Q8_0 shared expert)
+    captured in a HIP graph: every replay, with eager forwards of other
+    inputs and synchronisations between, equals the eager result bit for bit
+    (direct, skinny and fat sorted paths)."""
+    import torch
+    from q36_amd import moe
+    dw = q8_shared_layer["both"]
+    rng = np.random.default_rng(1100 + T)
+    x = torch.from_numpy(synth.hidden(rng, T)).cuda()
+    lg = torch.from_numpy(synth.normal_logits(rng, T)).cuda()
+    shg = torch.from_numpy(rng.standard_normal(T).astype(np.float32)).cuda()
+    x2 = torch.from_numpy(synth.hidden(rng, T)).cuda()
+    lg2 = torch.from_numpy(synth.normal_logits(rng, T)).cuda()
+    layer = moe.MoELayer(T)
+    out = torch.empty((T, 2048), dtype=torch.float32, device="cuda")
+    ref = layer.forward(dw, x, lg, shg, out_dtype=torch.float32).clone()
+    cap = torch.cuda.Stream()
+    layer.set_stream(cap)
+    with torch.cuda.stream(cap):
+        layer.forward(dw, x, lg, shg, out=out)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=cap):
+        layer.forward(dw, x, lg, shg, out=out)
+    torch.cuda.synchronize()
+    layer.set_stream(torch.cuda.current_stream())
+    for rep in range(4):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"replay {rep}"
+        other = layer.forward(dw, x2, lg2, shg, out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        assert not torch.equal(other, ref)
