@@ -122,6 +122,10 @@ int q36moe_weights_shared_type(const q36moe_weights *w);
  * is the matrix size. */
 int q36moe_weights_alloc(int n_expert, int d_model, int d_ff, int d_ff_sh,
                          q36moe_weights **out);
+/* Device addresses of the packed matrices.  gate_bytes / down_bytes are one
+ * routed gate (= up) / down matrix, the per-expert stride; a shared matrix
+ * is gate_bytes in MXFP4, or d_model*d_ff*17/16 when
+ * q36moe_weights_shared_type gives Q8_0 (int8 codes + f16 per 32). */
 int q36moe_weights_device_ptrs(const q36moe_weights *w, void **gate, void **up,
                                void **down, void **sh_gate, void **sh_up,
                                void **sh_down, size_t *gate_bytes, size_t *down_bytes);

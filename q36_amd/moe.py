@@ -209,8 +209,8 @@ class MoEWeights:
         out = {"gate": (p[0].value, gb.value * E), "up": (p[1].value, gb.value * E),
                "down": (p[2].value, db.value * E)}
         if self.d_ff_sh:
-            out.update({"sh_gate": (p[3].value, gb.value), "sh_up": (p[4].value, gb.value),
-                        "sh_down": (p[5].value, db.value)})
+            sb = gb.value if self.shared_type == GGML_MXFP4 else self.d_model * self.d_ff * 17 // 16
+            out.update({"sh_gate": (p[3].value, sb), "sh_up": (p[4].value, sb), "sh_down": (p[5].value, sb)})
         return out
 
     def free(self):
