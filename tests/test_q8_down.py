@@ -76,6 +76,28 @@ def test_deq_matches_reference_build(oracle, ggml_type):
         np.testing.assert_array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
 
 
+@pytest.mark.parametrize("name,ggml_type", [("q8_0", Q8_0), ("q5_k", Q5_K), ("q6_k", Q6_K)])
+def test_deq_golden_fixture(oracle, name, ggml_type):
+    """The oracle against the reference's q36_deq_row outputs committed in
+    tests/golden/kquant_dequant_ref.npz (made by tests/golden/make_golden.py
+    from the reference's own header), bit for bit; holds where the
+    reference tree is absent."""
+    import os
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "kquant_dequant_ref.npz")
+    g = np.load(path)
+    blocks, want = g[name + "_blocks"], g[name + "_values"]
+    got = oracle.deq_row(ggml_type, blocks, want.size).reshape(want.shape)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+    # and the product's requantiser consumes exactly these values
+    from q36_amd import moe
+    elems = synth.KQUANT_BLOCK[ggml_type][0]
+    K = 256 if elems == 256 else 32
+    pc, ps = moe.requant_q8(ggml_type, blocks.reshape(-1, blocks.shape[1] * (K // elems)), blocks.shape[0] * elems // K, K)
+    oc, os_ = oracle.requant_q8(ggml_type, blocks.reshape(-1, blocks.shape[1] * (K // elems)), blocks.shape[0] * elems // K, K)
+    np.testing.assert_array_equal(pc, oc)
+    np.testing.assert_array_equal(ps, os_)
+
+
 def _f16(v):
     return np.frombuffer(np.float16(v).tobytes(), dtype=np.uint8)
 
