@@ -10,7 +10,7 @@ over --layers distinct seeded layers (40 x 428 MB = 17 GB by default) so the
 Workload (configs of the q36 MoE layer, hidden 2048, 256 experts, top-8,
 expert FF 512, MXFP4 weights, e4m3 activations with per-32 E8M0 scales):
   decode1      T=1, N(0,1) router logits (the headline configuration)
-  decode8      T=8, N(0,1) router logits (decode batch)
+  decode2/4/8/16  T=2/4/8/16, N(0,1) router logits (decode batches)
   decode32     T=32, N(0,1) router logits (decode batch)
   ragged64     T=64, Zipf(1.1) expert popularity
   prefill4096  T=4096, N(0,1) logits
@@ -48,7 +48,10 @@ Q8_MAT_BYTES = D * FF + D * FF // 16           # q8_0-split down matrix, 1,114,1
 
 CONFIGS = {
     "decode1": dict(T=1, shared=False, steps=2000, warmup=200),
+    "decode2": dict(T=2, shared=False, steps=2000, warmup=200),
+    "decode4": dict(T=4, shared=False, steps=2000, warmup=200),
     "decode8": dict(T=8, shared=False, steps=2000, warmup=200),
+    "decode16": dict(T=16, shared=False, steps=2000, warmup=200),
     "decode32": dict(T=32, shared=False, steps=1000, warmup=100),
     "ragged64": dict(T=64, shared=False, steps=1000, warmup=100),
     "prefill4096": dict(T=4096, shared=False, steps=100, warmup=10),

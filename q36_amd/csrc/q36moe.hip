@@ -66,6 +66,7 @@ constexpr int kRouteTPBSmall = 4;  // tokens per workgroup for small batches (T 
 constexpr int kRouteSmallT = 512;
 constexpr int kRouteD = 2048;     // d_model of k_route (the q36 shape, q36.h:78-84)
 constexpr int kDirectMaxT = 16;    // largest batch routed to the direct (unsorted) path
+constexpr int kDirect2Tiles = 8;   // direct gate/up: two row tiles per workgroup from this batch on
 
 // ---------------------------------------------------------------------------
 // scalar formats
@@ -1638,7 +1639,7 @@ struct DirectGateupLds {
     __align__(16) uint8_t sx[kDD + 32];   // + 32 zero bytes
     uint8_t sxs[kDD / 32];
     float sxf[kDD / 32];                  // int8 x scales (q8_0-split shared expert)
-    float red[4][2][16];
+    float red[4][2][32];                  // per wave: gate / up partial sums of up to 2 row tiles
     uint32_t rlds[4][kRouteLds];
 };
 
@@ -1719,13 +1720,19 @@ __device__ __forceinline__ void direct_shared_q8(const DirectArgs &A, int t, int
     }
 }
 
-template <bool FUSED, bool SHQ8 = false>
-__device__ __forceinline__ void direct_gateup_body(const DirectArgs &A, int i, int ft,
+// NFT row tiles ft0 .. ft0+NFT-1 per workgroup: one routing and NFT tiles'
+// weight loads in flight.  Measured (gate/up us, one tile / two): T=2 7.2 /
+// 7.5, T=4 9.8 / 10.0, T=8 16.5 / 15.5, T=16 27.4 / 25.6; four tiles at
+// T=16 25.7.
+template <bool FUSED, bool SHQ8 = false, int NFT = 1>
+__device__ __forceinline__ void direct_gateup_body(const DirectArgs &A, int i, int ft0,
                                                    DirectGateupLds &L_) {
+    static_assert(NFT == 1 || (NFT == 2 && !FUSED), "row tiles per workgroup");
     if constexpr (SHQ8) {   // workgroup-uniform: the shared expert's entries
         const int nr0 = A.T * A.k;
         if (i >= nr0) {
-            direct_shared_q8(A, i - nr0, i, ft, L_);
+#pragma unroll
+            for (int u = 0; u < NFT; u++) direct_shared_q8(A, i - nr0, i, ft0 + u, L_);
             return;
         }
     }
@@ -1760,16 +1767,20 @@ __device__ __forceinline__ void direct_gateup_body(const DirectArgs &A, int i, i
     const uint8_t *Wg = (e < A.E) ? A.gate + (size_t)e * A.wstride : A.sh_gate;
     const uint8_t *Wu = (e < A.E) ? A.up + (size_t)e * A.wstride : A.sh_up;
     const size_t nib = (size_t)kDF * kDD / 2;
-    uint4 ag[4], au[4];
+    uint4 ag[NFT][4], au[NFT][4];
+    int sag[NFT], sau[NFT];
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const size_t o = ((size_t)ft * (kDD / 128) + wave * 4 + j) * 1024 + (size_t)lane * 16;
-        ag[j] = *reinterpret_cast<const uint4 *>(Wg + o);
-        au[j] = *reinterpret_cast<const uint4 *>(Wu + o);
+    for (int u = 0; u < NFT; u++) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const size_t o = ((size_t)(ft0 + u) * (kDD / 128) + wave * 4 + j) * 1024 + (size_t)lane * 16;
+            ag[u][j] = *reinterpret_cast<const uint4 *>(Wg + o);
+            au[u][j] = *reinterpret_cast<const uint4 *>(Wu + o);
+        }
+        const size_t so = nib + ((size_t)(ft0 + u) * 64 + lane) * (kDD / 128) + wave * 4;
+        sag[u] = *reinterpret_cast<const int *>(Wg + so);
+        sau[u] = *reinterpret_cast<const int *>(Wu + so);
     }
-    const size_t so = nib + ((size_t)ft * 64 + lane) * (kDD / 128) + wave * 4;
-    const int sag = *reinterpret_cast<const int *>(Wg + so);
-    const int sau = *reinterpret_cast<const int *>(Wu + so);
 
     if (A.x_fmt == kFmtE4M3) {
         *reinterpret_cast<uint2 *>(sx + wave * 512 + lane * 8) = make_uint2(xr.a[0], xr.a[1]);
@@ -1787,7 +1798,9 @@ __device__ __forceinline__ void direct_gateup_body(const DirectArgs &A, int i, i
     // B fragment: column 0 is the token; lanes of other columns read zeros
     const int q = lane >> 4;
     const bool col0 = (lane & 15) == 0;
-    v4f cg = {0.f, 0.f, 0.f, 0.f}, cu = {0.f, 0.f, 0.f, 0.f};
+    v4f cg[NFT], cu[NFT];
+#pragma unroll
+    for (int u = 0; u < NFT; u++) cg[u] = cu[u] = v4f{0.f, 0.f, 0.f, 0.f};
     static_for<0, 4>([&](auto J) {
         constexpr int j = decltype(J)::value;
         const int kt = wave * 4 + j;
@@ -1798,28 +1811,34 @@ __device__ __forceinline__ void direct_gateup_body(const DirectArgs &A, int i, i
         const v8i b = v8i{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w,
                           (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
         const int sb = sxs[kt * 4 + q];
-        const v8i a0 = v8i{(int)ag[j].x, (int)ag[j].y, (int)ag[j].z, (int)ag[j].w, 0, 0, 0, 0};
-        const v8i a1 = v8i{(int)au[j].x, (int)au[j].y, (int)au[j].z, (int)au[j].w, 0, 0, 0, 0};
-        cg = mfma_f4xf8<j>(a0, b, cg, sag, sb);
-        cu = mfma_f4xf8<j>(a1, b, cu, sau, sb);
+#pragma unroll
+        for (int u = 0; u < NFT; u++) {
+            const v8i a0 = v8i{(int)ag[u][j].x, (int)ag[u][j].y, (int)ag[u][j].z, (int)ag[u][j].w, 0, 0, 0, 0};
+            const v8i a1 = v8i{(int)au[u][j].x, (int)au[u][j].y, (int)au[u][j].z, (int)au[u][j].w, 0, 0, 0, 0};
+            cg[u] = mfma_f4xf8<j>(a0, b, cg[u], sag[u], sb);
+            cu[u] = mfma_f4xf8<j>(a1, b, cu[u], sau[u], sb);
+        }
     });
     Q36_TRACE_AT(4);
     if (col0) {
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            red[wave][0][4 * q + r] = cg[r];
-            red[wave][1][4 * q + r] = cu[r];
-        }
+        for (int u = 0; u < NFT; u++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                red[wave][0][16 * u + 4 * q + r] = cg[u][r];
+                red[wave][1][16 * u + 4 * q + r] = cu[u][r];
+            }
     }
     __syncthreads();
-    if (wave == 0 && lane < 16) {
+    if (wave == 0 && lane < 16 * NFT) {
+        const int ft = ft0 + (lane >> 4), lr = lane & 15;
         const float g = red[0][0][lane] + red[1][0][lane] + red[2][0][lane] + red[3][0][lane];
         const float u = red[0][1][lane] + red[1][1][lane] + red[2][1][lane] + red[3][1][lane];
         if constexpr (FUSED) {
             // publish without an L2-wide release fence: the row goes out as a
             // device-scope store (written through to the coherence point), the
             // wave waits for its completion, then counts this workgroup in
-            __hip_atomic_store(&A.hf[(size_t)i * kDF + ft * 16 + lane], silu(g) * u,
+            __hip_atomic_store(&A.hf[(size_t)i * kDF + ft * 16 + lr], silu(g) * u,
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __builtin_amdgcn_s_waitcnt(0);
             // system scope: the add is performed at the coherence point, where
@@ -1828,12 +1847,12 @@ __device__ __forceinline__ void direct_gateup_body(const DirectArgs &A, int i, i
             if (lane == 0)
                 __hip_atomic_fetch_add(&A.arrive[t], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         } else {
-            A.hf[(size_t)i * kDF + ft * 16 + lane] = silu(g) * u;
+            A.hf[(size_t)i * kDF + ft * 16 + lr] = silu(g) * u;
         }
     }
     Q36_TRACE_AT(5);
     Q36_TRACE_WG(1);
-    if (ft == 0) {
+    if (ft0 == 0) {
         if (threadIdx.x == 0 && routed) {
             A.idx[i] = e;
             A.wt[i] = wgt;
@@ -1849,10 +1868,10 @@ __device__ __forceinline__ void direct_gateup_body(const DirectArgs &A, int i, i
     }
 }
 
-template <bool SHQ8>
+template <bool SHQ8, int NFT>
 __global__ __launch_bounds__(256) void k_direct_gateup(DirectArgs A) {
     __shared__ DirectGateupLds L_;
-    direct_gateup_body<false, SHQ8>(A, blockIdx.x, blockIdx.y, L_);
+    direct_gateup_body<false, SHQ8, NFT>(A, blockIdx.x, blockIdx.y * NFT, L_);
 }
 
 // Token t x 16 output rows; wave s handles slot s (wave k: shared expert):
@@ -2574,10 +2593,20 @@ static void launch_stage(const q36moe_ctx *c, const Plan &P, int st, hipStream_t
             if (st == ST_GATEUP)
                 hipLaunchKernelGGL(k_decode_fused, dim3(P.di.n_gateup_wg + T * (D / 16)), dim3(256), 0, s, P.di);
         } else if (st == ST_GATEUP) {
-            if (P.di.sh_q8)
-                hipLaunchKernelGGL(k_direct_gateup<true>, dim3(n, FF / 16), dim3(256), 0, s, P.di);
-            else
-                hipLaunchKernelGGL(k_direct_gateup<false>, dim3(n, FF / 16), dim3(256), 0, s, P.di);
+            // two row tiles per workgroup from kDirect2Tiles tokens on (one
+            // routing and twice the loads in flight per workgroup; below
+            // that, more workgroups spread a small batch better)
+            if (T >= kDirect2Tiles) {
+                if (P.di.sh_q8)
+                    hipLaunchKernelGGL((k_direct_gateup<true, 2>), dim3(n, FF / 32), dim3(256), 0, s, P.di);
+                else
+                    hipLaunchKernelGGL((k_direct_gateup<false, 2>), dim3(n, FF / 32), dim3(256), 0, s, P.di);
+            } else {
+                if (P.di.sh_q8)
+                    hipLaunchKernelGGL((k_direct_gateup<true, 1>), dim3(n, FF / 16), dim3(256), 0, s, P.di);
+                else
+                    hipLaunchKernelGGL((k_direct_gateup<false, 1>), dim3(n, FF / 16), dim3(256), 0, s, P.di);
+            }
         } else if (st == ST_DOWN) {
             if (P.di.dn_q8 || P.di.sh_q8)
                 hipLaunchKernelGGL(k_direct_down<true>, dim3(D / 16, T), dim3(64 * (K + P.has_sh)), 0, s, P.di);
