@@ -74,7 +74,9 @@ uint8_t or_e4m3_encode(float v) {
     uint32_t u; memcpy(&u, &v, 4);
     uint8_t sign = (uint8_t)((u >> 31) << 7);
     uint32_t a = u & 0x7fffffffu;
-    if (a > 0x7f800000u) return sign | 0x7f;
+    /* NaN -> 0x7f whatever its sign: a NaN computed from inf * 0 has a
+     * platform-dependent sign bit */
+    if (a > 0x7f800000u) return 0x7f;
     if (a >= 0x43e00000u) return sign | 0x7e;          /* >= 448 */
     if (a < 0x3c800000u) {                            /* < 2^-6: subnormal */
         float f; memcpy(&f, &a, 4);
@@ -98,6 +100,9 @@ uint8_t or_e4m3_encode(float v) {
  * differs by one scale step and is pinned in tests). */
 int or_quant_exp(float amax) {
     if (!(amax > 0.0f)) return -127;
+    /* an infinite amax: ceil(log2(inf)) converts to the largest int in the
+     * reference's saturating float-to-int conversion, then clamps to 127 */
+    if (amax > 3.40282347e38f) return 127;
     float q = amax / 448.0f;
     int ex;
     float f = frexpf(q, &ex);                         /* q = f*2^ex, f in [.5,1) */

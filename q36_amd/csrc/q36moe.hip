@@ -72,12 +72,13 @@ constexpr int kDirect2Tiles = 8;   // direct gate/up: two row tiles per workgrou
 // scalar formats
 // ---------------------------------------------------------------------------
 
-// OCP E4M3FN, round-to-nearest-even, saturating at +-448, NaN -> 0x7f.
+// OCP E4M3FN, round-to-nearest-even, saturating at +-448, NaN -> 0x7f
+// (whatever its sign).
 __device__ __forceinline__ uint32_t e4m3_encode(float v) {
     const uint32_t u = __float_as_uint(v);
     const uint32_t sign = (u >> 24) & 0x80u;
     const uint32_t a = u & 0x7fffffffu;
-    if (a > 0x7f800000u) return sign | 0x7fu;
+    if (a > 0x7f800000u) return 0x7fu;
     if (a >= 0x43e00000u) return sign | 0x7eu;
     if (a < 0x3c800000u) {
         const float q = __builtin_rintf(__uint_as_float(a) * 512.0f);
@@ -110,6 +111,10 @@ __device__ __forceinline__ uint32_t e4m3x4(float a, float b, float c, float d) {
 // clamped to [-127, 127]; -127 for an all-zero block.
 __device__ __forceinline__ int quant_exp(float amax) {
     if (!(amax > 0.0f)) return -127;
+    // an infinite amax: the reference's ceil(log2(inf)) saturates in its
+    // float-to-int conversion and clamps to 127 (scale 0: finite codes 0,
+    // the infinite element NaN)
+    if (amax > 3.40282347e38f) return 127;
     const float q = amax / 448.0f;
     int ex;
     const float f = frexpf(q, &ex);

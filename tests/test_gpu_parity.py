@@ -143,6 +143,14 @@ def _quant_inputs(rng):
     mids = ((fin[:-1] + fin[1:]) / 2).astype(np.float32)
     x[3, :] = np.resize(np.concatenate([[448.0], mids]), 2048)
     x[3, ::32] = 448.0
+    # non-finite values: +-inf blocks (scale byte 254, finite codes 0, the
+    # infinite element NaN as the reference's saturating conversion gives),
+    # NaN elements (ignored by the block maximum, coded 0x7f)
+    x[4, 5] = np.inf
+    x[4, 40] = -np.inf
+    x[5, 7] = np.nan
+    x[5, 100] = -np.nan
+    x[6, :32] = np.float32(3.0e38)
     return x
 
 

@@ -139,6 +139,14 @@ def test_e4m3_encode_roundtrip_and_ties(oracle):
         assert oracle.e4m3_encode(np.nextafter(mid, np.float32(-1e9))) == b
 
 
+def test_quant_exp_infinite_amax(oracle):
+    # ceil(log2(inf / 448)) saturates to the largest int, clamped to 127
+    assert oracle.quant_exp(float("inf")) == 127
+    xq, xs = oracle.quant_e4m3(np.array([[1.0, np.inf] + [0.5] * 30], dtype=np.float32))
+    assert xs[0, 0] == 254
+    assert xq[0, 0] == 0 and xq[0, 1] == 0x7F and np.all(xq[0, 2:] == 0)
+
+
 def test_e4m3_encode_saturation_nan(oracle):
     for v in (448.0, 449.0, 463.9, 464.0, 480.0, 1e6, float("inf")):
         assert oracle.e4m3_encode(v) == 0x7E
