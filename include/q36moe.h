@@ -63,7 +63,8 @@ extern "C" {
 #define Q36MOE_TAP_EOFF      4  /* int32 [n_expert+1] sorted offsets    */
 #define Q36MOE_TAP_PERM      5  /* int32 [T*k] entry id per sorted slot */
 #define Q36MOE_TAP_POS       6  /* int32 [T*k] sorted slot per entry    */
-#define Q36MOE_TAP_HQ        7  /* u8    [T*k+T][d_ff] e4m3 SwiGLU rows */
+#define Q36MOE_TAP_HQ        7  /* u8    [T*k+T][d_ff] e4m3 SwiGLU rows
+                                   (int8 for q8_0-split down matrices)  */
 #define Q36MOE_TAP_HS        8  /* u8    [T*k+T][d_ff/32] E8M0          */
 #define Q36MOE_TAP_DNW       9  /* f32   [T*k+T][d_model] w * down rows */
 #define Q36MOE_TAP_HSF      10  /* f32   [T*k+T][d_ff/32] int8 h scales
@@ -170,6 +171,8 @@ void q36moe_ctx_free(q36moe_ctx *c);
  * out[t] = sum_s w[t][s] * E_{idx[t][s]}(x[t]) + sigmoid(shg[t]) * S(x[t]),
  * E(x) = down . q8(silu(gate . q8(x)) * up . q8(x)), q8 = per-32 E8M0 +
  * e4m3 quantisation, w = top-k softmax weights renormalised, times scale.
+ * A matrix uploaded in the q8_0-split layout (q36moe_weights_upload_typed)
+ * takes its activation quantised per 32 to int8 + fp32 scale instead.
  * Asynchronous on the context stream; T = 0 is a no-op. */
 int q36moe_forward(q36moe_ctx *c, const q36moe_weights *w,
                    const void *x, int x_fmt, const float *logits, int ld_logits,
@@ -205,7 +208,8 @@ int q36moe_add_rmsnorm_quant(float *h, const float *a, const float *w, int T, in
  * q36moe_add_rmsnorm_quant (or q36moe_quant_e4m3): xq [T][d_model] e4m3,
  * xs [T][d_model/32] E8M0, device pointers that must stay valid until the
  * forward has run (and while its XQ/XS taps are read).  Same result as
- * q36moe_forward on the x they were quantised from. */
+ * q36moe_forward on the x they were quantised from.  EINVAL with shg for a
+ * q8_0-split shared expert (it quantises the unquantised x itself). */
 int q36moe_forward_q8(q36moe_ctx *c, const q36moe_weights *w, const uint8_t *xq, const uint8_t *xs,
                       const float *logits, int ld_logits, const float *shg, int T, float scale,
                       void *out, int out_fmt);
@@ -250,7 +254,9 @@ int q36moe_num_stages(void);
  * with the weights w.  Bracketing many replays over rotating weight sets
  * with two events gives a kernel's average duration without per-launch
  * event overhead.  The stage's outputs are rewritten; call forward again
- * before reading results.  No counterpart in the reference (profiling aid). */
+ * before reading results.  w must have the formats (MXFP4 / q8_0-split
+ * down and shared expert) of the last forward's weights, else EINVAL.  No
+ * counterpart in the reference (profiling aid). */
 int q36moe_ctx_replay(q36moe_ctx *c, const q36moe_weights *w, int stage);
 
 /* GGUF v3 ingest (replaces gguf_open, gguf.c, and bind_moe + upload,
