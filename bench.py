@@ -149,18 +149,20 @@ def measured_traffic(config, stage):
     return None
 
 
-def cpu_baseline(cfg_name, T, seconds, shared):
-    """The C oracle's fp32 layer forward on host cores over a bounded sample
-    of tokens of the same configuration."""
-    from oracle import pyoracle
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _layer_tokens_per_s(pyoracle, w, cfg_name, T, shared, seconds, nth, seed):
     from q36_amd import synth
-    pyoracle.lib()
-    nth = len(os.sched_getaffinity(0))
-    w = synth.expert_weights(7, shared=shared)
-    rng = np.random.default_rng(8)
-    n = 0
-    t0 = time.perf_counter()
-    tokens = 0
+    rng = np.random.default_rng(seed)
+    busy, tokens, t0 = 0.0, 0, time.perf_counter()
     while time.perf_counter() - t0 < seconds:
         Tb = min(T, 4)
         x = synth.hidden(rng, Tb)
@@ -168,11 +170,61 @@ def cpu_baseline(cfg_name, T, seconds, shared):
         shg = rng.standard_normal(Tb).astype(np.float32) if shared else None
         t1 = time.perf_counter()
         pyoracle.moe_forward_f32(w, x, lg, shg, nthreads=nth)
-        n += time.perf_counter() - t1
+        busy += time.perf_counter() - t1
         tokens += Tb
-    return {"value": tokens / n, "unit": "tokens/s", "cores": nth, "kind": "port",
+    return tokens / busy, tokens, busy
+
+
+def _gemv_config0(pyoracle, nth, seconds):
+    """one 512x2048 MXFP4 matrix times one e4m3 vector
+    (dequant + GEMV, fp32 accumulation), through the oracle port; and the
+    reference's own q36_deq_row (built from its sources into oracle/_ref)
+    timed on the same blocks for the dequant alone, where it is present."""
+    from q36_amd import synth
+    rng = np.random.default_rng(9)
+    W = synth.mxfp4_blocks(rng, 512, 2048)
+    xq, xs = pyoracle.quant_e4m3(synth.hidden(rng, 1))
+    out = {}
+    for threads in (1, nth):
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < seconds:
+            pyoracle.gemv_mxfp4(W, xq, xs, nthreads=threads)
+            n += 1
+        out[f"port_gemv_us_{threads}t"] = (time.perf_counter() - t0) / n * 1e6
+    ref = pyoracle.ref_lib()
+    if ref is not None:
+        import ctypes
+        buf = np.ascontiguousarray(W.reshape(-1))
+        row = np.empty(2048, dtype=np.float32)
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < seconds:
+            for r in range(512):
+                ref.ref_deq_row(39, ctypes.c_void_p(buf.ctypes.data + r * 64 * 17), 2048,
+                                ctypes.c_void_p(row.ctypes.data))
+            n += 1
+        out["reference_dequant_us_1t"] = (time.perf_counter() - t0) / n * 1e6
+    return out
+
+
+def cpu_baseline(cfg_name, T, seconds, shared):
+    """The C oracle's fp32 layer forward on host cores over a bounded sample
+    of tokens of the same configuration (OpenMP over the host's cores, and
+    a shorter single-threaded sample), plus BASELINE config 0 (the CPU
+    dequant + GEMV of one expert matrix)."""
+    from oracle import pyoracle
+    from q36_amd import synth
+    pyoracle.lib()
+    nth = len(os.sched_getaffinity(0))
+    w = synth.expert_weights(7, shared=shared)
+    value, tokens, busy = _layer_tokens_per_s(pyoracle, w, cfg_name, T, shared, seconds, nth, 8)
+    single, tok1, busy1 = _layer_tokens_per_s(pyoracle, w, cfg_name, T, shared, seconds / 4, 1, 18)
+    return {"value": value, "unit": "tokens/s", "cores": nth, "kind": "port",
             "sample": f"{tokens} tokens of {cfg_name} (batches of <=4) through or_moe_forward_f32, "
-                      f"{n:.1f} s, OpenMP {nth} threads"}
+                      f"{busy:.1f} s, OpenMP {nth} threads",
+            "single_thread": {"value": single, "unit": "tokens/s", "cores": 1,
+                              "sample": f"{tok1} tokens, {busy1:.1f} s"},
+            "cpu_model": _cpu_model(),
+            "config0_gemv": _gemv_config0(pyoracle, nth, 1.0)}
 
 
 def main():
