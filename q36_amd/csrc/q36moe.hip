@@ -1,23 +1,33 @@
 // q36moe: W4A8 (MXFP4 weight x FP8-e4m3 activation) mixture-of-experts
 // layer for MI355X (gfx950).  Kernels + the C ABI declared in q36moe.h.
 //
-// Pipeline of one forward (all on the context stream, no host syncs):
-//   k_route    one wavefront per token: softmax top-k + renormalised weights
-//              (q36_ops.cuh:397-431), FP8 quantisation of x with per-32
-//              E8M0 scales (q36_engine.cu:2411-2428), and per-block expert
-//              histograms + in-block ranks for the sort.
-//   k_scan     one workgroup: per-expert offsets (exclusive scans in LDS),
-//              a stable scatter of entry ids t*k+s by expert (the
-//              deterministic replacement of k_moe_dispatch,
-//              q36_engine.cu:3387-3392) and the ragged tile list.
-//   k_expert_gemm<GATEUP>  gate and up rows of one expert x one token tile on
-//              v_mfma_scale_f32_16x16x128_f8f6f4 (E2M1 weights straight from
-//              HBM in fragment order, e4m3 activations staged in LDS), fused
-//              SwiGLU and FP8 re-quantisation of h (q36_engine.cu:3436-3450).
-//   k_expert_gemm<DOWN>    down rows x token tile, scaled by the routing
-//              weight (q36_engine.cu:3451-3463).
-//   k_combine  out[t] = sum_s (w*down)[t,s] + (sigmoid(shg)*shared)[t] in slot
-//              order, bf16 or f32 (q36_engine.cu:784-791, :3393-3401).
+// One forward runs on the context stream with no host synchronisation.
+// Direct path (decode, T <= 16):
+//   k_direct_gateup  (entry, 16 or 32 rows): every wave routes the token
+//              (softmax top-k, q36_ops.cuh:397-431), quantises its quarter of
+//              x (per-32 E8M0 + e4m3, q36_engine.cu:2411-2428), gate and up on
+//              v_mfma_scale_f32_16x16x128_f8f6f4, SwiGLU rows in fp32.
+//   k_direct_down    (token, 16 output rows): a wave per slot quantises its h
+//              row and multiplies it by the down tile; the slots are summed in
+//              slot order with the gated shared expert (q36_engine.cu:784-791).
+// Sorted path (any T):
+//   k_route    routing + x quantisation per token, per-block expert counts
+//              and in-block ranks; k_colscan / k_scatter: the stable counting
+//              sort (the deterministic k_moe_dispatch, q36_engine.cu:3387-3392)
+//              and the ragged tile list.
+//   k_skinny_gateup (tiles <= 32 rows) or k_gateup_dma (<= 160 rows, A and B
+//              staged in LDS by direct-to-LDS loads): gate/up + SwiGLU +
+//              quantisation of h in sorted order (q36_engine.cu:3436-3450).
+//   k_down_lds down rows x staged h, scaled by the routing weight
+//              (q36_engine.cu:3451-3463); k_combine: the weighted sum back in
+//              token order (q36_engine.cu:3393-3401).
+// q8_0-split matrices (the reference's requantised k-quant experts and its
+// Q8_0 shared expert) run on int8 MFMA with per-32 scales: down_q8_tile in
+// k_down_lds<true>, the Q8 branches of k_direct_down<true> and
+// k_direct_gateup<true, *>, and the shared gate/up body (k_shared_gateup_q8,
+// or the leading workgroups of k_gateup_dma).  In front of the boundary:
+// k_router_f32 / k_router_f16 (router logits) and k_add_rmsnorm_quant (the
+// residual + RMSNorm + quantisation producer).
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
