@@ -245,7 +245,25 @@ def main():
         for _ in range(4):
             dst.copy_(src)
         torch.cuda.synchronize()
-        print(json.dumps({"copy_bytes": n, "launches": 4}))
+        # achievable-bandwidth reference points: the copy (read + write) and a
+        # read-only reduction over the same bytes, as f32
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+        f = src.view(torch.float32)
+        f.sum()
+        ev[0].record()
+        for _ in range(10):
+            dst.copy_(src)
+        ev[1].record()
+        ev[2].record()
+        for _ in range(10):
+            f.sum()
+        ev[3].record()
+        torch.cuda.synchronize()
+        copy_us = ev[0].elapsed_time(ev[1]) * 100.0
+        read_us = ev[2].elapsed_time(ev[3]) * 100.0
+        print(json.dumps({"copy_bytes": n, "launches": 4,
+                          "copy_us": copy_us, "copy_gbs": 2 * n / copy_us / 1e3,
+                          "read_us": read_us, "read_gbs": n / read_us / 1e3}))
         return
 
     cfg = CONFIGS[args.config]
