@@ -343,6 +343,23 @@ def test_forward_decode1(dev, oracle, layer_w, path):
     _check_layer("decode1", dev, oracle, layer_w, x, lg, None, path=path)
 
 
+# Batch sizes between the named configurations, each on a forced path (0 =
+# the automatic choice), with Zipf routing on every other case and the
+# shared expert on some: (T, path, zipf, shared).
+SWEEP = [(3, 2, False, True), (9, 4, True, False), (17, 0, False, False), (31, 1, True, True),
+         (100, 4, False, True), (257, 0, True, False), (1000, 1, False, False), (2049, 0, True, True)]
+
+
+@pytest.mark.parametrize("T,path,zipf,shared", SWEEP, ids=[f"T{c[0]}_p{c[1]}" for c in SWEEP])
+def test_forward_batch_sweep(dev, oracle, layer_w, T, path, zipf, shared):
+    rng = np.random.default_rng(700 + T)
+    x = synth.hidden(rng, T)
+    lg = synth.zipf_logits(rng, T) if zipf else synth.normal_logits(rng, T)
+    shg = rng.standard_normal(T).astype(np.float32) if shared else None
+    sample = None if T <= 32 else np.sort(rng.choice(T, size=24, replace=False))
+    _check_layer(f"sweep{T}", dev, oracle, layer_w, x, lg, shg, sample=sample, path=path)
+
+
 @pytest.mark.parametrize("path", PATHS)
 @pytest.mark.parametrize("T", [2, 7, 16])
 def test_forward_small_batches(dev, oracle, layer_w, T, path):
