@@ -460,6 +460,18 @@ __device__ __forceinline__ uint32_t q8b4(float a, float b, float c, float d, flo
 __device__ __forceinline__ float f16lo(uint32_t d) { return (float)__builtin_bit_cast(_Float16, (uint16_t)d); }
 __device__ __forceinline__ float f16hi(uint32_t d) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(d >> 16)); }
 
+// Scaling an int8 block result without an integer-to-float convert: the
+// MFMA accumulates onto kQ8Bias (the fp32 bits of 1.5 * 2^23), so its i32
+// result r = kQ8Bias + ci reads as the fp32 value 12582912 + ci exactly
+// (|ci| <= 32 * 128 * 128 < 2^22).  A weight scale w is an f16 value, so
+// 12582912 * w is exact in fp32 and fma(r, w, -12582912 * w) = round(ci * w),
+// one rounding, as convert-then-multiply has.  The block then costs two fmas
+// per output (this and the one applying the activation scale) once
+// -12582912 * w is at hand.
+constexpr int kQ8Bias = 0x4B400000;
+constexpr float kQ8BiasF = 12582912.0f;
+__device__ __forceinline__ float q8_scaled(int r, float w, float nwb) { return fmaf(__int_as_float(r), w, nwb); }
+
 struct RouteArgs {
     const float *logits; int ld; int T; int E; int k; float scale;
     const void *x; int x_fmt; int D; int nb;
@@ -1049,16 +1061,17 @@ __device__ __forceinline__ void shared_gateup_q8_body(const GemmArgs &A, int tb,
             for (int a = 0; a < 4; a++) {
                 const long av = (long)(((uint64_t)cur.af[a][2 * h + 1] << 32) | cur.af[a][2 * h]);
                 const uint32_t s01 = cur.sf[a][2 * h], s23 = cur.sf[a][2 * h + 1];
-                const float w0 = f16lo(s01), w1 = f16hi(s01), w2 = f16lo(s23), w3 = f16hi(s23);
+                const float w[4] = {f16lo(s01), f16hi(s01), f16lo(s23), f16hi(s23)};
+                float nw[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) nw[i] = -kQ8BiasF * w[i];
 #pragma unroll
                 for (int j = 0; j < kShCt; j++) {
                     const long b = (long)(((uint64_t)cur.bx[j][h].y << 32) | cur.bx[j][h].x);
-                    const v4i ci = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, b, v4i{0, 0, 0, 0}, 0, 0, 0);
+                    const v4i ci = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, b, v4i{kQ8Bias, kQ8Bias, kQ8Bias, kQ8Bias}, 0, 0, 0);
                     const float dhh = h ? cur.dh[j].y : cur.dh[j].x;
-                    acc[a][j][0] += (float)ci[0] * (w0 * dhh);
-                    acc[a][j][1] += (float)ci[1] * (w1 * dhh);
-                    acc[a][j][2] += (float)ci[2] * (w2 * dhh);
-                    acc[a][j][3] += (float)ci[3] * (w3 * dhh);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) acc[a][j][i] = fmaf(q8_scaled(ci[i], w[i], nw[i]), dhh, acc[a][j][i]);
                 }
             }
         cur = nxt;
@@ -1441,11 +1454,11 @@ constexpr int kDlSfStride = 20;
 // scales against int8 weights with f16 scales.  Each 32-block is one
 // v_mfma_i32_16x16x32_i8 whose exact integer result is scaled by the
 // weight row's f16 scale times the h row's fp32 scale and accumulated in
-// fp32.  The wave's 4 row tiles run as 4 passes over the staged B (codes
-// and fp32 scales of one row tile are 96 VGPRs); B is staged once per chunk,
-// as in the MXFP4 body.  The kernel is VALU-bound (per block and output a
-// convert, a scale product and an fma), so every pass is software-pipelined
-// by one block.
+// fp32 (two fmas per output and block, q8_scaled).  The wave's 4 row tiles
+// run as 4 passes over the staged B (codes and fp32 scales of one row tile
+// are 160 VGPRs); B is staged once per chunk, as in the MXFP4 body.  Each
+// pass is software-pipelined by one block: a block's scaling overlaps the
+// next block's MFMA.
 __device__ __forceinline__ void down_q8_tile(const GemmArgs &A, const uint8_t *W, int p0, int p1, int rb, uint8_t *sb,
                                              float (*ssf)[kDlSfStride], float *ws) {
     constexpr int KD = 512, NKP = KD / 64, NKB = KD / 32;
@@ -1470,6 +1483,7 @@ __device__ __forceinline__ void down_q8_tile(const GemmArgs &A, const uint8_t *W
             const int mt = mt0 + ps;
             u32x4 ac[NKP];
             float dw[NKB][4];   // f16 scales of rows 4q..4q+3, widened once per pass
+            float ndw[NKB][4];  // -12582912 * dw (exact)
 #pragma unroll
             for (int kp = 0; kp < NKP; kp++) {
                 ac[kp] = *reinterpret_cast<const u32x4 *>(W + ((size_t)mt * NKP + kp) * 1024 + lane * 16);
@@ -1480,6 +1494,8 @@ __device__ __forceinline__ void down_q8_tile(const GemmArgs &A, const uint8_t *W
                     dw[2 * kp + h][1] = f16hi(sv[2 * h]);
                     dw[2 * kp + h][2] = f16lo(sv[2 * h + 1]);
                     dw[2 * kp + h][3] = f16hi(sv[2 * h + 1]);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) ndw[2 * kp + h][i] = -kQ8BiasF * dw[2 * kp + h][i];
                 }
             }
             for (int j = 0; j < ntt; j++) {
@@ -1505,10 +1521,11 @@ __device__ __forceinline__ void down_q8_tile(const GemmArgs &A, const uint8_t *W
                     const long b = (long)(((uint64_t)bv[kb].y << 32) | bv[kb].x);
                     const u32x4 f = ac[kb >> 1];
                     const long a = (kb & 1) ? (long)(((uint64_t)f[3] << 32) | f[2]) : (long)(((uint64_t)f[1] << 32) | f[0]);
-                    const v4i ci = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, v4i{0, 0, 0, 0}, 0, 0, 0);
+                    const v4i ci = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, v4i{kQ8Bias, kQ8Bias, kQ8Bias, kQ8Bias}, 0, 0, 0);
                     if (kb > 0) {   // the previous block, while this one's MFMA runs
 #pragma unroll
-                        for (int i = 0; i < 4; i++) acc[i] += (float)prev[i] * (dw[kb - 1][i] * dh[kb - 1]);
+                        for (int i = 0; i < 4; i++)
+                            acc[i] = fmaf(q8_scaled(prev[i], dw[kb - 1][i], ndw[kb - 1][i]), dh[kb - 1], acc[i]);
                     }
                     prev = ci;
                     // one block per scheduling group: left alone, the compiler
@@ -1517,7 +1534,8 @@ __device__ __forceinline__ void down_q8_tile(const GemmArgs &A, const uint8_t *W
                     __builtin_amdgcn_sched_barrier(0);
                 }
 #pragma unroll
-                for (int i = 0; i < 4; i++) acc[i] += (float)prev[i] * (dw[NKB - 1][i] * dh[NKB - 1]);
+                for (int i = 0; i < 4; i++)
+                    acc[i] = fmaf(q8_scaled(prev[i], dw[NKB - 1][i], ndw[NKB - 1][i]), dh[NKB - 1], acc[i]);
                 if (j * 16 + n < nr) {
                     const int p = c0 + j * 16 + n;
                     const float w = ws[j * 16 + n];
@@ -1707,14 +1725,18 @@ __device__ __forceinline__ void direct_shared_q8(const DirectArgs &A, int t, int
             const float dh = sxf[kb];
             const long a0 = (long)(((uint64_t)ag[u][2 * h + 1] << 32) | ag[u][2 * h]);
             const long a1 = (long)(((uint64_t)au[u][2 * h + 1] << 32) | au[u][2 * h]);
-            const v4i gi = __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, b, v4i{0, 0, 0, 0}, 0, 0, 0);
-            const v4i ui = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, b, v4i{0, 0, 0, 0}, 0, 0, 0);
+            const v4i bias = {kQ8Bias, kQ8Bias, kQ8Bias, kQ8Bias};
+            const v4i gi = __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, b, bias, 0, 0, 0);
+            const v4i ui = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, b, bias, 0, 0, 0);
             const uint32_t g01 = sg[u][2 * h], g23 = sg[u][2 * h + 1];
             const uint32_t u01 = su[u][2 * h], u23 = su[u][2 * h + 1];
-            cg[0] += (float)gi[0] * (f16lo(g01) * dh); cg[1] += (float)gi[1] * (f16hi(g01) * dh);
-            cg[2] += (float)gi[2] * (f16lo(g23) * dh); cg[3] += (float)gi[3] * (f16hi(g23) * dh);
-            cu[0] += (float)ui[0] * (f16lo(u01) * dh); cu[1] += (float)ui[1] * (f16hi(u01) * dh);
-            cu[2] += (float)ui[2] * (f16lo(u23) * dh); cu[3] += (float)ui[3] * (f16hi(u23) * dh);
+            const float wg[4] = {f16lo(g01), f16hi(g01), f16lo(g23), f16hi(g23)};
+            const float wu[4] = {f16lo(u01), f16hi(u01), f16lo(u23), f16hi(u23)};
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                cg[r] = fmaf(q8_scaled(gi[r], wg[r], -kQ8BiasF * wg[r]), dh, cg[r]);
+                cu[r] = fmaf(q8_scaled(ui[r], wu[r], -kQ8BiasF * wu[r]), dh, cu[r]);
+            }
             // one block per scheduling group (otherwise all 32 MFMA results
             // are held at once)
             asm volatile("" : "+v"(cg), "+v"(cu));
@@ -1967,14 +1989,13 @@ __global__ __launch_bounds__(576) void k_direct_down(DirectArgs A) {
             const long b = (long)(((uint64_t)bv.y << 32) | bv.x);
             const u32x4 f = ac[kb >> 1];
             const long av = (kb & 1) ? (long)(((uint64_t)f[3] << 32) | f[2]) : (long)(((uint64_t)f[1] << 32) | f[0]);
-            const v4i ci = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, b, v4i{0, 0, 0, 0}, 0, 0, 0);
+            const v4i ci = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, b, v4i{kQ8Bias, kQ8Bias, kQ8Bias, kQ8Bias}, 0, 0, 0);
             const float dh = shf[wave][kb];
             const u32x4 sv = as[kb >> 1];
             const uint32_t s01 = (kb & 1) ? sv[2] : sv[0], s23 = (kb & 1) ? sv[3] : sv[1];
-            c[0] += (float)ci[0] * (f16lo(s01) * dh);
-            c[1] += (float)ci[1] * (f16hi(s01) * dh);
-            c[2] += (float)ci[2] * (f16lo(s23) * dh);
-            c[3] += (float)ci[3] * (f16hi(s23) * dh);
+            const float w[4] = {f16lo(s01), f16hi(s01), f16lo(s23), f16hi(s23)};
+#pragma unroll
+            for (int r = 0; r < 4; r++) c[r] = fmaf(q8_scaled(ci[r], w[r], -kQ8BiasF * w[r]), dh, c[r]);
         }
     } else {
         static_for<0, 4>([&](auto J) {
