@@ -46,6 +46,9 @@ MAT_BYTES = D * FF // 2 + D * FF // 32         # one packed expert matrix, 557,0
 EXPERT_BYTES = 3 * MAT_BYTES                   # gate + up + down, 1,671,168 B
 Q8_MAT_BYTES = D * FF + D * FF // 16           # q8_0-split down matrix, 1,114,112 B
 
+# the configurations measured beside the headline one, in the same run
+SWEEP = ["decode1", "decode2", "decode4", "decode8", "decode16", "decode32", "ragged64", "prefill4096", "mixed"]
+
 CONFIGS = {
     "decode1": dict(T=1, shared=False, steps=2000, warmup=200),
     "decode2": dict(T=2, shared=False, steps=2000, warmup=200),
@@ -76,8 +79,11 @@ def parse():
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--path", type=int, default=0, help="q36moe_ctx_set_path mode (0 auto)")
     ap.add_argument("--graph", type=int, default=1,
-                    help="1: time a HIP graph of one forward per weight layer (how a model's "
-                         "layer loop runs when captured); 0: eager launches only")
+                    help="1: time the K steps as one HIP graph (how a model's layer loop runs "
+                         "when captured); 0: eager launches only")
+    ap.add_argument("--replays", type=int, default=5, help="timed replays of the K-step graph (median)")
+    ap.add_argument("--no-sweep", action="store_true",
+                    help="skip the other configurations (configs sub-object)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (counter calibration)")
     return ap.parse_args()
@@ -98,11 +104,6 @@ def make_inputs(cfg_name, T, n, seed, dev):
         ls.append(torch.from_numpy(lg).to(dev))
         ss.append(torch.from_numpy(rng.standard_normal(T).astype(np.float32)).to(dev))
     return xs, ls, ss
-
-
-def distinct_experts(layer, moe):
-    idx = layer.tap(moe.TAP_TOPK_IDX).cpu().numpy()
-    return int(np.unique(idx).size)
 
 
 def kernel_bytes(stage, T, U, shared, dn_q8=False, sh_q8=False):
@@ -227,6 +228,126 @@ def cpu_baseline(cfg_name, T, seconds, shared):
             "config0_gemv": _gemv_config0(pyoracle, nth, 1.0)}
 
 
+def flush_mall(buf):
+    """Evict the 256 MB memory-side cache: one copy over 2 x 512 MiB."""
+    buf[1].copy_(buf[0])
+
+
+def algorithmic(T, U, shared, dn_q8=False, sh_q8=False):
+    """Algorithmic HBM bytes and MFMA FLOPs of one layer forward: the weights
+    of the U routed experts hit (+ the shared expert), f32 x, f32 logits and
+    bf16 out per token."""
+    by = (U + (1 if shared else 0)) * EXPERT_BYTES + T * (D * 4 + E * 4 + D * 2)
+    if dn_q8:
+        by += U * (Q8_MAT_BYTES - MAT_BYTES)
+    if sh_q8:
+        by += 3 * (Q8_MAT_BYTES - MAT_BYTES)
+    fl = kernel_flops("gateup", T, shared) + kernel_flops("down", T, shared)
+    return by, fl
+
+
+class Bench:
+    """One configuration on a shared set of weight layers and one context."""
+
+    def __init__(self, args, layers, layer, stream, flush):
+        self.args, self.layers, self.layer, self.stream, self.flush = args, layers, layer, stream, flush
+
+    def setup(self, cfg_name, seed):
+        import torch
+        cfg = CONFIGS[cfg_name]
+        self.name, self.T, self.shared = cfg_name, cfg["T"], cfg["shared"]
+        n_in = self.args.inputs if self.T < 1024 else min(self.args.inputs, 4)
+        self.xs, self.ls, self.ss = make_inputs(cfg_name, self.T, n_in, seed, torch.device("cuda:0"))
+        self.out = torch.empty((self.T, D), dtype=torch.bfloat16, device="cuda:0")
+
+    def step(self, i):
+        j = i % len(self.xs)
+        self.layer.forward(self.layers[i % len(self.layers)], self.xs[j], self.ls[j],
+                           self.ss[j] if self.shared else None, out=self.out)
+
+    def graph(self, first, count):
+        """A HIP graph of `count` consecutive forwards from step `first`."""
+        import torch
+        cap = torch.cuda.Stream()
+        self.layer.set_stream(cap)
+        with torch.cuda.stream(cap):
+            self.step(first)          # allocator / first-launch work outside the capture
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=cap):
+            for i in range(count):
+                self.step(first + i)
+        torch.cuda.synchronize()
+        self.layer.set_stream(self.stream)
+        return g
+
+    def time_replays(self, g, n):
+        """Milliseconds of each of n replays of g, the memory-side cache
+        flushed before each (untimed)."""
+        import torch
+        out = []
+        for _ in range(n):
+            flush_mall(self.flush)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(self.stream)
+            g.replay()
+            e1.record(self.stream)
+            torch.cuda.synchronize()
+            out.append(e0.elapsed_time(e1))
+        return out
+
+    def stage_times(self, budget_us=2e5):
+        """Average duration of each stage's kernels: the stage of the last
+        forward launched again back to back over the rotating weight sets,
+        bracketed by two HIP events on the layer's stream."""
+        import torch
+        from q36_amd import moe
+        self.step(0)
+        torch.cuda.synchronize()
+        U = int(np.unique(self.layer.tap(moe.TAP_TOPK_IDX).cpu().numpy()).size)
+        path = self.layer.last_path
+        st_us = {}
+        for st in moe.MoELayer.STAGES:
+            for i in range(5):
+                self.layer.replay(self.layers[i % len(self.layers)], st)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(self.stream)
+            reps = 0
+            t0 = time.perf_counter()
+            while True:
+                for i in range(20):
+                    self.layer.replay(self.layers[(reps + i) % len(self.layers)], st)
+                reps += 20
+                if reps >= 2000 or (time.perf_counter() - t0) * 1e6 > budget_us:
+                    break
+            e1.record(self.stream)
+            torch.cuda.synchronize()
+            st_us[st] = 1e3 * e0.elapsed_time(e1) / reps
+        # stages without kernels on a path time as the empty-launch floor
+        if path == 1:
+            for st in ("route", "scan", "combine"):
+                st_us[st] = 0.0
+        self.step(0)              # `out` holds a real result again
+        torch.cuda.synchronize()
+        return U, path, st_us
+
+    def summary(self, ms_layer, U, path, st_us, dn_q8=False, sh_q8=False):
+        T, shared = self.T, self.shared
+        by, fl = algorithmic(T, U, shared, dn_q8, sh_q8)
+        r = {"tokens": T, "us_per_layer": ms_layer * 1e3, "tokens_per_s": T / (ms_layer * 1e-3),
+             "distinct_experts": U, "path": {0: "sorted_fat", 1: "direct", 2: "sorted_skinny"}.get(path, path),
+             "layer_bytes": by, "layer_hbm_frac": by / (ms_layer * 1e-3) / 1e9 / HBM_PEAK_GBS,
+             "layer_flops": fl, "layer_mfma_frac": fl / (ms_layer * 1e-3) / 1e12 / MFMA_FP8_PEAK_TFS,
+             "stage_us": st_us}
+        for st in ("gateup", "down"):
+            kf, kb = kernel_flops(st, T, shared), kernel_bytes(st, T, U, shared, dn_q8, sh_q8)
+            r[st] = {"us": st_us[st], "mfma_frac": kf / (st_us[st] * 1e-6) / 1e12 / MFMA_FP8_PEAK_TFS,
+                     "hbm_frac": kb / (st_us[st] * 1e-6) / 1e9 / HBM_PEAK_GBS, "flops": kf, "bytes": kb}
+        return r
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -237,39 +358,16 @@ def main():
     from q36_amd import moe
 
     if args.copy_mib:
-        # a plain copy of known size: the reference point that scales the
-        # FETCH_SIZE / WRITE_SIZE counters of the layer kernels
-        n = args.copy_mib << 20
-        src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
-        dst = torch.empty_like(src)
-        for _ in range(4):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        # achievable-bandwidth reference points: the copy (read + write) and a
-        # read-only reduction over the same bytes, as f32
-        ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
-        f = src.view(torch.float32)
-        f.sum()
-        ev[0].record()
-        for _ in range(10):
-            dst.copy_(src)
-        ev[1].record()
-        ev[2].record()
-        for _ in range(10):
-            f.sum()
-        ev[3].record()
-        torch.cuda.synchronize()
-        copy_us = ev[0].elapsed_time(ev[1]) * 100.0
-        read_us = ev[2].elapsed_time(ev[3]) * 100.0
-        print(json.dumps({"copy_bytes": n, "launches": 4,
-                          "copy_us": copy_us, "copy_gbs": 2 * n / copy_us / 1e3,
-                          "read_us": read_us, "read_gbs": n / read_us / 1e3}))
+        copy_reference(args.copy_mib)
         return
 
     cfg = CONFIGS[args.config]
     T, shared = cfg["T"], cfg["shared"]
     steps = args.steps if args.steps is not None else cfg["steps"]
     warmup = args.warmup if args.warmup is not None else cfg["warmup"]
+    if steps < 1 or warmup < 0:
+        print(json.dumps({"error": "--steps must be >= 1 and --warmup >= 0"}))
+        sys.exit(2)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     stream = torch.cuda.current_stream()
@@ -279,6 +377,8 @@ def main():
     host_up = dn_q8 or sh_q8
     if args.layers is None:
         args.layers = 16 if host_up else 40
+    sweep = [] if (args.no_sweep or host_up) else [c for c in SWEEP if c != args.config]
+    with_shared = shared or any(CONFIGS[c]["shared"] for c in sweep)
     layers = []
     for l in range(args.layers):
         if host_up:
@@ -298,84 +398,45 @@ def main():
                                       sw.get("sh_down"), down_type=dn_t, sh_type=sh_t)
             del sw, dn
         else:
-            w = moe.MoEWeights.alloc(E, D, FF, FF if shared else 0)
+            w = moe.MoEWeights.alloc(E, D, FF, FF if with_shared else 0)
             w.fill_synthetic(args.seed * 1000 + l)
         layers.append(w)
-    xs, ls, ss = make_inputs(args.config, T, args.inputs, args.seed, dev)
-    layer = moe.MoELayer(T, stream=stream)
+    max_T = max([T] + [CONFIGS[c]["T"] for c in sweep])
+    layer = moe.MoELayer(max_T, stream=stream)
     layer.set_path(args.path)
-    out = torch.empty((T, D), dtype=torch.bfloat16, device=dev)
+    flush = torch.empty((2, 512 << 20), dtype=torch.uint8, device=dev)
+    B = Bench(args, layers, layer, stream, flush)
+    B.setup(args.config, args.seed)
     torch.cuda.synchronize()
 
-    def step(i):
-        j = i % args.inputs
-        layer.forward(layers[i % args.layers], xs[j], ls[j], ss[j] if shared else None,
-                      out=out)
-
+    # the contract: W untimed warmup steps, then exactly K timed steps
     for i in range(warmup):
-        step(i)
+        B.step(i)
     torch.cuda.synchronize()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     ev0.record(stream)
     for i in range(steps):
-        step(warmup + i)
+        B.step(warmup + i)
     ev1.record(stream)
     torch.cuda.synchronize()
     ms_eager = ev0.elapsed_time(ev1) / steps
-    ms = ms_eager
-    graph_layers = 0
+    ms, timed = ms_eager, "eager stream launches"
+    replay_ms = []
     if args.graph:
-        # one forward per weight layer (inputs cycling) captured once, then
-        # replayed: the host issues one launch per args.layers layers
-        graph_layers = args.layers
-        cap = torch.cuda.Stream()
-        layer.set_stream(cap)
-        with torch.cuda.stream(cap):
-            for i in range(graph_layers):
-                step(i)
-        torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=cap):
-            for i in range(graph_layers):
-                step(i)
-        torch.cuda.synchronize()
-        layer.set_stream(stream)
-        reps = max(1, steps // graph_layers)
-        g.replay()
-        torch.cuda.synchronize()
-        ev0.record(stream)
-        for _ in range(reps):
-            g.replay()
-        ev1.record(stream)
-        torch.cuda.synchronize()
-        ms = ev0.elapsed_time(ev1) / (reps * graph_layers)
-        steps = reps * graph_layers
+        # the same K steps (layers and inputs rotating as above) captured as
+        # one HIP graph -- how a model's captured layer loop issues them --
+        # replayed with the memory-side cache flushed first; the first replay
+        # is untimed, the median of the timed ones is the figure
+        g = B.graph(warmup, steps)
+        B.time_replays(g, 1)
+        replay_ms = B.time_replays(g, args.replays)
+        ms = float(np.median(replay_ms)) / steps
+        timed = (f"HIP graph of the {steps} timed layer forwards; median of {args.replays} replays, "
+                 "memory-side cache flushed before each")
+        del g
 
-    # per-kernel durations: one more forward fixes the stage inputs, then
-    # each stage's kernels are launched again `reps` times back to back over
-    # the rotating weight sets, bracketed by two HIP events on the layer's
-    # stream (the stream the kernels run on)
-    step(0)
-    torch.cuda.synchronize()
-    U = distinct_experts(layer, moe)
-    reps = max(50, min(2000, int(2e5 / max(ms * 1e3, 1.0))))
-    st_us = {}
-    for st in moe.MoELayer.STAGES:
-        for i in range(5):
-            layer.replay(layers[i % args.layers], st)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for i in range(reps):
-            layer.replay(layers[i % args.layers], st)
-        e1.record(stream)
-        torch.cuda.synchronize()
-        st_us[st] = 1e3 * e0.elapsed_time(e1) / reps
-    # stages without kernels on this path time as the empty-launch floor;
-    # report them as 0
-    path = layer.last_path
-    if path == 1:
-        for st in ("route", "scan", "combine"):
-            st_us[st] = 0.0
+    U, path, st_us = B.stage_times()
+    head = B.summary(ms, U, path, st_us, dn_q8, sh_q8)
     dom = "gateup" if st_us["gateup"] >= st_us["down"] else "down"
     prefill = T >= 256
     if prefill:
@@ -384,31 +445,16 @@ def main():
         roof = {"bound": "mfma", "achieved": ach, "peak": MFMA_FP8_PEAK_TFS, "unit": "TFLOP/s",
                 "frac": ach / MFMA_FP8_PEAK_TFS, "traffic": None, "kernel": dom,
                 "kernel_us": st_us[dom], "flops_per_launch": fl,
-                "hbm_gbs": kernel_bytes(dom, T, U, shared, dn_q8, sh_q8) / (st_us[dom] * 1e-6) / 1e9}
+                "layer_mfma_frac": head["layer_mfma_frac"], "layer_hbm_frac": head["layer_hbm_frac"]}
     else:
         by = kernel_bytes(dom, T, U, shared, dn_q8, sh_q8)
         ach = by / (st_us[dom] * 1e-6) / 1e9
         roof = {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": ach / HBM_PEAK_GBS, "traffic": None, "kernel": dom,
-                "kernel_us": st_us[dom], "bytes_per_launch": by}
+                "kernel_us": st_us[dom], "bytes_per_launch": by,
+                "layer_hbm_frac": head["layer_hbm_frac"], "layer_bytes": head["layer_bytes"]}
     roof["traffic"] = None if host_up else measured_traffic(args.config, dom)
-    # both grouped GEMMs against both ceilings (the dominant one is `roof`)
-    gemm = {}
-    for st in ("gateup", "down"):
-        fl, by = kernel_flops(st, T, shared), kernel_bytes(st, T, U, shared, dn_q8, sh_q8)
-        gemm[st] = {"us": st_us[st], "tflops": fl / (st_us[st] * 1e-6) / 1e12,
-                    "mfma_frac": fl / (st_us[st] * 1e-6) / 1e12 / MFMA_FP8_PEAK_TFS,
-                    "gbs": by / (st_us[st] * 1e-6) / 1e9,
-                    "hbm_frac": by / (st_us[st] * 1e-6) / 1e9 / HBM_PEAK_GBS}
-    # the forward once more, so `out` holds a real result again
-    step(0)
-    torch.cuda.synchronize()
 
-    layer_bytes = (U + (1 if shared else 0)) * EXPERT_BYTES + T * (D * 4 + E * 4 + D * 2)
-    if dn_q8:
-        layer_bytes += U * (Q8_MAT_BYTES - MAT_BYTES)
-    if sh_q8:
-        layer_bytes += 3 * (Q8_MAT_BYTES - MAT_BYTES)
     res = {
         "metric": "MoE layer tokens/s (W4A8, 1 GPU)",
         "value": T / (ms * 1e-3),
@@ -419,6 +465,7 @@ def main():
         "ms_per_step": ms,
         "us_per_layer": ms * 1e3,
         "us_per_layer_eager": ms_eager * 1e3,
+        "replay_ms": replay_ms,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -430,18 +477,61 @@ def main():
                    "tokens": T, "d_model": D, "n_expert": E, "down_type": args.down_type,
                    "shared_type": args.shared_type if shared else None,
                    "top_k": K, "d_ff": FF, "shared_expert": shared,
-                   "weight_layers_rotated": args.layers,
-                   "launch": (f"HIP graph of {graph_layers} layer forwards, replayed"
-                              if graph_layers else "eager stream launches")},
-        "layer_hbm_fraction": layer_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                   "weight_layers_rotated": args.layers, "launch": timed},
+        "layer_hbm_fraction": head["layer_hbm_frac"],
         "distinct_experts": U,
         "stage_us": st_us,
         "roofline": roof,
-        "grouped_gemms": gemm,
+        "grouped_gemms": {st: head[st] for st in ("gateup", "down")},
     }
+    # the other BASELINE configurations, measured in the same run on the same
+    # weight layers: a HIP graph of one forward per layer, median of replays
+    cfgs = {}
+    for c in sweep:
+        B.setup(c, args.seed + 17)
+        for i in range(3):
+            B.step(i)
+        g = B.graph(0, args.layers)
+        B.time_replays(g, 1)
+        rms = B.time_replays(g, 3)
+        del g
+        U_c, path_c, st_c = B.stage_times(budget_us=5e4)
+        cfgs[c] = B.summary(float(np.median(rms)) / args.layers, U_c, path_c, st_c)
+    if cfgs:
+        res["configs"] = cfgs
     if not args.no_cpu and not host_up:
         res["cpu_baseline"] = cpu_baseline(args.config, T, args.cpu_seconds, shared)
     print(json.dumps(res))
+
+
+def copy_reference(mib):
+    """A plain copy of known size: the reference point that scales the
+    FETCH_SIZE / WRITE_SIZE counters of the layer kernels, and the
+    achievable-bandwidth reference points (copy, read-only f32 sum)."""
+    import torch
+    n = mib << 20
+    src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    f = src.view(torch.float32)
+    f.sum()
+    ev[0].record()
+    for _ in range(10):
+        dst.copy_(src)
+    ev[1].record()
+    ev[2].record()
+    for _ in range(10):
+        f.sum()
+    ev[3].record()
+    torch.cuda.synchronize()
+    copy_us = ev[0].elapsed_time(ev[1]) * 100.0
+    read_us = ev[2].elapsed_time(ev[3]) * 100.0
+    print(json.dumps({"copy_bytes": n, "launches": 4,
+                      "copy_us": copy_us, "copy_gbs": 2 * n / copy_us / 1e3,
+                      "read_us": read_us, "read_gbs": n / read_us / 1e3}))
 
 
 if __name__ == "__main__":

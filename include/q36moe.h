@@ -104,8 +104,7 @@ int q36moe_weights_upload(const void *gate, const void *up, const void *down,
  * quantised per 32 to int8 with an fp32 scale (d = amax/127; h for a
  * q8_0-split down, and x for a q8_0-split shared expert) and the product runs
  * on int8 MFMA, each 32-block's integer dot product scaled by both scales.
- * A q8_0-split layer refuses decode path 3 (the one-kernel variant), and a
- * q8_0-split shared expert refuses q36moe_forward_q8 (its x must be the
+ * A q8_0-split shared expert refuses q36moe_forward_q8 (its x must be the
  * unquantised input): EINVAL. */
 int q36moe_weights_upload_typed(const void *gate, const void *up, const void *down, int down_type,
                                 const void *sh_gate, const void *sh_up, const void *sh_down, int sh_type,
@@ -166,9 +165,12 @@ int q36moe_ctx_set_stream(q36moe_ctx *c, void *stream);
 void q36moe_ctx_free(q36moe_ctx *c);
 
 /* The MoE layer.  x [T][d_model] (f32 or bf16, row stride d_model),
- * logits [T][ld_logits] f32 (first n_expert columns used), shg [T] f32
- * shared-expert gate logits or NULL, out [T][d_model] (f32 or bf16).
- * out[t] = sum_s w[t][s] * E_{idx[t][s]}(x[t]) + sigmoid(shg[t]) * S(x[t]),
+ * logits [T][ld_logits] f32 (first n_expert columns used), shg the
+ * shared-expert gate logits or NULL: token t's at shg[t * ld_shg] (ld_shg 0
+ * means 1; the reference's batched decode keeps it as column 256 of each
+ * 257-wide router row, q36_engine.cu:2092-2095, which is shg = logits + 256,
+ * ld_shg = 257), out [T][d_model] (f32 or bf16).
+ * out[t] = sum_s w[t][s] * E_{idx[t][s]}(x[t]) + sigmoid(shg[t*ld_shg]) * S(x[t]),
  * E(x) = down . q8(silu(gate . q8(x)) * up . q8(x)), q8 = per-32 E8M0 +
  * e4m3 quantisation, w = top-k softmax weights renormalised, times scale.
  * A matrix uploaded in the q8_0-split layout (q36moe_weights_upload_typed)
@@ -176,7 +178,7 @@ void q36moe_ctx_free(q36moe_ctx *c);
  * Asynchronous on the context stream; T = 0 is a no-op. */
 int q36moe_forward(q36moe_ctx *c, const q36moe_weights *w,
                    const void *x, int x_fmt, const float *logits, int ld_logits,
-                   const float *shg, int T, float scale, void *out, int out_fmt);
+                   const float *shg, int ld_shg, int T, float scale, void *out, int out_fmt);
 
 /* Stage entry points (device pointers, asynchronous on `stream`). */
 int q36moe_router_topk(const float *logits, int T, int n_expert, int ld, int k,
@@ -211,29 +213,25 @@ int q36moe_add_rmsnorm_quant(float *h, const float *a, const float *w, int T, in
  * q36moe_forward on the x they were quantised from.  EINVAL with shg for a
  * q8_0-split shared expert (it quantises the unquantised x itself). */
 int q36moe_forward_q8(q36moe_ctx *c, const q36moe_weights *w, const uint8_t *xq, const uint8_t *xs,
-                      const float *logits, int ld_logits, const float *shg, int T, float scale,
-                      void *out, int out_fmt);
+                      const float *logits, int ld_logits, const float *shg, int ld_shg, int T,
+                      float scale, void *out, int out_fmt);
 
 /* Execution path of q36moe_forward.  The sorted path (route + sort + grouped
  * expert GEMMs + combine) serves any T, with fat tiles (up to 160 rows per
  * expert tile, weights staged through LDS) or skinny tiles (up to 32 rows,
  * weights streamed straight into registers); the direct path (no sort,
  * slots combined in registers) serves T <= 16 as two kernels (gate/up, then
- * down), or as one kernel whose down-role workgroups wait on per-token
- * counters (mode 3; measured slower on MI355X: each device-scope poll is a
- * memory round trip).  mode 0 picks the two-kernel direct path for T <= 16,
- * skinny tiles while T*k <= 8*n_expert and fat tiles above; 1 forces sorted
- * with fat tiles, 4 sorted with skinny tiles, 2 direct, 3 the one-kernel
- * direct path (EINVAL from forward when T > 16 in modes 2/3).  last_path:
- * 0 sorted (fat), 1 direct, 2 sorted (skinny).  With the direct path the
- * PERM/POS taps are the identity (rows in entry order) and the EOFF/DNW taps
- * are unavailable. */
+ * down).  mode 0 picks the direct path for T <= 16, skinny tiles while
+ * T*k <= 8*n_expert and fat tiles above; 1 forces sorted with fat tiles,
+ * 4 sorted with skinny tiles, 2 direct (EINVAL from forward when T > 16).
+ * Mode 3 (a one-kernel decode variant, measured slower) no longer exists:
+ * EINVAL.  last_path: 0 sorted (fat), 1 direct, 2 sorted (skinny).  With the
+ * direct path the PERM/POS taps are the identity (rows in entry order) and
+ * the EOFF/DNW taps are unavailable. */
 int q36moe_ctx_set_path(q36moe_ctx *c, int mode);
 int q36moe_ctx_last_path(const q36moe_ctx *c);
 
-/* Synchronises the context stream and reports whether any bounded
- * inter-workgroup wait of the one-kernel direct path gave up since the last
- * check (Q36MOE_EHIP; the wait counters are reset).  0 otherwise. */
+/* Synchronises the context stream; Q36MOE_EHIP if it reports an error. */
 int q36moe_ctx_check(q36moe_ctx *c);
 
 /* Copy one internal buffer of the last forward into dst (device pointer,

@@ -44,26 +44,6 @@
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
-#ifdef Q36MOE_TRACE
-__device__ unsigned long long g_q36_trace[64];
-__device__ unsigned long long g_q36_clk[64];
-__device__ unsigned long long g_q36_wg[2 * 4096];
-#define Q36_TRACE_WG(n)                                                                  \
-    do {                                                                                 \
-        const unsigned wg_ = blockIdx.y * gridDim.x + blockIdx.x;                        \
-        if (threadIdx.x == 0 && wg_ < 4096u) g_q36_wg[2 * wg_ + (n)] = wall_clock64();   \
-    } while (0)
-#define Q36_TRACE_AT(n)                                                                  \
-    do {                                                                                 \
-        if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) {                  \
-            g_q36_trace[n] = wall_clock64();                                             \
-            g_q36_clk[n] = __builtin_amdgcn_s_memtime();                                 \
-        }                                                                                \
-    } while (0)
-#else
-#define Q36_TRACE_AT(n) do {} while (0)
-#define Q36_TRACE_WG(n) do {} while (0)
-#endif
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef int v4i __attribute__((ext_vector_type(4)));
 
@@ -250,7 +230,6 @@ __device__ __forceinline__ Pick route_pick(const float *__restrict__ l, int E, i
         // than the key keeps the load outside any branch
         key[j] = logit_key(ok[j] ? lv[j] : __uint_as_float(0x7fffffffu));
     }
-    Q36_TRACE_AT(10);
     // 1. bound: min over the 8 group maxima (a group with no valid key gives 0)
     uint32_t lm = max(max(key[0], key[1]), max(key[2], key[3]));
     const uint32_t gm = group8_max(lm);
@@ -275,7 +254,6 @@ __device__ __forceinline__ Pick route_pick(const float *__restrict__ l, int E, i
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    Q36_TRACE_AT(11);
     // 3. rank each candidate; ranks below k are the picks
     for (int c0 = 0; c0 < nc; c0 += 64) {
         const int ci = c0 + lane;
@@ -296,7 +274,6 @@ __device__ __forceinline__ Pick route_pick(const float *__restrict__ l, int E, i
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    Q36_TRACE_AT(12);
     // 4. weights
     const int me = lane < k ? lane : 0;
     const float vmax = key_val(lds[0]);
@@ -308,7 +285,6 @@ __device__ __forceinline__ Pick route_pick(const float *__restrict__ l, int E, i
     P.idx = (int)lds[kMaxTopK + me];
     P.slot = me;
     P.w = fast_exp(key_val(lds[me]) - vmax) * __builtin_amdgcn_rcpf(wsum) * scale;
-    Q36_TRACE_AT(13);
     return P;
 }
 
@@ -500,7 +476,6 @@ __global__ __launch_bounds__(64 * TPB) void k_route(RouteArgs A) {
     for (int e = threadIdx.x; e < A.E; e += 64 * TPB) tmask[e] = 0u;
     __syncthreads();
     const int t = t0 + wave;
-    Q36_TRACE_AT(20);
     if (t < A.T) {
         // x of the token (kRouteD values, 8 per lane per pass) is loaded
         // before routing so both latencies overlap
@@ -517,7 +492,6 @@ __global__ __launch_bounds__(64 * TPB) void k_route(RouteArgs A) {
             ent[wave * A.k + lane] = P.idx;
             atomicOr(&tmask[P.idx], 1u << wave);
         }
-        Q36_TRACE_AT(21);
         if (preq) {
             // codes stay where the caller put them; only the lane-group-major
             // copy of the scales is made for the grouped GEMM
@@ -547,16 +521,13 @@ __global__ __launch_bounds__(64 * TPB) void k_route(RouteArgs A) {
         }
         }
     }
-    Q36_TRACE_AT(22);
     __syncthreads();
-    Q36_TRACE_AT(23);
     const int ntok = min(TPB, A.T - t0);
     if (threadIdx.x < ntok * A.k) {
         const int tl = threadIdx.x / A.k;
         const int e = ent[threadIdx.x];
         A.rank[(size_t)t0 * A.k + threadIdx.x] = __popc(tmask[e] & ((1u << tl) - 1u));
     }
-    Q36_TRACE_AT(24);
     for (int e = threadIdx.x; e < A.E; e += 64 * TPB)
         A.blk_cnt[(size_t)e * A.nb + blockIdx.x] = __popc(tmask[e]);
 }
@@ -583,7 +554,7 @@ __global__ __launch_bounds__(256) void k_quant(const void *x, int x_fmt, int T, 
 // ---------------------------------------------------------------------------
 struct ScanArgs {
     const int32_t *blk_cnt; int nb; int tpb; int inline_cols; int E; int T; int k;
-    const int32_t *idx; const float *wt; const int32_t *rank; const float *shg;
+    const int32_t *idx; const float *wt; const int32_t *rank; const float *shg; int ld_shg;
     int tn;      // rows per routed tile
     int tn_sh;   // rows per shared-expert tile
     int32_t *blk_off; int32_t *tot; int32_t *e_off; int32_t *perm; int32_t *pos;
@@ -699,7 +670,7 @@ __global__ __launch_bounds__(256) void k_scatter(ScanArgs A) {
     if (A.shg) {
         for (int t = b * A.tpb + tid; t < min(A.T, (b + 1) * A.tpb); t += 256) {
             A.row_tok[n + t] = t;
-            A.row_w[n + t] = 1.0f / (1.0f + expf(-A.shg[t]));
+            A.row_w[n + t] = 1.0f / (1.0f + expf(-A.shg[(size_t)t * A.ld_shg]));
         }
     }
     if (b == 0) {
@@ -905,7 +876,6 @@ __device__ __forceinline__ void body(const GemmArgs &A, Lds &L, const uint8_t *W
     issue_a(0, 0);
     issue_b(0, 0);
     issue_a(1, 1);
-    if (wave == 0) Q36_TRACE_AT(29);
 
     v4f acc[4][NJ1];
 #pragma unroll
@@ -931,7 +901,6 @@ __device__ __forceinline__ void body(const GemmArgs &A, Lds &L, const uint8_t *W
                 for (int j = 0; j < NJ; j++) asm volatile("" : "+v"(acc[a][j]));
             wait_vm(kt + 1 < NKT ? 2 : 0);
             dma_barrier();
-            if (wave == 0) Q36_TRACE_AT(30 + kt);
             if constexpr (st == 0) {
 #pragma unroll
                 for (int a = 0; a < 4; a++) {
@@ -974,7 +943,6 @@ __device__ __forceinline__ void body(const GemmArgs &A, Lds &L, const uint8_t *W
         });
     }
 
-    if (wave == 0) Q36_TRACE_AT(46);
     // SwiGLU of gate tile i and up tile i (i = 0, 1: one 32-row h block)
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
@@ -1109,8 +1077,6 @@ __global__ __launch_bounds__(256, 2) void k_gateup_dma(GemmArgs A) {
     const int ti = 8 * (jx / NRB) + xcd;
     const int mt0 = (jx % NRB) * gdma::RT;
     if (ti >= *A.ntiles) return;
-    Q36_TRACE_WG(0);
-    Q36_TRACE_AT(28);
     const int4 tile = A.tiles[ti];
     const int e = tile.x, p0 = tile.y, p1 = tile.z;
     if (e == A.E && A.shq8) return;      // k_shared_gateup_q8's rows
@@ -1128,8 +1094,6 @@ __global__ __launch_bounds__(256, 2) void k_gateup_dma(GemmArgs A) {
         case 4: gdma::body<4>(A, L, Wg, Wu, mt0, p0, p1, hq8); break;
         default: gdma::body<5>(A, L, Wg, Wu, mt0, p0, p1, hq8); break;
     }
-    Q36_TRACE_AT(47);
-    Q36_TRACE_WG(1);
 }
 
 // ---------------------------------------------------------------------------
@@ -1560,8 +1524,6 @@ __global__ __launch_bounds__(64 * kDlW, Q8 ? 2 : 1) void k_down_lds(GemmArgs A) 
     const int xcd = blockIdx.x & 7, jx = blockIdx.x >> 3;
     const int ti = 8 * (jx / NRB) + xcd, rb = jx % NRB;
     if (ti >= *A.ntiles) return;
-    Q36_TRACE_WG(0);
-    Q36_TRACE_AT(48);
     const int4 tile = A.tiles[ti];
     const int e = __builtin_amdgcn_readfirstlane(tile.x), p0 = tile.y, p1 = tile.z;
     if constexpr (Q8) {
@@ -1595,7 +1557,6 @@ __global__ __launch_bounds__(64 * kDlW, Q8 ? 2 : 1) void k_down_lds(GemmArgs A) 
             ws[c] = A.row_w[c0 + c];
         }
         __syncthreads();
-        Q36_TRACE_AT(49);
         const int ntt = (nr + 15) >> 4;
         for (int j = 0; j < ntt; j++) {
             // padding columns read row 0 of the chunk; never stored
@@ -1631,8 +1592,6 @@ __global__ __launch_bounds__(64 * kDlW, Q8 ? 2 : 1) void k_down_lds(GemmArgs A) 
             }
         }
     }
-    Q36_TRACE_AT(50);
-    Q36_TRACE_WG(1);
 }
 
 // ---------------------------------------------------------------------------
@@ -1641,7 +1600,7 @@ __global__ __launch_bounds__(64 * kDlW, Q8 ? 2 : 1) void k_down_lds(GemmArgs A) 
 struct DirectArgs {
     const float *logits; int ld; int T; int E; int k; float scale;
     const void *x; int x_fmt;
-    const float *shg;
+    const float *shg; int ld_shg;               // shared-gate logit of token t: shg[t * ld_shg]
     const uint8_t *gate, *up, *down;            // routed experts (packed)
     const uint8_t *sh_gate, *sh_up, *sh_down;   // shared expert (packed) or null
     size_t wstride;                             // bytes per packed matrix
@@ -1651,9 +1610,6 @@ struct DirectArgs {
     float *hf;                                  // [entries][FF] fp32 SwiGLU rows
     uint8_t *hq; uint8_t *hs;                   // quantised h (tap)
     void *out; int out_fmt;
-    // fused kernel only: per-token arrival / departure counters (zero
-    // between calls), error flag, and the number of gate/up workgroups
-    uint32_t *arrive; uint32_t *depart; uint32_t *err; int n_gateup_wg;
     const uint8_t *xs_in;                       // scales of pre-quantised x (x_fmt kFmtE4M3)
     size_t dn_wstride;                          // bytes per routed down matrix
     int dn_q8;                                  // routed down is q8_0-split
@@ -1761,10 +1717,10 @@ __device__ __forceinline__ void direct_shared_q8(const DirectArgs &A, int t, int
 // weight loads in flight.  Measured (gate/up us, one tile / two): T=2 7.2 /
 // 7.5, T=4 9.8 / 10.0, T=8 16.5 / 15.5, T=16 27.4 / 25.6; four tiles at
 // T=16 25.7.
-template <bool FUSED, bool SHQ8 = false, int NFT = 1>
+template <bool SHQ8 = false, int NFT = 1>
 __device__ __forceinline__ void direct_gateup_body(const DirectArgs &A, int i, int ft0,
                                                    DirectGateupLds &L_) {
-    static_assert(NFT == 1 || (NFT == 2 && !FUSED), "row tiles per workgroup");
+    static_assert(NFT == 1 || NFT == 2, "row tiles per workgroup");
     if constexpr (SHQ8) {   // workgroup-uniform: the shared expert's entries
         const int nr0 = A.T * A.k;
         if (i >= nr0) {
@@ -1783,8 +1739,6 @@ __device__ __forceinline__ void direct_gateup_body(const DirectArgs &A, int i, i
     const int t = routed ? i / A.k : i - nr;
     const int s = routed ? i % A.k : 0;
 
-    Q36_TRACE_AT(0);
-    Q36_TRACE_WG(0);
     // issue this wave's x loads first (512 values, 8 per lane)
     const X8 xr = load8_raw(A.x, A.x_fmt, (size_t)t * kDD + wave * 512 + lane * 8);
 
@@ -1797,9 +1751,8 @@ __device__ __forceinline__ void direct_gateup_body(const DirectArgs &A, int i, i
         const int L = __builtin_ctzll(m);
         e = __builtin_amdgcn_readlane(P.idx, L);
         wgt = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(P.w), L));
-        Q36_TRACE_AT(1);
     } else {
-        wgt = 1.0f / (1.0f + expf(-A.shg[t]));
+        wgt = 1.0f / (1.0f + expf(-A.shg[(size_t)t * A.ld_shg]));
     }
     const uint8_t *Wg = (e < A.E) ? A.gate + (size_t)e * A.wstride : A.sh_gate;
     const uint8_t *Wu = (e < A.E) ? A.up + (size_t)e * A.wstride : A.sh_up;
@@ -1827,10 +1780,8 @@ __device__ __forceinline__ void direct_gateup_body(const DirectArgs &A, int i, i
         cvt8(xr, A.x_fmt, xv);
         quant8_lane(xv, lane, sx + wave * 512 + lane * 8, sxs + wave * 16 + (lane >> 2));
     }
-    Q36_TRACE_AT(2);
     if (threadIdx.x < 8) reinterpret_cast<uint32_t *>(sx + kDD)[threadIdx.x] = 0u;
     __syncthreads();
-    Q36_TRACE_AT(3);
 
     // B fragment: column 0 is the token; lanes of other columns read zeros
     const int q = lane >> 4;
@@ -1856,7 +1807,6 @@ __device__ __forceinline__ void direct_gateup_body(const DirectArgs &A, int i, i
             cu[u] = mfma_f4xf8<j>(a1, b, cu[u], sau[u], sb);
         }
     });
-    Q36_TRACE_AT(4);
     if (col0) {
 #pragma unroll
         for (int u = 0; u < NFT; u++)
@@ -1871,24 +1821,8 @@ __device__ __forceinline__ void direct_gateup_body(const DirectArgs &A, int i, i
         const int ft = ft0 + (lane >> 4), lr = lane & 15;
         const float g = red[0][0][lane] + red[1][0][lane] + red[2][0][lane] + red[3][0][lane];
         const float u = red[0][1][lane] + red[1][1][lane] + red[2][1][lane] + red[3][1][lane];
-        if constexpr (FUSED) {
-            // publish without an L2-wide release fence: the row goes out as a
-            // device-scope store (written through to the coherence point), the
-            // wave waits for its completion, then counts this workgroup in
-            __hip_atomic_store(&A.hf[(size_t)i * kDF + ft * 16 + lr], silu(g) * u,
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __builtin_amdgcn_s_waitcnt(0);
-            // system scope: the add is performed at the coherence point, where
-            // the pollers' device-scope loads look (an agent-scope add sits in
-            // this XCD's L2 and reaches them microseconds later)
-            if (lane == 0)
-                __hip_atomic_fetch_add(&A.arrive[t], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        } else {
-            A.hf[(size_t)i * kDF + ft * 16 + lr] = silu(g) * u;
-        }
+        A.hf[(size_t)i * kDF + ft * 16 + lr] = silu(g) * u;
     }
-    Q36_TRACE_AT(5);
-    Q36_TRACE_WG(1);
     if (ft0 == 0) {
         if (threadIdx.x == 0 && routed) {
             A.idx[i] = e;
@@ -1908,7 +1842,7 @@ __device__ __forceinline__ void direct_gateup_body(const DirectArgs &A, int i, i
 template <bool SHQ8, int NFT>
 __global__ __launch_bounds__(256) void k_direct_gateup(DirectArgs A) {
     __shared__ DirectGateupLds L_;
-    direct_gateup_body<false, SHQ8, NFT>(A, blockIdx.x, blockIdx.y * NFT, L_);
+    direct_gateup_body<SHQ8, NFT>(A, blockIdx.x, blockIdx.y * NFT, L_);
 }
 
 // Token t x 16 output rows; wave s handles slot s (wave k: shared expert):
@@ -1932,7 +1866,7 @@ __global__ __launch_bounds__(576) void k_direct_down(DirectArgs A) {
     const bool wq8 = Q8 && (routed ? A.dn_q8 : A.sh_q8);   // wave-uniform: selects the MFMA kind
     const int i = routed ? t * A.k + wave : nr + t;
     const int e = routed ? A.idx[i] : A.E;
-    const float wgt = routed ? A.wt[i] : 1.0f / (1.0f + expf(-A.shg[t]));
+    const float wgt = routed ? A.wt[i] : 1.0f / (1.0f + expf(-A.shg[(size_t)t * A.ld_shg]));
     const int q = lane >> 4;
     const bool col0 = (lane & 15) == 0;
     constexpr int NKP = kDF / 64, NKB = kDF / 32;
@@ -2022,143 +1956,6 @@ __global__ __launch_bounds__(576) void k_direct_down(DirectArgs A) {
         const size_t o = (size_t)t * kDD + rt * 16 + lane;
         if (A.out_fmt == Q36MOE_FMT_F32) static_cast<float *>(A.out)[o] = acc;
         else static_cast<uint16_t *>(A.out)[o] = (uint16_t)f32_to_bf16(acc);
-    }
-}
-
-// Single-kernel decode: workgroups [0, n_gateup_wg) are the gate/up role
-// (entry i x 16 rows, as k_direct_gateup); the rest are the down role (token
-// t x 16 output rows).  A down-role workgroup routes its token itself,
-// prefetches its down tiles, then waits until all gate/up workgroups of
-// token t have published their SwiGLU rows (per-token arrival counter,
-// release/acquire at device scope).  Workgroups are dispatched in index
-// order, so every gate/up workgroup is resident or finished before any
-// down-role workgroup waits, and gate/up workgroups never wait; the wait is
-// bounded as a backstop (error flag, then the workgroup goes on).  The last
-// down-role workgroup of a token resets both counters for the next call.
-constexpr uint32_t kSpinLimit = 1u << 22;
-
-__global__ __launch_bounds__(256) void k_decode_fused(DirectArgs A) {
-    __shared__ DirectGateupLds Lg;
-    __shared__ __align__(16) uint8_t sh[4][3][kDF + 32];
-    __shared__ uint8_t shs[4][3][kDF / 32];
-    __shared__ float red[3 * 4][16];
-    const int bid = blockIdx.x;
-    if (bid < A.n_gateup_wg) {
-        direct_gateup_body<true>(A, bid / (kDF / 16), bid % (kDF / 16), Lg);
-        return;
-    }
-    const int d = bid - A.n_gateup_wg;
-    const int t = d / (kDD / 16), rt = d % (kDD / 16);
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-    const bool has_sh = A.sh_down != nullptr;
-    const int nslot = A.k + (has_sh ? 1 : 0);
-    // slots of this wave: wave, wave + 4, wave + 8
-    const Pick P = route_pick(A.logits + (size_t)t * A.ld, A.E, A.k, A.scale, Lg.rlds[wave]);
-    uint4 a[3][4];
-    int sa[3];
-    float wgt[3];
-    const size_t nib = (size_t)kDD * kDF / 2;
-#pragma unroll
-    for (int m = 0; m < 3; m++) {
-        const int sl = wave + 4 * m;
-        wgt[m] = 0.0f;
-        if (sl < nslot) {
-            const uint8_t *W;
-            if (sl < A.k) {
-                const uint64_t b = __ballot(lane < A.k && P.slot == sl);
-                const int L = __builtin_ctzll(b);
-                const int e = __builtin_amdgcn_readlane(P.idx, L);
-                wgt[m] = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(P.w), L));
-                W = A.down + (size_t)e * A.wstride;
-            } else {
-                wgt[m] = 1.0f / (1.0f + expf(-A.shg[t]));
-                W = A.sh_down;
-            }
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-                a[m][j] = *reinterpret_cast<const uint4 *>(W + ((size_t)rt * 4 + j) * 1024 + (size_t)lane * 16);
-            sa[m] = *reinterpret_cast<const int *>(W + nib + ((size_t)rt * 64 + lane) * 4);
-        }
-    }
-    // wait for the SwiGLU rows of token t: wave 0 polls, the others hold at
-    // the barrier (few pollers keep the counter line uncontended)
-    Q36_TRACE_WG(0);
-    if (wave == 0) {
-        const uint32_t target = (uint32_t)nslot * (kDF / 16);
-        uint32_t spins = 0;
-        while (__hip_atomic_load(&A.arrive[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-            if (++spins > kSpinLimit) {
-                if (lane == 0) atomicOr(A.err, 1u);
-                break;
-            }
-            __builtin_amdgcn_s_sleep(8);
-        }
-    }
-    __syncthreads();
-    Q36_TRACE_WG(1);
-#pragma unroll
-    for (int m = 0; m < 3; m++) {
-        const int sl = wave + 4 * m;
-        if (sl < nslot) {
-            const int i = sl < A.k ? t * A.k + sl : A.T * A.k + t;
-            float hv[8];
-            // device-scope loads: read at the coherence point, not a stale L2 line
-#pragma unroll
-            for (int v = 0; v < 8; v++)
-                hv[v] = __hip_atomic_load(&A.hf[(size_t)i * kDF + lane * 8 + v], __ATOMIC_RELAXED,
-                                          __HIP_MEMORY_SCOPE_AGENT);
-            quant8_lane(hv, lane, &sh[wave][m][lane * 8], &shs[wave][m][lane >> 2]);
-            if (lane < 8) reinterpret_cast<uint32_t *>(&sh[wave][m][kDF])[lane] = 0u;
-            if (rt == 0) {   // quantised h (tap)
-                *reinterpret_cast<uint2 *>(A.hq + (size_t)i * kDF + lane * 8) =
-                    *reinterpret_cast<const uint2 *>(&sh[wave][m][lane * 8]);
-                if ((lane & 3) == 0) A.hs[(size_t)i * (kDF / 32) + (lane >> 2)] = shs[wave][m][lane >> 2];
-            }
-        }
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const int q = lane >> 4;
-    const bool col0 = (lane & 15) == 0;
-#pragma unroll
-    for (int m = 0; m < 3; m++) {
-        const int sl = wave + 4 * m;
-        if (sl < nslot) {
-            v4f c = {0.f, 0.f, 0.f, 0.f};
-            static_for<0, 4>([&](auto J) {
-                constexpr int j = decltype(J)::value;
-                const uint8_t *b0p = col0 ? &sh[wave][m][j * 128 + 16 * q] : &sh[wave][m][kDF];
-                const uint8_t *b1p = col0 ? &sh[wave][m][j * 128 + 64 + 16 * q] : &sh[wave][m][kDF + 16];
-                const uint4 b0 = *reinterpret_cast<const uint4 *>(b0p);
-                const uint4 b1 = *reinterpret_cast<const uint4 *>(b1p);
-                const v8i b = v8i{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w,
-                                  (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
-                const int sb = shs[wave][m][j * 4 + q];
-                const v8i av = v8i{(int)a[m][j].x, (int)a[m][j].y, (int)a[m][j].z, (int)a[m][j].w, 0, 0, 0, 0};
-                c = mfma_f4xf8<j>(av, b, c, sa[m], sb);
-            });
-            if (col0) {
-#pragma unroll
-                for (int r = 0; r < 4; r++) red[sl][4 * q + r] = c[r] * wgt[m];
-            }
-        }
-    }
-    __syncthreads();
-    if (wave == 0 && lane < 16) {
-        float acc = 0.0f;
-        for (int sl = 0; sl < nslot; sl++) acc += red[sl][lane];
-        const size_t o = (size_t)t * kDD + rt * 16 + lane;
-        if (A.out_fmt == Q36MOE_FMT_F32) static_cast<float *>(A.out)[o] = acc;
-        else static_cast<uint16_t *>(A.out)[o] = (uint16_t)f32_to_bf16(acc);
-    }
-    if (threadIdx.x == 0) {
-        const uint32_t old =
-            __hip_atomic_fetch_add(&A.depart[t], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        if (old == (uint32_t)(kDD / 16) - 1) {   // last reader of token t
-            __hip_atomic_store(&A.arrive[t], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(&A.depart[t], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
     }
 }
 
@@ -2267,7 +2064,7 @@ struct q36moe_weights {
 // Kernel arguments of the last forward; the weights are bound per launch so
 // a stage can be replayed over other weight sets (q36moe_ctx_replay).
 struct Plan {
-    int T, has_sh, direct, mode3, skinny, tiles, nb;
+    int T, has_sh, direct, skinny, tiles, nb;
     RouteArgs ra;
     ScanArgs sa;
     GemmArgs ga, da;
@@ -2293,8 +2090,7 @@ struct q36moe_ctx {
     int8_t *xq8; float *xsf;        // int8 x + fp32 scales (q8_0-split shared expert, sorted path)
     float *dnw;
     float *hf;                      // direct path: fp32 SwiGLU rows
-    uint32_t *sync;                 // fused decode: arrive[16], depart[16], err
-    int path_mode;                  // 0 auto, 1 sorted (fat tiles), 2 direct, 3 one-kernel direct, 4 sorted (skinny tiles)
+    int path_mode;                  // 0 auto, 1 sorted (fat tiles), 2 direct, 4 sorted (skinny tiles)
     int last_T, last_sh, last_path;
     int timing;
     Plan *plan;                     // kernel arguments of the last forward
@@ -2545,7 +2341,6 @@ int q36moe_ctx_create(int max_tokens, int n_expert, int d_model, int d_ff, int t
     const size_t o_dnw = take(rows * d_model * 4);
     const size_t direct_rows = (size_t)(max_tokens < kDirectMaxT ? max_tokens : kDirectMaxT) * (top_k + 1);
     const size_t o_hf = take(direct_rows * d_ff * 4);
-    const size_t o_sync = take((2 * kDirectMaxT + 1) * 4);
     if (hipMalloc(&c->base, off) != hipSuccess) {
         delete c;
         return Q36MOE_ENOMEM;
@@ -2572,12 +2367,6 @@ int q36moe_ctx_create(int max_tokens, int n_expert, int d_model, int d_ff, int t
     c->xsf = reinterpret_cast<float *>(b + o_xsf);
     c->dnw = reinterpret_cast<float *>(b + o_dnw);
     c->hf = reinterpret_cast<float *>(b + o_hf);
-    c->sync = reinterpret_cast<uint32_t *>(b + o_sync);
-    if (hipMemset(c->sync, 0, (2 * kDirectMaxT + 1) * 4) != hipSuccess) {
-        (void)hipFree(c->base);
-        delete c;
-        return Q36MOE_EHIP;
-    }
     for (int i = 0; i <= ST_COUNT; i++) {
         if (hipEventCreate(&c->ev[i]) != hipSuccess) {
             for (int j = 0; j < i; j++) (void)hipEventDestroy(c->ev[j]);
@@ -2625,10 +2414,7 @@ static void launch_stage(const q36moe_ctx *c, const Plan &P, int st, hipStream_t
     const int T = P.T, K = c->K, D = c->D, FF = c->FF;
     if (P.direct) {
         const int n = T * K + (P.has_sh ? T : 0);
-        if (P.mode3) {
-            if (st == ST_GATEUP)
-                hipLaunchKernelGGL(k_decode_fused, dim3(P.di.n_gateup_wg + T * (D / 16)), dim3(256), 0, s, P.di);
-        } else if (st == ST_GATEUP) {
+        if (st == ST_GATEUP) {
             // two row tiles per workgroup from kDirect2Tiles tokens on (one
             // routing and twice the loads in flight per workgroup; below
             // that, more workgroups spread a small batch better)
@@ -2708,7 +2494,7 @@ int q36moe_ctx_replay(q36moe_ctx *c, const q36moe_weights *w, int stage) {
 // scales of already quantised activations
 static int forward_impl(q36moe_ctx *c, const q36moe_weights *w, const void *x, int x_fmt,
                         const uint8_t *xs_in, const float *logits, int ld_logits, const float *shg,
-                        int T, float scale, void *out, int out_fmt) {
+                        int ld_shg, int T, float scale, void *out, int out_fmt) {
     if (!c || !w || T < 0 || T > c->max_T) return Q36MOE_EINVAL;
     if (w->E != c->E || w->D != c->D || w->FF != c->FF) return Q36MOE_EINVAL;
     if (out_fmt != Q36MOE_FMT_F32 && out_fmt != Q36MOE_FMT_BF16) return Q36MOE_EINVAL;
@@ -2718,6 +2504,8 @@ static int forward_impl(q36moe_ctx *c, const q36moe_weights *w, const void *x, i
     if (!x || !logits || !out || ld_logits < c->E) return Q36MOE_EINVAL;
     if (x_fmt == kFmtE4M3 && !xs_in) return Q36MOE_EINVAL;
     if (shg && !w->sh_gate) return Q36MOE_EINVAL;
+    if (ld_shg < 0) return Q36MOE_EINVAL;
+    if (ld_shg == 0) ld_shg = 1;
     const int has_sh = shg != nullptr;
     const int E = c->E, D = c->D, FF = c->FF, K = c->K;
     const int n = T * K;
@@ -2726,11 +2514,9 @@ static int forward_impl(q36moe_ctx *c, const q36moe_weights *w, const void *x, i
     hipStream_t s = c->stream;
 
     const int pm = c->path_mode;
-    const bool direct = (pm == 2 || pm == 3) ? (T <= kDirectMaxT) : (pm == 1 || pm == 4) ? false
-                                                                                      : (T <= kDirectMaxT);
-    if ((pm == 2 || pm == 3) && !direct) return Q36MOE_EINVAL;
+    const bool direct = pm == 2 ? (T <= kDirectMaxT) : (pm == 1 || pm == 4) ? false : (T <= kDirectMaxT);
+    if (pm == 2 && !direct) return Q36MOE_EINVAL;
     const bool shq8 = has_sh && w->sh_q8;
-    if (pm == 3 && (w->dn_q8 || shq8)) return Q36MOE_EINVAL;   // the one-kernel decode is MXFP4-only
     // a q8_0-split shared expert quantises x itself (int8 + fp32 per 32):
     // pre-quantised e4m3 input cannot feed it
     if (shq8 && x_fmt == kFmtE4M3) return Q36MOE_EINVAL;
@@ -2746,19 +2532,17 @@ static int forward_impl(q36moe_ctx *c, const q36moe_weights *w, const void *x, i
 
     Plan &P = *c->plan;
     P = Plan{};
-    P.T = T; P.has_sh = has_sh; P.direct = direct; P.mode3 = pm == 3; P.skinny = skinny;
+    P.T = T; P.has_sh = has_sh; P.direct = direct; P.skinny = skinny;
     P.tiles = tiles; P.nb = nb; P.out = out; P.out_fmt = out_fmt;
     if (direct) {
-        const int ngu = (n + (has_sh ? T : 0)) * (FF / 16);
-        P.di = DirectArgs{logits, ld_logits, T, E, K, scale, x, x_fmt, shg,
+        P.di = DirectArgs{logits, ld_logits, T, E, K, scale, x, x_fmt, shg, ld_shg,
                           nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0,
                           c->topk_idx, c->topk_w, c->pos, c->perm, c->xq, c->xs, c->hf,
-                          c->hq, c->hs, out, out_fmt, c->sync, c->sync + kDirectMaxT,
-                          c->sync + 2 * kDirectMaxT, ngu, xs_in, 0, 0, c->hsf};
+                          c->hq, c->hs, out, out_fmt, xs_in, 0, 0, c->hsf};
     } else {
         P.ra = RouteArgs{logits, ld_logits, T, E, K, scale, x, x_fmt, D, nb,
                          c->topk_idx, c->topk_w, c->xq, c->xs, c->xs2, c->blk_cnt, c->rank, xs_in};
-        P.sa = ScanArgs{c->blk_cnt, nb, tpb, nb <= kScanInlineBlocks ? 1 : 0, E, T, K, c->topk_idx, c->topk_w, c->rank, shg, tn, tn_sh,
+        P.sa = ScanArgs{c->blk_cnt, nb, tpb, nb <= kScanInlineBlocks ? 1 : 0, E, T, K, c->topk_idx, c->topk_w, c->rank, shg, ld_shg, tn, tn_sh,
                         c->blk_off, c->tot, c->e_off, c->perm, c->pos, c->row_tok, c->row_w, c->tiles,
                         c->ntiles};
         GemmArgs &ga = P.ga;
@@ -2809,17 +2593,17 @@ static int forward_impl(q36moe_ctx *c, const q36moe_weights *w, const void *x, i
 }
 
 int q36moe_forward(q36moe_ctx *c, const q36moe_weights *w, const void *x, int x_fmt,
-                   const float *logits, int ld_logits, const float *shg, int T, float scale,
+                   const float *logits, int ld_logits, const float *shg, int ld_shg, int T, float scale,
                    void *out, int out_fmt) {
     if (x_fmt != Q36MOE_FMT_F32 && x_fmt != Q36MOE_FMT_BF16) return Q36MOE_EINVAL;
-    return forward_impl(c, w, x, x_fmt, nullptr, logits, ld_logits, shg, T, scale, out, out_fmt);
+    return forward_impl(c, w, x, x_fmt, nullptr, logits, ld_logits, shg, ld_shg, T, scale, out, out_fmt);
 }
 
 int q36moe_forward_q8(q36moe_ctx *c, const q36moe_weights *w, const uint8_t *xq, const uint8_t *xs,
-                      const float *logits, int ld_logits, const float *shg, int T, float scale,
+                      const float *logits, int ld_logits, const float *shg, int ld_shg, int T, float scale,
                       void *out, int out_fmt) {
     if (T > 0 && !xs) return Q36MOE_EINVAL;
-    return forward_impl(c, w, xq, kFmtE4M3, xs, logits, ld_logits, shg, T, scale, out, out_fmt);
+    return forward_impl(c, w, xq, kFmtE4M3, xs, logits, ld_logits, shg, ld_shg, T, scale, out, out_fmt);
 }
 
 int q36moe_router_topk(const float *logits, int T, int n_expert, int ld, int k, float scale,
@@ -2910,7 +2694,7 @@ int q36moe_ctx_copy_tap(q36moe_ctx *c, int tap, void *dst, size_t bytes, size_t 
 }
 
 int q36moe_ctx_set_path(q36moe_ctx *c, int mode) {
-    if (!c || mode < 0 || mode > 4) return Q36MOE_EINVAL;
+    if (!c || mode < 0 || mode > 4 || mode == 3) return Q36MOE_EINVAL;
     c->path_mode = mode;
     return Q36MOE_OK;
 }
@@ -2919,17 +2703,7 @@ int q36moe_ctx_last_path(const q36moe_ctx *c) { return c ? c->last_path : Q36MOE
 
 int q36moe_ctx_check(q36moe_ctx *c) {
     if (!c) return Q36MOE_EINVAL;
-    uint32_t err = 0;
-    if (hipMemcpyAsync(&err, c->sync + 2 * kDirectMaxT, 4, hipMemcpyDeviceToHost, c->stream) != hipSuccess ||
-        hipStreamSynchronize(c->stream) != hipSuccess)
-        return Q36MOE_EHIP;
-    if (err) {
-        // a bounded wait gave up: clear the counters so later calls start clean
-        (void)hipMemsetAsync(c->sync, 0, (2 * kDirectMaxT + 1) * 4, c->stream);
-        (void)hipStreamSynchronize(c->stream);
-        return Q36MOE_EHIP;
-    }
-    return Q36MOE_OK;
+    return hip_rc(hipStreamSynchronize(c->stream));
 }
 
 int q36moe_ctx_set_timing(q36moe_ctx *c, int on) {

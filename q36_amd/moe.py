@@ -63,12 +63,12 @@ def lib():
     L.q36moe_ctx_set_stream.argtypes = [vp, vp]
     L.q36moe_ctx_free.argtypes = [vp]
     L.q36moe_ctx_free.restype = None
-    L.q36moe_forward.argtypes = [vp, vp, vp, i, vp, i, vp, i, f, vp, i]
+    L.q36moe_forward.argtypes = [vp, vp, vp, i, vp, i, vp, i, i, f, vp, i]
     L.q36moe_router_topk.argtypes = [vp, i, i, i, i, f, i, vp, vp, vp]
     L.q36moe_router_logits.argtypes = [vp, i, i, vp, i, i, i, i, vp, i, vp, vp]
     L.q36moe_quant_e4m3.argtypes = [vp, i, i, i, vp, vp, vp]
     L.q36moe_add_rmsnorm_quant.argtypes = [vp, vp, vp, i, i, f, vp, vp, vp, vp]
-    L.q36moe_forward_q8.argtypes = [vp, vp, vp, vp, vp, i, vp, i, f, vp, i]
+    L.q36moe_forward_q8.argtypes = [vp, vp, vp, vp, vp, i, vp, i, i, f, vp, i]
     L.q36moe_ctx_copy_tap.argtypes = [vp, i, vp, sz, ctypes.POINTER(sz)]
     L.q36moe_ctx_set_path.argtypes = [vp, i]
     L.q36moe_ctx_last_path.argtypes = [vp]
@@ -112,6 +112,17 @@ def _dev(t, name, dtype=None):
     if dtype is not None and t.dtype != dtype:
         raise Q36MoEError(f"{name} must be {dtype}, got {t.dtype}")
     return ctypes.c_void_p(t.data_ptr())
+
+
+def _shg(shg):
+    """(pointer, element stride) of a [T] f32 GPU tensor of shared-gate
+    logits, which may be a strided view such as column 256 of 257-wide
+    router rows; (None, 0) without one."""
+    if shg is None:
+        return None, 0
+    if not isinstance(shg, torch.Tensor) or not shg.is_cuda or shg.dtype != torch.float32 or shg.dim() != 1:
+        raise Q36MoEError("shg must be a 1-D float32 GPU tensor")
+    return ctypes.c_void_p(shg.data_ptr()), max(1, shg.stride(0)) if shg.numel() > 1 else 1
 
 
 def _host_u8(a):
@@ -293,8 +304,9 @@ class MoELayer:
         check(lib().q36moe_ctx_set_stream(self._h, _stream(stream)), "q36moe_ctx_set_stream")
 
     def forward(self, weights, x, logits, shg=None, scale=1.0, out_dtype=torch.bfloat16, out=None):
-        """x [T, d_model] f32|bf16, logits [T, >=n_expert] f32, shg [T] f32 or
-        None -> out [T, d_model] (bf16 or f32)."""
+        """x [T, d_model] f32|bf16, logits [T, >=n_expert] f32 (row stride
+        free), shg [T] f32 (any stride, e.g. column 256 of 257-wide router
+        rows) or None -> out [T, d_model] (bf16 or f32)."""
         T = x.shape[0]
         xf = FMT_F32 if x.dtype == torch.float32 else FMT_BF16
         if x.dtype not in (torch.float32, torch.bfloat16):
@@ -310,10 +322,10 @@ class MoELayer:
         lp = ctypes.c_void_p(logits.data_ptr()) if T else None
         if T and (not logits.is_cuda or logits.dtype != torch.float32):
             raise Q36MoEError("logits must be a float32 GPU tensor")
-        sp = _dev(shg, "shg", torch.float32) if shg is not None else None
+        sp, sld = _shg(shg)
         xp = _dev(x, "x") if T else None
         op = _dev(out, "out") if T else None
-        check(lib().q36moe_forward(self._h, weights._h, xp, xf, lp, ld, sp, T, float(scale), op, of),
+        check(lib().q36moe_forward(self._h, weights._h, xp, xf, lp, ld, sp, sld, T, float(scale), op, of),
               "q36moe_forward")
         self.last_T = T
         self.last_shared = shg is not None
@@ -328,12 +340,14 @@ class MoELayer:
         of = FMT_F32 if out.dtype == torch.float32 else FMT_BF16
         if logits.dim() != 2 or logits.shape[0] != T or logits.stride(1) != 1:
             raise Q36MoEError("logits must be [T, n_expert] with contiguous rows")
-        lp = _dev(logits, "logits", torch.float32) if T else None
-        sp = _dev(shg, "shg", torch.float32) if shg is not None else None
+        if T and (not logits.is_cuda or logits.dtype != torch.float32):
+            raise Q36MoEError("logits must be a float32 GPU tensor")
+        lp = ctypes.c_void_p(logits.data_ptr()) if T else None
+        sp, sld = _shg(shg)
         qp = _dev(xq, "xq", torch.uint8) if T else None
         sc = _dev(xs, "xs", torch.uint8) if T else None
         op = _dev(out, "out") if T else None
-        check(lib().q36moe_forward_q8(self._h, weights._h, qp, sc, lp, logits.stride(0), sp, T, float(scale),
+        check(lib().q36moe_forward_q8(self._h, weights._h, qp, sc, lp, logits.stride(0), sp, sld, T, float(scale),
                                       op, of), "q36moe_forward_q8")
         self.last_T = T
         self.last_shared = shg is not None
@@ -360,12 +374,12 @@ class MoELayer:
               "q36moe_ctx_copy_tap")
         return dst
 
-    PATH_AUTO, PATH_SORTED, PATH_DIRECT, PATH_DIRECT_FUSED, PATH_SORTED_SKINNY = 0, 1, 2, 3, 4
+    PATH_AUTO, PATH_SORTED, PATH_DIRECT, PATH_SORTED_SKINNY = 0, 1, 2, 4
 
     def set_path(self, mode):
         """0 auto (direct for T <= 16, skinny tiles while T*k <= 8*n_expert),
-        1 sorted (fat tiles), 2 direct (two kernels), 3 direct (one kernel),
-        4 sorted (skinny tiles)."""
+        1 sorted (fat tiles), 2 direct, 4 sorted (skinny tiles); 3 is
+        refused (EINVAL)."""
         check(lib().q36moe_ctx_set_path(self._h, mode), "q36moe_ctx_set_path")
 
     @property
@@ -374,8 +388,7 @@ class MoELayer:
         return lib().q36moe_ctx_last_path(self._h)
 
     def check(self):
-        """Synchronise; raise if a bounded wait of the one-kernel direct
-        path gave up since the last check."""
+        """Synchronise the layer's stream; raise on a HIP error."""
         check(lib().q36moe_ctx_check(self._h), "q36moe_ctx_check")
 
     def set_timing(self, on):

@@ -90,7 +90,7 @@ def test_pack_rejects_bad_args(L):
 
 def test_entry_points_reject_bad_args_without_gpu(L):
     """Validation happens before any HIP call, so these run on a CPU host."""
-    assert L.q36moe_forward(None, None, None, 0, None, 256, None, 1, ctypes.c_float(1.0), None, 0) == -22
+    assert L.q36moe_forward(None, None, None, 0, None, 256, None, 0, 1, ctypes.c_float(1.0), None, 0) == -22
     assert L.q36moe_router_topk(None, 4, 300, 300, 8, ctypes.c_float(1.0), 1, None, None, None) == -22
     assert L.q36moe_router_topk(None, 4, 256, 256, 9, ctypes.c_float(1.0), 1, None, None, None) == -22
     assert L.q36moe_router_topk(None, 0, 256, 256, 8, ctypes.c_float(1.0), 1, None, None, None) == 0
@@ -106,7 +106,7 @@ def test_entry_points_reject_bad_args_without_gpu(L):
     assert arq(None, None, None, 4, 2048, ctypes.c_float(-1.0), None, None, None, None) == -22  # eps
     assert arq(None, None, None, 4, 2048, ctypes.c_float(1e-6), None, None, ctypes.c_void_p(8), None) == -22  # xq w/o xs
     assert arq(None, None, None, 0, 2048, ctypes.c_float(1e-6), None, None, None, None) == 0
-    assert L.q36moe_forward_q8(None, None, None, None, None, 256, None, 1, ctypes.c_float(1.0), None, 0) == -22
+    assert L.q36moe_forward_q8(None, None, None, None, None, 256, None, 0, 1, ctypes.c_float(1.0), None, 0) == -22
     assert L.q36moe_quant_e4m3(None, 2, 4, 128, None, None, None) == -22
     assert L.q36moe_quant_e4m3(None, 0, 0, 128, None, None, None) == 0
     h = ctypes.c_void_p()

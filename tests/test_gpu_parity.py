@@ -10,10 +10,14 @@
       2. down + combine from the GPU's own h rows vs fp64:
            max relative error  max_i |y_ti - ref_ti| / max_i |ref_ti|   <= 2e-3
            element-wise  |y_ti - ref_ti| / max(|ref_ti|, 0.05 max_i |ref_ti|) <= 2e-3
-      3. end to end vs the fp64 oracle, reported; asserted only as a gross
-         error backstop (<= 1e-2): a single midpoint flip of a large h code
-         (up to 1/16 of the value) moves outputs by up to ~2e-3 of the row
-         max, so stages 1+2 carry the 2e-3 bar on identical quantised inputs;
+      3. end to end vs the fp64 oracle, the same two 2e-3 bars, per token:
+         a token none of whose h rows has a midpoint flip is held against
+         the plain oracle (q36moe_oracle.c, its own fp64 path); a token with
+         flips against the oracle with the GPU's code substituted at each
+         flipped element only (everything else of that reference is the
+         oracle's own arithmetic; stage 1 has shown every other code equal),
+         because one legitimate flip of a large h code (up to 1/16 of the
+         value) moves outputs by up to ~2e-3 of the row max;
     an element-wise bound needs the floor near zero, and bf16's own half-ulp
     is up to 2^-8 relative, above 2e-3, so the bars apply to the fp32 result;
   * bf16 output: the RNE bf16 rounding of the f32 output, bit for bit.
@@ -251,10 +255,13 @@ def _check_h_rows(oracle, w, x, gi, perm, hq, hs, rows, n_expert=256, k=8):
     E8M0 scales equal the oracle's quantisation of fp32(h), except codes whose
     fp64 value lies within 1e-4 * blockmax of a rounding midpoint (fp32 vs
     fp64 accumulation order) and scales whose block amax lies within 1e-4 of a
-    power-of-two boundary.  Returns the number of such flips."""
+    power-of-two boundary.  Returns {row: (flips, codes, scales)}: the number
+    of such flips in the row and the oracle's codes / scales of the row with
+    the GPU's value substituted at each flipped element (a flipped scale
+    substitutes its block)."""
     xq, xs = oracle.quant_e4m3(x)
     xd = oracle.dequant_e4m3(xq, xs)
-    flips = 0
+    out = {}
     T = x.shape[0]
     for p in rows:
         if p < T * k:
@@ -265,21 +272,26 @@ def _check_h_rows(oracle, w, x, gi, perm, hq, hs, rows, n_expert=256, k=8):
             t = p - T * k
             hg = oracle.expert_h(w["sh_gate"], w["sh_up"], xd[t])
         oq, os_ = oracle.quant_e4m3(hg.astype(np.float32)[None])
+        oq, os_ = oq[0].copy(), os_[0].copy()
+        flips = 0
         for b in range(hg.size // 32):
             sl = slice(32 * b, 32 * b + 32)
-            if hs[p, b] != os_[0, b]:
+            if hs[p, b] != os_[b]:
                 amax = np.abs(hg[sl]).max() / 448.0
                 rel = abs(amax / 2.0 ** np.round(np.log2(amax)) - 1)
-                assert rel < 1e-4, f"row {p} block {b}: scale {hs[p, b]} vs {os_[0, b]}"
+                assert rel < 1e-4, f"row {p} block {b}: scale {hs[p, b]} vs {os_[b]}"
                 flips += 1
+                os_[b], oq[sl] = hs[p, b], hq[p, sl]
                 continue
-            bad = np.nonzero(hq[p, sl] != oq[0, sl])[0]
+            bad = np.nonzero(hq[p, sl] != oq[sl])[0]
             if bad.size:
-                v = hg[sl] * 2.0 ** -(int(os_[0, b]) - 127)
+                v = hg[sl] * 2.0 ** -(int(os_[b]) - 127)
                 d = _fp8_mid_distance(v[bad])
                 assert np.all(d <= 1e-4 * np.abs(v).max()), f"row {p} block {b}: codes {bad}"
                 flips += bad.size
-    return flips
+                oq[32 * b + bad] = hq[p, 32 * b + bad]
+        out[p] = (flips, oq, os_)
+    return out
 
 
 def _check_layer(name, dev, oracle, layer_w, x, lg, shg, sample=None, x_dtype=torch.float32,
@@ -303,7 +315,8 @@ def _check_layer(name, dev, oracle, layer_w, x, lg, shg, sample=None, x_dtype=to
     rows = [int(pos[t * 8 + s]) for t in toks for s in range(8)]
     if shg is not None:
         rows += [T * 8 + int(t) for t in toks]
-    flips = _check_h_rows(oracle, w, x, gi, perm, hq, hs, rows)
+    hrows = _check_h_rows(oracle, w, x, gi, perm, hq, hs, rows)
+    flips = sum(v[0] for v in hrows.values())
     # stage 2: down + combine from the GPU's own h
     _, ow = oracle.router_topk(lg, 8)
     ref_h = np.zeros((toks.size, x.shape[1]))
@@ -317,24 +330,43 @@ def _check_layer(name, dev, oracle, layer_w, x, lg, shg, sample=None, x_dtype=to
             hd = oracle.dequant_e4m3(hq[p:p + 1], hs[p:p + 1])[0]
             ref_h[j] += 1 / (1 + np.exp(-float(shg[t]))) * oracle.expert_down(w["sh_down"], hd)
     el_h, norm_h = _row_err(y32[toks], ref_h)
-    # stage 3: end to end against the full fp64 oracle
+    # stage 3: end to end, per token: the plain fp64 oracle for tokens without
+    # flips, the oracle with the flipped codes substituted for the others
     ref = oracle.moe_forward(w, x, lg, shg, tokens=toks)
-    el, normwise = _row_err(y32[toks], ref)
-    _, bf16_norm = _row_err(y16[toks], ref)
+    tok_rows = {int(t): [int(pos[t * 8 + s]) for s in range(8)] + ([T * 8 + int(t)] if shg is not None else [])
+                for t in toks}
+    ref_sub = ref.copy()
+    n_flipped_tok = 0
+    for j, t in enumerate(toks):
+        if sum(hrows[p][0] for p in tok_rows[int(t)]) == 0:
+            continue
+        n_flipped_tok += 1
+        ref_sub[j] = 0.0
+        for s in range(8):
+            p = int(pos[t * 8 + s])
+            hd = oracle.dequant_e4m3(hrows[p][1][None], hrows[p][2][None])[0]
+            ref_sub[j] += ow[t, s] * oracle.expert_down(w["down"][gi[t, s]], hd)
+        if shg is not None:
+            p = T * 8 + int(t)
+            hd = oracle.dequant_e4m3(hrows[p][1][None], hrows[p][2][None])[0]
+            ref_sub[j] += 1 / (1 + np.exp(-float(shg[t]))) * oracle.expert_down(w["sh_down"], hd)
+    el, normwise = _row_err(y32[toks], ref_sub)
+    _, raw_norm = _row_err(y32[toks], ref)
+    _, bf16_norm = _row_err(y16[toks], ref_sub)
     ref32 = oracle.moe_forward(w, x, lg, shg, act_mode=1, tokens=toks)
     drift = float(np.abs(ref32 - ref).max() / np.abs(ref).max())
     _metrics(name, T=int(T), tokens_checked=int(toks.size), h_rows=len(rows), h_flips=int(flips),
-             stage2_max_rel=norm_h, stage2_elementwise=el_h, e2e_max_rel=normwise,
-             e2e_elementwise=el, bf16_max_rel=bf16_norm, distinct_experts=int(np.unique(gi).size),
-             w4a32_drift=drift)
+             tokens_with_flips=n_flipped_tok, stage2_max_rel=norm_h, stage2_elementwise=el_h,
+             e2e_max_rel=normwise, e2e_elementwise=el, e2e_unsubstituted_max_rel=raw_norm,
+             bf16_max_rel=bf16_norm, distinct_experts=int(np.unique(gi).size), w4a32_drift=drift)
     assert flips <= 0.01 * len(rows) * hq.shape[1]
     assert norm_h <= TOL and el_h <= TOL, f"{name}: down/combine error {norm_h:.3g} / {el_h:.3g}"
-    assert normwise <= 1e-2, f"{name}: end-to-end max relative error {normwise:.3g}"
+    assert normwise <= TOL and el <= TOL, f"{name}: end-to-end error {normwise:.3g} / {el:.3g}"
     return layer
 
 
 PATHS = [pytest.param(1, id="sorted"), pytest.param(4, id="sorted_skinny"),
-         pytest.param(2, id="direct"), pytest.param(3, id="direct_fused")]
+         pytest.param(2, id="direct")]
 
 
 @pytest.mark.parametrize("path", PATHS)
@@ -366,29 +398,6 @@ def test_forward_small_batches(dev, oracle, layer_w, T, path):
     rng = np.random.default_rng(300 + T)
     x, lg = synth.hidden(rng, T), synth.normal_logits(rng, T)
     _check_layer(f"small{T}", dev, oracle, layer_w, x, lg, None, path=path)
-
-
-def test_fused_decode_repeated_calls(dev, layer_w):
-    """The one-kernel direct path over 40 back-to-back calls of varying T
-    (its wait counters must reset themselves) equals the two-kernel direct
-    path bit for bit."""
-    _, dw = layer_w
-    rng = np.random.default_rng(4242)
-    fused, two = moe.MoELayer(16), moe.MoELayer(16)
-    fused.set_path(3)
-    two.set_path(2)
-    xs, ls, ys = [], [], []
-    for c in range(40):
-        T = int(rng.integers(1, 17))
-        x = torch.from_numpy(synth.hidden(rng, T)).to(dev)
-        lg = torch.from_numpy(synth.normal_logits(rng, T)).to(dev)
-        xs.append(x)
-        ls.append(lg)
-        ys.append(fused.forward(dw, x, lg, out_dtype=torch.float32))
-    fused.check()
-    for x, lg, y in zip(xs, ls, ys):
-        assert torch.equal(y, two.forward(dw, x, lg, out_dtype=torch.float32))
-    two.check()
 
 
 @pytest.mark.parametrize("path", [pytest.param(0, id="auto"), pytest.param(1, id="sorted")])
@@ -600,7 +609,7 @@ def test_add_rmsnorm_quant(dev, oracle, T, with_a):
     np.testing.assert_array_equal(xs.cpu().numpy(), os_)
 
 
-@pytest.mark.parametrize("T,path", [(1, 0), (5, 2), (5, 3), (40, 4), (40, 1), (600, 0)])
+@pytest.mark.parametrize("T,path", [(1, 0), (5, 2), (40, 4), (40, 1), (600, 0)])
 def test_forward_q8_equals_forward(dev, layer_w, T, path):
     """The pre-quantised entry gives bit-identical results (outputs and
     routing/quantisation taps) to forward on the x it was quantised from, on
@@ -620,3 +629,33 @@ def test_forward_q8_equals_forward(dev, layer_w, T, path):
     np.testing.assert_array_equal(ya.cpu().numpy(), yb.cpu().numpy())
     for tap in (moe.TAP_TOPK_IDX, moe.TAP_XQ, moe.TAP_XS, moe.TAP_HQ):
         np.testing.assert_array_equal(la.tap(tap).cpu().numpy(), lb.tap(tap).cpu().numpy())
+
+
+@pytest.mark.parametrize("T,path", [(1, 2), (5, 2), (40, 4), (600, 1)])
+def test_forward_strided_shared_gate(dev, layer_w, T, path):
+    """The reference's batched decode keeps the shared-gate logit in column
+    256 of each 257-wide router row (q36_engine.cu:2092-2095): forward takes
+    logits = rows[:, :256] and shg = rows[:, 256] (stride 257) directly and
+    gives the same bits as the gathered contiguous copy, on the direct, skinny
+    and fat paths."""
+    _, dw = layer_w
+    rng = np.random.default_rng(1200 + T)
+    rows = np.concatenate([synth.normal_logits(rng, T), rng.standard_normal((T, 1)).astype(np.float32)], axis=1)
+    x = torch.from_numpy(synth.hidden(rng, T)).to(dev)
+    rt = torch.from_numpy(np.ascontiguousarray(rows)).to(dev)
+    la, lb = moe.MoELayer(T), moe.MoELayer(T)
+    la.set_path(path)
+    lb.set_path(path)
+    ya = la.forward(dw, x, rt[:, :256], rt[:, 256], out_dtype=torch.float32)
+    yb = lb.forward(dw, x, rt[:, :256].contiguous(), rt[:, 256].contiguous(), out_dtype=torch.float32)
+    xq, xs = moe.quant_e4m3(x)
+    yc = moe.MoELayer(T).forward_q8(dw, xq, xs, rt[:, :256], rt[:, 256], out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert rt[:, 256].stride(0) == 257
+    np.testing.assert_array_equal(ya.cpu().numpy(), yb.cpu().numpy())
+    # the automatic path of these sizes is the forced one
+    np.testing.assert_array_equal(ya.cpu().numpy(), yc.cpu().numpy())
+    # and the shared expert is really in the sum
+    yn = moe.MoELayer(T).forward(dw, x, rt[:, :256].contiguous(), None, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert not torch.equal(ya, yn)

@@ -12,7 +12,10 @@ product's host requantiser and packer against it bit for bit.  GPU tests
 (marked gpu) run the layer through the C ABI on every path, with the bars of
 test_gpu_parity.py: int8 h codes equal the oracle's quantisation of fp32(h)
 except at rounding midpoints; down + combine from the GPU's own h within
-2e-3 of fp64; end to end within 1e-2.
+2e-3 of fp64; end to end within 2e-3 per token (against the plain oracle, or
+with the GPU's codes substituted at the flipped elements of a token that has
+midpoint flips).  The Q8_0 shared-expert tests check the shared row's codes
+only, so their end-to-end figure keeps a 1e-2 backstop.
 """
 import ctypes
 
@@ -385,6 +388,8 @@ def _check_q8_layer(oracle, q8_layer, x, lg, shg, path, sample=None):
     xd = oracle.dequant_e4m3(xq, xs)
     flips = 0
     ref_h = np.zeros((toks.size, x.shape[1]))
+    ref_sub = np.zeros((toks.size, x.shape[1]))   # oracle h codes, the GPU's at flips
+    tok_flips = np.zeros(toks.size, dtype=np.int64)
     for j, t in enumerate(toks):
         for s in range(k):
             p, e = int(pos[t * k + s]), int(gi[t, s])
@@ -400,6 +405,11 @@ def _check_q8_layer(oracle, q8_layer, x, lg, shg, path, sample=None):
                 assert np.all(np.abs(np.abs(v - np.floor(v)) - 0.5) <= 127e-4), f"token {t} slot {s}: codes {bad}"
                 assert np.all(np.abs(hq[p, bad].astype(np.int64) - oq[bad]) == 1)
                 flips += bad.size
+                tok_flips[j] += bad.size
+            sub = oq.astype(np.float64)
+            sub[bad] = hq[p, bad]
+            ref_sub[j] += ow[t, s] * oracle.expert_down_q8(w["down_q8"][e], w["down_q8d"][e],
+                                                           sub * np.repeat(od.astype(np.float64), 32))
             # stage 2: down from the GPU's own int8 h
             hd = hq[p].astype(np.float64) * np.repeat(hsf[p].astype(np.float64), 32)
             ref_h[j] += ow[t, s] * oracle.expert_down_q8(w["down_q8"][e], w["down_q8d"][e], hd)
@@ -407,12 +417,21 @@ def _check_q8_layer(oracle, q8_layer, x, lg, shg, path, sample=None):
             p = T * k + int(t)
             hd = oracle.dequant_e4m3(hq[p:p + 1].view(np.uint8), hs[p:p + 1])[0]
             ref_h[j] += 1 / (1 + np.exp(-float(shg[t]))) * oracle.expert_down(w["sh_down"], hd)
+            ref_sub[j] += 1 / (1 + np.exp(-float(shg[t]))) * oracle.expert_down(w["sh_down"], hd)
     el_h, norm_h = _row_err(y32[toks], ref_h)
+    # end to end: tokens without flipped routed h codes against the plain
+    # oracle; the others against the oracle with the GPU's codes at the flips
+    # (the shared expert's MXFP4 h is the GPU's in both; its parity is held by
+    # the MXFP4 layer tests)
     ref = oracle.moe_forward(_oracle_w(w), x, lg, shg, tokens=toks.astype(np.int32))
-    _, e2e = _row_err(y32[toks], ref)
+    if shg is not None:
+        ref = ref_sub.copy()
+    else:
+        ref[tok_flips > 0] = ref_sub[tok_flips > 0]
+    el, e2e = _row_err(y32[toks], ref)
     assert flips <= 0.01 * toks.size * k * 512
     assert norm_h <= TOL and el_h <= TOL, f"down/combine error {norm_h:.3g} / {el_h:.3g}"
-    assert e2e <= 1e-2, f"end-to-end max relative error {e2e:.3g}"
+    assert e2e <= TOL and el <= TOL, f"end-to-end error {e2e:.3g} / {el:.3g}"
     return layer
 
 
@@ -442,7 +461,7 @@ def test_forward_q8_down_zipf_ragged(oracle, q8_layer):
 
 
 @pytest.mark.gpu
-def test_q8_down_path3_and_replay_format_checks(q8_layer):
+def test_q8_down_path_and_replay_format_checks(q8_layer):
     import torch
     from q36_amd import moe
     w, dw = q8_layer
@@ -450,10 +469,8 @@ def test_q8_down_path3_and_replay_format_checks(q8_layer):
     x = torch.from_numpy(synth.hidden(rng, 2)).cuda()
     lg = torch.from_numpy(synth.normal_logits(rng, 2)).cuda()
     layer = moe.MoELayer(4)
-    layer.set_path(3)       # the one-kernel decode is MXFP4-only
     with pytest.raises(moe.Q36MoEError):
-        layer.forward(dw, x, lg)
-    layer.set_path(0)
+        layer.set_path(3)   # the one-kernel decode mode no longer exists
     layer.forward(dw, x, lg)
     # a plan made for a q8 down does not replay over MXFP4 weights
     mx = moe.MoEWeights.upload(w["gate"], w["up"], synth.expert_weights(2027)["down"])
@@ -618,9 +635,6 @@ def test_q8_shared_refusals(q8_shared_layer):
     with pytest.raises(moe.Q36MoEError):     # int8 x needs the unquantised input
         layer.forward_q8(dw, xq, xs, lg, shg)
     layer.forward_q8(dw, xq, xs, lg)          # without the shared expert it is fine
-    layer.set_path(3)
-    with pytest.raises(moe.Q36MoEError):
-        layer.forward(dw, x, lg, shg)
     torch.cuda.synchronize()
 
 
