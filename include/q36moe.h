@@ -180,6 +180,21 @@ int q36moe_forward(q36moe_ctx *c, const q36moe_weights *w,
                    const void *x, int x_fmt, const float *logits, int ld_logits,
                    const float *shg, int ld_shg, int T, float scale, void *out, int out_fmt);
 
+/* q36moe_forward without a context and without allocating anything: the
+ * scratch is a static device array in the library (8 MiB per GPU it runs
+ * on, held until the process ends), so a caller that cannot allocate -- code
+ * under HIP graph capture, a tight serving loop, a harness that forbids
+ * hipMalloc -- can still run the layer.  No counterpart in the reference
+ * (its engine allocates once at create time).  Same arguments and result as
+ * q36moe_forward on a context with top_k and the automatic path, for T <=
+ * 64 tokens (larger T: EINVAL); asynchronous on `stream`.  Every call on a
+ * GPU shares that GPU's array: calls that overlap on one GPU (two streams,
+ * two threads) race and must be serialised by the caller.  No tap or replay
+ * reads this scratch. */
+int q36moe_forward_noalloc(const q36moe_weights *w, const void *x, int x_fmt, const float *logits, int ld_logits,
+                           const float *shg, int ld_shg, int T, int top_k, float scale, void *out, int out_fmt,
+                           void *stream);
+
 /* Stage entry points (device pointers, asynchronous on `stream`). */
 int q36moe_router_topk(const float *logits, int T, int n_expert, int ld, int k,
                        float scale, int renorm, int32_t *idx, float *wt, void *stream);

@@ -34,6 +34,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <atomic>
+#include <mutex>
 #include <new>
 #include <thread>
 #include <type_traits>
@@ -2072,16 +2073,15 @@ struct Plan {
     const void *out; int out_fmt;
 };
 
-struct q36moe_ctx {
-    int dev;
-    hipStream_t stream;
+// Device scratch of one forward for up to max_T tokens, carved from one
+// base address (a context's allocation, or the library's static array for
+// q36moe_forward_noalloc).  No kernel relies on its contents at entry.
+struct Scratch {
     int max_T, E, D, FF, K;
     int nb_max;
     size_t tile_cap;
-    void *base;
     int32_t *topk_idx; float *topk_w; int32_t *rank;
     uint8_t *xq, *xs, *xs2;
-    const uint8_t *tap_xq, *tap_xs;   // where the last forward's quantised x is
     int32_t *blk_cnt, *blk_off, *tot, *e_off, *perm, *pos, *row_tok;
     float *row_w;
     int4 *tiles; int32_t *ntiles;
@@ -2090,6 +2090,14 @@ struct q36moe_ctx {
     int8_t *xq8; float *xsf;        // int8 x + fp32 scales (q8_0-split shared expert, sorted path)
     float *dnw;
     float *hf;                      // direct path: fp32 SwiGLU rows
+};
+
+struct q36moe_ctx {
+    int dev;
+    hipStream_t stream;
+    Scratch s;
+    void *base;
+    const uint8_t *tap_xq, *tap_xs;   // where the last forward's quantised x is
     int path_mode;                  // 0 auto, 1 sorted (fat tiles), 2 direct, 4 sorted (skinny tiles)
     int last_T, last_sh, last_path;
     int timing;
@@ -2150,6 +2158,86 @@ size_t type_row_bytes(int t, int K) {
     return 0;
 }
 
+
+// Lays out the scratch of one forward for up to max_T tokens from `base`
+// (or only sizes it when base is null); returns the bytes it spans.
+size_t carve_scratch(uint8_t *base, int max_T, int E, int D, int FF, int K, Scratch *S) {
+    Scratch z{};
+    Scratch &c = S ? *S : z;
+    c.max_T = max_T; c.E = E; c.D = D; c.FF = FF; c.K = K;
+    c.nb_max = (max_T + kRouteTPBSmall - 1) / kRouteTPBSmall;
+    const size_t n = (size_t)max_T * K;
+    const size_t rows = n + max_T;            // routed entries + shared rows
+    c.tile_cap = n / 16 + (size_t)(n < (size_t)E ? n : E) + (max_T + 15) / 16 + 16;
+    size_t off = 0;
+    auto take = [&off](size_t bytes) { size_t o = off; off = align256(off + bytes); return o; };
+    const size_t o_idx = take(n * 4), o_w = take(n * 4), o_rank = take(n * 4);
+    const size_t o_xq = take((size_t)max_T * D), o_xs = take((size_t)max_T * D / 32);
+    const size_t o_xs2 = take((size_t)max_T * D / 32);
+    const size_t o_bc = take((size_t)c.nb_max * E * 4), o_bo = take((size_t)c.nb_max * E * 4);
+    const size_t o_tot = take((size_t)E * 4);
+    const size_t o_eo = take((size_t)(E + 1) * 4), o_perm = take(n * 4), o_pos = take(n * 4);
+    const size_t o_rt = take(rows * 4), o_rw = take(rows * 4);
+    const size_t o_tiles = take(c.tile_cap * 16), o_nt = take(4);
+    const size_t o_hq = take(rows * FF), o_hs = take(rows * FF / 32), o_hs2 = take(rows * FF / 32);
+    const size_t o_hsf = take(rows * FF / 32 * 4);
+    const size_t o_xq8 = take((size_t)max_T * D), o_xsf = take((size_t)max_T * D / 32 * 4);
+    const size_t o_dnw = take(rows * D * 4);
+    const size_t direct_rows = (size_t)(max_T < kDirectMaxT ? max_T : kDirectMaxT) * (K + 1);
+    const size_t o_hf = take(direct_rows * FF * 4);
+    if (!base) return off;
+    uint8_t *b = base;
+    c.topk_idx = reinterpret_cast<int32_t *>(b + o_idx);
+    c.topk_w = reinterpret_cast<float *>(b + o_w);
+    c.rank = reinterpret_cast<int32_t *>(b + o_rank);
+    c.xq = b + o_xq; c.xs = b + o_xs; c.xs2 = b + o_xs2;
+    c.blk_cnt = reinterpret_cast<int32_t *>(b + o_bc);
+    c.blk_off = reinterpret_cast<int32_t *>(b + o_bo);
+    c.tot = reinterpret_cast<int32_t *>(b + o_tot);
+    c.e_off = reinterpret_cast<int32_t *>(b + o_eo);
+    c.perm = reinterpret_cast<int32_t *>(b + o_perm);
+    c.pos = reinterpret_cast<int32_t *>(b + o_pos);
+    c.row_tok = reinterpret_cast<int32_t *>(b + o_rt);
+    c.row_w = reinterpret_cast<float *>(b + o_rw);
+    c.tiles = reinterpret_cast<int4 *>(b + o_tiles);
+    c.ntiles = reinterpret_cast<int32_t *>(b + o_nt);
+    c.hq = b + o_hq; c.hs = b + o_hs; c.hs2 = b + o_hs2;
+    c.hsf = reinterpret_cast<float *>(b + o_hsf);
+    c.xq8 = reinterpret_cast<int8_t *>(b + o_xq8);
+    c.xsf = reinterpret_cast<float *>(b + o_xsf);
+    c.dnw = reinterpret_cast<float *>(b + o_dnw);
+    c.hf = reinterpret_cast<float *>(b + o_hf);
+    return off;
+}
+
+// Scratch of q36moe_forward_noalloc: one static array per GPU, sized for
+// kNoAllocMaxT tokens of the q36 shape (256 experts, top-8, d_model 2048,
+// d_ff 512: about 5.7 MB of the 8 MiB).  In host code `scratch` names a
+// host-side stand-in, not device memory: the device address of each GPU's
+// copy is looked up once per device (hipGetSymbolAddress, with that device
+// current) and only that address is handed to kernels.
+constexpr int kNoAllocMaxT = 64;
+constexpr size_t kNoAllocBytes = (size_t)8 << 20;
+constexpr int kNoAllocMaxDev = 64;
+__device__ __align__(256) uint8_t scratch[kNoAllocBytes];
+
+std::mutex g_noalloc_mu;
+uint8_t *g_noalloc_ptr[kNoAllocMaxDev];
+
+// Device address of this GPU's scratch array (looked up on first use).
+int noalloc_scratch(uint8_t **out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return Q36MOE_EHIP;
+    if (dev < 0 || dev >= kNoAllocMaxDev) return Q36MOE_EINVAL;
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    if (!g_noalloc_ptr[dev]) {
+        void *p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return Q36MOE_EHIP;
+        g_noalloc_ptr[dev] = static_cast<uint8_t *>(p);
+    }
+    *out = g_noalloc_ptr[dev];
+    return Q36MOE_OK;
+}
 
 }  // namespace
 
@@ -2320,53 +2408,13 @@ int q36moe_ctx_create(int max_tokens, int n_expert, int d_model, int d_ff, int t
         return Q36MOE_EHIP;
     }
     c->stream = static_cast<hipStream_t>(stream);
-    c->max_T = max_tokens; c->E = n_expert; c->D = d_model; c->FF = d_ff; c->K = top_k;
-    c->nb_max = (max_tokens + kRouteTPBSmall - 1) / kRouteTPBSmall;
-    const size_t n = (size_t)max_tokens * top_k;
-    const size_t rows = n + max_tokens;            // routed entries + shared rows
-    c->tile_cap = n / 16 + (size_t)(n < (size_t)n_expert ? n : n_expert) + (max_tokens + 15) / 16 + 16;
-    size_t off = 0;
-    auto take = [&off](size_t bytes) { size_t o = off; off = align256(off + bytes); return o; };
-    const size_t o_idx = take(n * 4), o_w = take(n * 4), o_rank = take(n * 4);
-    const size_t o_xq = take((size_t)max_tokens * d_model), o_xs = take((size_t)max_tokens * d_model / 32);
-    const size_t o_xs2 = take((size_t)max_tokens * d_model / 32);
-    const size_t o_bc = take((size_t)c->nb_max * n_expert * 4), o_bo = take((size_t)c->nb_max * n_expert * 4);
-    const size_t o_tot = take((size_t)n_expert * 4);
-    const size_t o_eo = take((size_t)(n_expert + 1) * 4), o_perm = take(n * 4), o_pos = take(n * 4);
-    const size_t o_rt = take(rows * 4), o_rw = take(rows * 4);
-    const size_t o_tiles = take(c->tile_cap * 16), o_nt = take(4);
-    const size_t o_hq = take(rows * d_ff), o_hs = take(rows * d_ff / 32), o_hs2 = take(rows * d_ff / 32);
-    const size_t o_hsf = take(rows * d_ff / 32 * 4);
-    const size_t o_xq8 = take((size_t)max_tokens * d_model), o_xsf = take((size_t)max_tokens * d_model / 32 * 4);
-    const size_t o_dnw = take(rows * d_model * 4);
-    const size_t direct_rows = (size_t)(max_tokens < kDirectMaxT ? max_tokens : kDirectMaxT) * (top_k + 1);
-    const size_t o_hf = take(direct_rows * d_ff * 4);
-    if (hipMalloc(&c->base, off) != hipSuccess) {
+    const size_t bytes = carve_scratch(nullptr, max_tokens, n_expert, d_model, d_ff, top_k, nullptr);
+    if (hipMalloc(&c->base, bytes) != hipSuccess) {
         delete c;
         return Q36MOE_ENOMEM;
     }
-    uint8_t *b = static_cast<uint8_t *>(c->base);
-    c->topk_idx = reinterpret_cast<int32_t *>(b + o_idx);
-    c->topk_w = reinterpret_cast<float *>(b + o_w);
-    c->rank = reinterpret_cast<int32_t *>(b + o_rank);
-    c->xq = b + o_xq; c->xs = b + o_xs; c->xs2 = b + o_xs2;
-    c->tap_xq = c->xq; c->tap_xs = c->xs;
-    c->blk_cnt = reinterpret_cast<int32_t *>(b + o_bc);
-    c->blk_off = reinterpret_cast<int32_t *>(b + o_bo);
-    c->tot = reinterpret_cast<int32_t *>(b + o_tot);
-    c->e_off = reinterpret_cast<int32_t *>(b + o_eo);
-    c->perm = reinterpret_cast<int32_t *>(b + o_perm);
-    c->pos = reinterpret_cast<int32_t *>(b + o_pos);
-    c->row_tok = reinterpret_cast<int32_t *>(b + o_rt);
-    c->row_w = reinterpret_cast<float *>(b + o_rw);
-    c->tiles = reinterpret_cast<int4 *>(b + o_tiles);
-    c->ntiles = reinterpret_cast<int32_t *>(b + o_nt);
-    c->hq = b + o_hq; c->hs = b + o_hs; c->hs2 = b + o_hs2;
-    c->hsf = reinterpret_cast<float *>(b + o_hsf);
-    c->xq8 = reinterpret_cast<int8_t *>(b + o_xq8);
-    c->xsf = reinterpret_cast<float *>(b + o_xsf);
-    c->dnw = reinterpret_cast<float *>(b + o_dnw);
-    c->hf = reinterpret_cast<float *>(b + o_hf);
+    carve_scratch(static_cast<uint8_t *>(c->base), max_tokens, n_expert, d_model, d_ff, top_k, &c->s);
+    c->tap_xq = c->s.xq; c->tap_xs = c->s.xs;
     for (int i = 0; i <= ST_COUNT; i++) {
         if (hipEventCreate(&c->ev[i]) != hipSuccess) {
             for (int j = 0; j < i; j++) (void)hipEventDestroy(c->ev[j]);
@@ -2410,8 +2458,8 @@ static void bind_weights(Plan &P, const q36moe_weights *w) {
 // Launches the kernels of one stage (direct path: ST_GATEUP is the routing +
 // gate/up kernel, ST_DOWN the down + combine kernel; its other stages are
 // empty).
-static void launch_stage(const q36moe_ctx *c, const Plan &P, int st, hipStream_t s) {
-    const int T = P.T, K = c->K, D = c->D, FF = c->FF;
+static void launch_stage(const Scratch &c, const Plan &P, int st, hipStream_t s) {
+    const int T = P.T, K = c.K, D = c.D, FF = c.FF;
     if (P.direct) {
         const int n = T * K + (P.has_sh ? T : 0);
         if (st == ST_GATEUP) {
@@ -2446,7 +2494,7 @@ static void launch_stage(const q36moe_ctx *c, const Plan &P, int st, hipStream_t
             break;
         case ST_SCAN:
             if (!P.sa.inline_cols)
-                hipLaunchKernelGGL(k_colscan, dim3((c->E + kColExp - 1) / kColExp), dim3(256), 0, s, P.sa);
+                hipLaunchKernelGGL(k_colscan, dim3((c.E + kColExp - 1) / kColExp), dim3(256), 0, s, P.sa);
             hipLaunchKernelGGL(k_scatter, dim3(P.nb), dim3(256), 0, s, P.sa);
             break;
         case ST_GATEUP:
@@ -2468,7 +2516,7 @@ static void launch_stage(const q36moe_ctx *c, const Plan &P, int st, hipStream_t
                                    s, P.da);
             break;
         case ST_COMBINE:
-            hipLaunchKernelGGL(k_combine, dim3(T), dim3(256), 0, s, c->dnw, c->pos, T, K, D, P.has_sh,
+            hipLaunchKernelGGL(k_combine, dim3(T), dim3(256), 0, s, c.dnw, c.pos, T, K, D, P.has_sh,
                                const_cast<void *>(P.out), P.out_fmt);
             break;
         default: break;
@@ -2478,7 +2526,7 @@ static void launch_stage(const q36moe_ctx *c, const Plan &P, int st, hipStream_t
 int q36moe_ctx_replay(q36moe_ctx *c, const q36moe_weights *w, int stage) {
     if (!c || !w || stage < 0 || stage >= ST_COUNT) return Q36MOE_EINVAL;
     if (c->last_T <= 0) return Q36MOE_EINVAL;
-    if (w->E != c->E || w->D != c->D || w->FF != c->FF) return Q36MOE_EINVAL;
+    if (w->E != c->s.E || w->D != c->s.D || w->FF != c->s.FF) return Q36MOE_EINVAL;
     if (c->plan->has_sh && !w->sh_gate) return Q36MOE_EINVAL;
     // the plan's h quantisation matches the down format it was made for
     if ((c->plan->direct ? c->plan->di.dn_q8 : c->plan->da.hq8) != w->dn_q8) return Q36MOE_EINVAL;
@@ -2486,34 +2534,35 @@ int q36moe_ctx_replay(q36moe_ctx *c, const q36moe_weights *w, int stage) {
         return Q36MOE_EINVAL;
     Plan P = *c->plan;
     bind_weights(P, w);
-    launch_stage(c, P, stage, c->stream);
+    launch_stage(c->s, P, stage, c->stream);
     return hipGetLastError() == hipSuccess ? Q36MOE_OK : Q36MOE_EHIP;
 }
 
+// Plans one forward on scratch c and launches its kernels on stream s
+// (events ev[0..ST_COUNT] around the stages when ev is non-null).
 // x_fmt: Q36MOE_FMT_F32 / _BF16, or kFmtE4M3 with x the codes and xs_in the
-// scales of already quantised activations
-static int forward_impl(q36moe_ctx *c, const q36moe_weights *w, const void *x, int x_fmt,
-                        const uint8_t *xs_in, const float *logits, int ld_logits, const float *shg,
-                        int ld_shg, int T, float scale, void *out, int out_fmt) {
-    if (!c || !w || T < 0 || T > c->max_T) return Q36MOE_EINVAL;
-    if (w->E != c->E || w->D != c->D || w->FF != c->FF) return Q36MOE_EINVAL;
+// scales of already quantised activations.
+static int launch_forward(const Scratch &c, Plan &P, int pm, const q36moe_weights *w, const void *x, int x_fmt,
+                          const uint8_t *xs_in, const float *logits, int ld_logits, const float *shg,
+                          int ld_shg, int T, float scale, void *out, int out_fmt, hipStream_t s,
+                          hipEvent_t *ev) {
+    if (!w || T < 0 || T > c.max_T) return Q36MOE_EINVAL;
+    if (w->E != c.E || w->D != c.D || w->FF != c.FF) return Q36MOE_EINVAL;
     if (out_fmt != Q36MOE_FMT_F32 && out_fmt != Q36MOE_FMT_BF16) return Q36MOE_EINVAL;
     // kernels are instantiated for the q36 shape (q36.h:78-84)
-    if (c->D != 2048 || c->FF != 512) return Q36MOE_EINVAL;
+    if (c.D != 2048 || c.FF != 512) return Q36MOE_EINVAL;
     if (T == 0) return Q36MOE_OK;
-    if (!x || !logits || !out || ld_logits < c->E) return Q36MOE_EINVAL;
+    if (!x || !logits || !out || ld_logits < c.E) return Q36MOE_EINVAL;
     if (x_fmt == kFmtE4M3 && !xs_in) return Q36MOE_EINVAL;
     if (shg && !w->sh_gate) return Q36MOE_EINVAL;
     if (ld_shg < 0) return Q36MOE_EINVAL;
     if (ld_shg == 0) ld_shg = 1;
     const int has_sh = shg != nullptr;
-    const int E = c->E, D = c->D, FF = c->FF, K = c->K;
+    const int E = c.E, D = c.D, FF = c.FF, K = c.K;
     const int n = T * K;
     const int tpb = T <= kRouteSmallT ? kRouteTPBSmall : kRouteTPB;
     const int nb = (T + tpb - 1) / tpb;
-    hipStream_t s = c->stream;
 
-    const int pm = c->path_mode;
     const bool direct = pm == 2 ? (T <= kDirectMaxT) : (pm == 1 || pm == 4) ? false : (T <= kDirectMaxT);
     if (pm == 2 && !direct) return Q36MOE_EINVAL;
     const bool shq8 = has_sh && w->sh_q8;
@@ -2530,56 +2579,66 @@ static int forward_impl(q36moe_ctx *c, const q36moe_weights *w, const void *x, i
     int tiles = n / tn + (n < E ? n : E) + (has_sh ? (T + tn_sh - 1) / tn_sh : 0);
     tiles = (tiles + 7) & ~7;   // whole groups of 8 for the XCD-major tile order
 
-    Plan &P = *c->plan;
     P = Plan{};
     P.T = T; P.has_sh = has_sh; P.direct = direct; P.skinny = skinny;
     P.tiles = tiles; P.nb = nb; P.out = out; P.out_fmt = out_fmt;
     if (direct) {
         P.di = DirectArgs{logits, ld_logits, T, E, K, scale, x, x_fmt, shg, ld_shg,
                           nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0,
-                          c->topk_idx, c->topk_w, c->pos, c->perm, c->xq, c->xs, c->hf,
-                          c->hq, c->hs, out, out_fmt, xs_in, 0, 0, c->hsf};
+                          c.topk_idx, c.topk_w, c.pos, c.perm, c.xq, c.xs, c.hf,
+                          c.hq, c.hs, out, out_fmt, xs_in, 0, 0, c.hsf};
     } else {
         P.ra = RouteArgs{logits, ld_logits, T, E, K, scale, x, x_fmt, D, nb,
-                         c->topk_idx, c->topk_w, c->xq, c->xs, c->xs2, c->blk_cnt, c->rank, xs_in};
-        P.sa = ScanArgs{c->blk_cnt, nb, tpb, nb <= kScanInlineBlocks ? 1 : 0, E, T, K, c->topk_idx, c->topk_w, c->rank, shg, ld_shg, tn, tn_sh,
-                        c->blk_off, c->tot, c->e_off, c->perm, c->pos, c->row_tok, c->row_w, c->tiles,
-                        c->ntiles};
+                         c.topk_idx, c.topk_w, c.xq, c.xs, c.xs2, c.blk_cnt, c.rank, xs_in};
+        P.sa = ScanArgs{c.blk_cnt, nb, tpb, nb <= kScanInlineBlocks ? 1 : 0, E, T, K, c.topk_idx, c.topk_w, c.rank,
+                        shg, ld_shg, tn, tn_sh, c.blk_off, c.tot, c.e_off, c.perm, c.pos, c.row_tok, c.row_w,
+                        c.tiles, c.ntiles};
         GemmArgs &ga = P.ga;
         ga.E = E; ga.M = FF;
-        ga.tiles = c->tiles; ga.ntiles = c->ntiles;
+        ga.tiles = c.tiles; ga.ntiles = c.ntiles;
         // pre-quantised codes are read where the caller left them
-        ga.bq = x_fmt == kFmtE4M3 ? static_cast<const uint8_t *>(x) : c->xq;
-        ga.bs2 = c->xs2; ga.row_tok = c->row_tok; ga.row_w = c->row_w;
-        ga.hq = c->hq; ga.hs = c->hs; ga.hs2 = c->hs2; ga.ldo = FF;
-        ga.hsf = c->hsf;
-        ga.xq8 = c->xq8; ga.xsf = c->xsf; ga.T = T; ga.nrouted = n;
+        ga.bq = x_fmt == kFmtE4M3 ? static_cast<const uint8_t *>(x) : c.xq;
+        ga.bs2 = c.xs2; ga.row_tok = c.row_tok; ga.row_w = c.row_w;
+        ga.hq = c.hq; ga.hs = c.hs; ga.hs2 = c.hs2; ga.ldo = FF;
+        ga.hsf = c.hsf;
+        ga.xq8 = c.xq8; ga.xsf = c.xsf; ga.T = T; ga.nrouted = n;
         ga.sh_wgs = shq8 && !skinny ? (T + kShTok - 1) / kShTok * kShRb : 0;
         GemmArgs &da = P.da;
         da = ga;
         da.M = D;
-        da.bq = c->hq; da.bs2 = c->hs2; da.dnw = c->dnw; da.ldo = D;
-        da.bsf = c->hsf;
+        da.bq = c.hq; da.bs2 = c.hs2; da.dnw = c.dnw; da.ldo = D;
+        da.bsf = c.hsf;
     }
     bind_weights(P, w);
     if (!direct && shq8) {   // k_route also writes the int8 x the shared expert reads
-        P.ra.xq8 = c->xq8;
-        P.ra.xsf = c->xsf;
+        P.ra.xq8 = c.xq8;
+        P.ra.xsf = c.xsf;
     }
     for (int st = 0; st < ST_COUNT; st++) {
-        if (c->timing) (void)hipEventRecord(c->ev[st], s);
+        if (ev) (void)hipEventRecord(ev[st], s);
         launch_stage(c, P, st, s);
     }
-    if (c->timing) (void)hipEventRecord(c->ev[ST_COUNT], s);
+    if (ev) (void)hipEventRecord(ev[ST_COUNT], s);
+    return hipGetLastError() == hipSuccess ? Q36MOE_OK : Q36MOE_EHIP;
+}
+
+static int forward_impl(q36moe_ctx *c, const q36moe_weights *w, const void *x, int x_fmt,
+                        const uint8_t *xs_in, const float *logits, int ld_logits, const float *shg,
+                        int ld_shg, int T, float scale, void *out, int out_fmt) {
+    if (!c) return Q36MOE_EINVAL;
+    Plan P;
+    const int rc = launch_forward(c->s, P, c->path_mode, w, x, x_fmt, xs_in, logits, ld_logits, shg, ld_shg, T,
+                                  scale, out, out_fmt, c->stream, c->timing ? c->ev : nullptr);
+    if (rc || T == 0) return rc;
+    *c->plan = P;
     c->last_T = T;
-    c->last_sh = has_sh;
-    c->last_path = direct ? 1 : skinny ? 2 : 0;
+    c->last_sh = P.has_sh;
+    c->last_path = P.direct ? 1 : P.skinny ? 2 : 0;
     // the sorted path reads pre-quantised codes in place; the direct path
     // copies every token's codes into the context
-    const bool in_place = !direct && x_fmt == kFmtE4M3;
-    c->tap_xq = in_place ? static_cast<const uint8_t *>(x) : c->xq;
-    c->tap_xs = in_place ? xs_in : c->xs;
-    if (hipGetLastError() != hipSuccess) return Q36MOE_EHIP;
+    const bool in_place = !P.direct && x_fmt == kFmtE4M3;
+    c->tap_xq = in_place ? static_cast<const uint8_t *>(x) : c->s.xq;
+    c->tap_xs = in_place ? xs_in : c->s.xs;
     if (c->timing) {
         if (hipEventSynchronize(c->ev[ST_COUNT]) != hipSuccess) return Q36MOE_EHIP;
         for (int st = 0; st < ST_COUNT; st++) {
@@ -2597,6 +2656,24 @@ int q36moe_forward(q36moe_ctx *c, const q36moe_weights *w, const void *x, int x_
                    void *out, int out_fmt) {
     if (x_fmt != Q36MOE_FMT_F32 && x_fmt != Q36MOE_FMT_BF16) return Q36MOE_EINVAL;
     return forward_impl(c, w, x, x_fmt, nullptr, logits, ld_logits, shg, ld_shg, T, scale, out, out_fmt);
+}
+
+int q36moe_forward_noalloc(const q36moe_weights *w, const void *x, int x_fmt, const float *logits, int ld_logits,
+                           const float *shg, int ld_shg, int T, int top_k, float scale, void *out, int out_fmt,
+                           void *stream) {
+    if (!w || x_fmt < Q36MOE_FMT_F32 || x_fmt > Q36MOE_FMT_BF16) return Q36MOE_EINVAL;
+    if (T < 0 || T > kNoAllocMaxT || top_k < 1 || top_k > kMaxTopK || top_k > w->E) return Q36MOE_EINVAL;
+    if (carve_scratch(nullptr, kNoAllocMaxT, w->E, w->D, w->FF, top_k, nullptr) > kNoAllocBytes)
+        return Q36MOE_EINVAL;
+    if (T == 0) return Q36MOE_OK;
+    uint8_t *base = nullptr;
+    const int rc = noalloc_scratch(&base);
+    if (rc) return rc;
+    Scratch S;
+    carve_scratch(base, kNoAllocMaxT, w->E, w->D, w->FF, top_k, &S);
+    Plan P;
+    return launch_forward(S, P, 0, w, x, x_fmt, nullptr, logits, ld_logits, shg, ld_shg, T, scale, out, out_fmt,
+                          static_cast<hipStream_t>(stream), nullptr);
 }
 
 int q36moe_forward_q8(q36moe_ctx *c, const q36moe_weights *w, const uint8_t *xq, const uint8_t *xs,
@@ -2660,31 +2737,31 @@ int q36moe_quant_e4m3(const void *x, int x_fmt, int T, int K, uint8_t *xq, uint8
 
 int q36moe_ctx_copy_tap(q36moe_ctx *c, int tap, void *dst, size_t bytes, size_t *written) {
     if (!c || !dst) return Q36MOE_EINVAL;
-    const size_t T = (size_t)c->last_T, n = T * c->K, rows = n + (c->last_sh ? T : 0);
+    const size_t T = (size_t)c->last_T, n = T * c->s.K, rows = n + (c->last_sh ? T : 0);
     const void *src = nullptr;
     size_t sz = 0;
     switch (tap) {
-        case Q36MOE_TAP_TOPK_IDX: src = c->topk_idx; sz = n * 4; break;
-        case Q36MOE_TAP_TOPK_W: src = c->topk_w; sz = n * 4; break;
-        case Q36MOE_TAP_XQ: src = c->tap_xq; sz = T * c->D; break;
-        case Q36MOE_TAP_XS: src = c->tap_xs; sz = T * c->D / 32; break;
+        case Q36MOE_TAP_TOPK_IDX: src = c->s.topk_idx; sz = n * 4; break;
+        case Q36MOE_TAP_TOPK_W: src = c->s.topk_w; sz = n * 4; break;
+        case Q36MOE_TAP_XQ: src = c->tap_xq; sz = T * c->s.D; break;
+        case Q36MOE_TAP_XS: src = c->tap_xs; sz = T * c->s.D / 32; break;
         case Q36MOE_TAP_EOFF:
             if (c->last_path == 1) return Q36MOE_EINVAL;   // the direct path does not sort
-            src = c->e_off; sz = (size_t)(c->E + 1) * 4; break;
-        case Q36MOE_TAP_PERM: src = c->perm; sz = n * 4; break;
-        case Q36MOE_TAP_POS: src = c->pos; sz = n * 4; break;
-        case Q36MOE_TAP_HQ: src = c->hq; sz = rows * c->FF; break;
-        case Q36MOE_TAP_HS: src = c->hs; sz = rows * c->FF / 32; break;
-        case Q36MOE_TAP_HSF: src = c->hsf; sz = rows * c->FF / 32 * 4; break;
+            src = c->s.e_off; sz = (size_t)(c->s.E + 1) * 4; break;
+        case Q36MOE_TAP_PERM: src = c->s.perm; sz = n * 4; break;
+        case Q36MOE_TAP_POS: src = c->s.pos; sz = n * 4; break;
+        case Q36MOE_TAP_HQ: src = c->s.hq; sz = rows * c->s.FF; break;
+        case Q36MOE_TAP_HS: src = c->s.hs; sz = rows * c->s.FF / 32; break;
+        case Q36MOE_TAP_HSF: src = c->s.hsf; sz = rows * c->s.FF / 32 * 4; break;
         case Q36MOE_TAP_XQ8:
             if (c->last_path == 1) return Q36MOE_EINVAL;   // quantised in LDS only
-            src = c->xq8; sz = T * c->D; break;
+            src = c->s.xq8; sz = T * c->s.D; break;
         case Q36MOE_TAP_XSF:
             if (c->last_path == 1) return Q36MOE_EINVAL;
-            src = c->xsf; sz = T * c->D / 32 * 4; break;
+            src = c->s.xsf; sz = T * c->s.D / 32 * 4; break;
         case Q36MOE_TAP_DNW:
             if (c->last_path == 1) return Q36MOE_EINVAL;   // combined in registers
-            src = c->dnw; sz = rows * c->D * 4; break;
+            src = c->s.dnw; sz = rows * c->s.D * 4; break;
         default: return Q36MOE_EINVAL;
     }
     if (bytes < sz) return Q36MOE_EINVAL;

@@ -69,6 +69,7 @@ def lib():
     L.q36moe_quant_e4m3.argtypes = [vp, i, i, i, vp, vp, vp]
     L.q36moe_add_rmsnorm_quant.argtypes = [vp, vp, vp, i, i, f, vp, vp, vp, vp]
     L.q36moe_forward_q8.argtypes = [vp, vp, vp, vp, vp, i, vp, i, i, f, vp, i]
+    L.q36moe_forward_noalloc.argtypes = [vp, vp, i, vp, i, vp, i, i, i, f, vp, i, vp]
     L.q36moe_ctx_copy_tap.argtypes = [vp, i, vp, sz, ctypes.POINTER(sz)]
     L.q36moe_ctx_set_path.argtypes = [vp, i]
     L.q36moe_ctx_last_path.argtypes = [vp]
@@ -554,3 +555,30 @@ def probe_mfma(a, b, sa, sb, fmt_a, fmt_b):
                                   fmt_a, fmt_b, ctypes.c_void_p(c.data_ptr()), _stream()),
           "q36moe_probe_mfma")
     return c
+
+
+NOALLOC_MAX_T = 64
+
+
+def forward_noalloc(weights, x, logits, shg=None, top_k=8, scale=1.0, out=None, out_dtype=torch.bfloat16,
+                    stream=None):
+    """q36moe_forward_noalloc: the layer without a context, on the library's
+    static per-GPU scratch (T <= NOALLOC_MAX_T).  `out` may be given so the
+    call itself allocates nothing on the device either."""
+    T = x.shape[0]
+    if x.dtype not in (torch.float32, torch.bfloat16):
+        raise Q36MoEError("x must be float32 or bfloat16")
+    xf = FMT_F32 if x.dtype == torch.float32 else FMT_BF16
+    if out is None:
+        out = torch.empty((T, weights.d_model), dtype=out_dtype, device=x.device)
+    of = FMT_F32 if out.dtype == torch.float32 else FMT_BF16
+    if logits.dim() != 2 or logits.shape[0] != T or logits.stride(1) != 1:
+        raise Q36MoEError("logits must be [T, n_expert] with contiguous rows")
+    if T and (not logits.is_cuda or logits.dtype != torch.float32):
+        raise Q36MoEError("logits must be a float32 GPU tensor")
+    sp, sld = _shg(shg)
+    check(lib().q36moe_forward_noalloc(weights._h, _dev(x, "x") if T else None, xf,
+                                       ctypes.c_void_p(logits.data_ptr()) if T else None, logits.stride(0),
+                                       sp, sld, T, top_k, float(scale), _dev(out, "out") if T else None, of,
+                                       _stream(stream)), "q36moe_forward_noalloc")
+    return out
