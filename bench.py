@@ -122,9 +122,9 @@ def kernel_bytes(stage, T, U, shared, dn_q8=False, sh_q8=False):
         # gate+up weights of the hit experts, the activations, h out
         return U * 2 * MAT_BYTES + (2 * sh_mat if shared else 0) + xq + hq
     if stage == "down":
-        # down weights, h in, weighted f32 rows out
+        # down weights, h in, weighted rows out (f16 + an exponent byte per 16)
         dn = U * (Q8_MAT_BYTES if dn_q8 else MAT_BYTES) + (sh_mat if shared else 0)
-        return dn + hq + P * D * 4
+        return dn + hq + P * (D * 2 + D // 16)
     raise ValueError(stage)
 
 

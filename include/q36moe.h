@@ -66,7 +66,9 @@ extern "C" {
 #define Q36MOE_TAP_HQ        7  /* u8    [T*k+T][d_ff] e4m3 SwiGLU rows
                                    (int8 for q8_0-split down matrices)  */
 #define Q36MOE_TAP_HS        8  /* u8    [T*k+T][d_ff/32] E8M0          */
-#define Q36MOE_TAP_DNW       9  /* f32   [T*k+T][d_model] w * down rows */
+#define Q36MOE_TAP_DNW       9  /* f32   [T*k+T][d_model] w * down rows
+                                   (staged as f16 with a power-of-two
+                                   scale per 16 columns; widened here)  */
 #define Q36MOE_TAP_HSF      10  /* f32   [T*k+T][d_ff/32] int8 h scales
                                    (q8_0-split down; HQ then holds int8) */
 #define Q36MOE_TAP_XQ8      11  /* i8    [T][d_model] int8 x of a q8_0-split

@@ -704,7 +704,8 @@ struct GemmArgs {
     const uint8_t *bs2;       // their E8M0 scales, lane-group-major [row][4][K/128]
     const int32_t *row_tok; const float *row_w;
     uint8_t *hq, *hs, *hs2;   // GATEUP output rows (sorted slot): h, natural and lane-major scales
-    float *dnw;               // DOWN output rows (sorted slot), weighted
+    uint16_t *dnh;            // DOWN output rows (sorted slot), weighted, as f16 [row][ldo]
+    uint8_t *dne;             // with one exponent byte per 16 columns [row][ldo / 16]
     int ldo;                  // output row length
     // q8_0-split routed down: GATEUP writes the routed rows of h as int8
     // with fp32 scales (hsf [row][ldo/32]); DOWN reads them from bsf
@@ -1386,6 +1387,33 @@ constexpr int kDlW = 4;                  // waves
 constexpr int kDlRT = 4;                 // row tiles per wave
 constexpr int kDlRows = 128;             // B rows staged per chunk
 
+// Staging of a weighted down row: f16 with a power-of-two scale per 16
+// columns.  The 16 columns of group g of row p are held by lanes q = 0..3 of
+// one MFMA column, 4 each; their maximum |v| has the biased fp32 exponent eb
+// (clamped to [15, 254]; 255 keeps inf / NaN), the group is stored as
+// v * 2^(141 - eb) (exact: a power of two), every value of which is below
+// 2^15 < 65504, rounded to f16 (RNE, relative error <= 2^-11), with eb in
+// dne; the combine multiplies back by 2^(eb - 141).  Half the bytes of an
+// f32 staging (which the reference uses, q36_engine.cu:3451-3463) for a
+// rounding of 2^-11 of each staged value.
+__device__ __forceinline__ void store_dn16(const GemmArgs &A, int p, int g, int q, bool valid, float v0, float v1,
+                                           float v2, float v3) {
+    float a = fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3)));
+    a = fmaxf(a, __shfl_xor(a, 16, 64));
+    a = fmaxf(a, __shfl_xor(a, 32, 64));
+    uint32_t eb = (__float_as_uint(a) >> 23) & 0xffu;
+    eb = eb == 255u ? 255u : eb < 15u ? 15u : eb > 254u ? 254u : eb;
+    const float mul = __uint_as_float((268u - eb) << 23);
+    if (valid) {
+        const uint32_t lo = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(v0 * mul)) |
+                            ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(v1 * mul)) << 16);
+        const uint32_t hi = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(v2 * mul)) |
+                            ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(v3 * mul)) << 16);
+        *reinterpret_cast<uint2 *>(A.dnh + (size_t)p * A.ldo + g * 16 + 4 * q) = make_uint2(lo, hi);
+        if (q == 0) A.dne[(size_t)p * (A.ldo / 16) + g] = (uint8_t)eb;
+    }
+}
+
 // byte offset of (row r, 16-byte chunk c) of a staged h row: rows of 512 B,
 // chunk index XORed (low 4 bits) with the row, so the 16 rows of a fragment
 // read fall in 16 distinct bank groups
@@ -1501,11 +1529,10 @@ __device__ __forceinline__ void down_q8_tile(const GemmArgs &A, const uint8_t *W
 #pragma unroll
                 for (int i = 0; i < 4; i++)
                     acc[i] = fmaf(q8_scaled(prev[i], dw[NKB - 1][i], ndw[NKB - 1][i]), dh[NKB - 1], acc[i]);
-                if (j * 16 + n < nr) {
-                    const int p = c0 + j * 16 + n;
-                    const float w = ws[j * 16 + n];
-                    *reinterpret_cast<float4 *>(A.dnw + (size_t)p * A.ldo + mt * 16 + 4 * q) =
-                        make_float4(acc[0] * w, acc[1] * w, acc[2] * w, acc[3] * w);
+                {
+                    const float w = ws[r];
+                    store_dn16(A, c0 + j * 16 + n, mt, q, j * 16 + n < nr, acc[0] * w, acc[1] * w, acc[2] * w,
+                               acc[3] * w);
                 }
             }
         }
@@ -1581,14 +1608,13 @@ __global__ __launch_bounds__(64 * kDlW, Q8 ? 2 : 1) void k_down_lds(GemmArgs A) 
                     const v8i av = v8i{(int)f[0], (int)f[1], (int)f[2], (int)f[3], 0, 0, 0, 0};
                     acc[i] = mfma_sel(kt, av, bv[kt], acc[i], (int)sa[i], (int)sbw);
                 }
-            if (j * 16 + n < nr) {
-                const int p = c0 + j * 16 + n;
-                const float w = ws[j * 16 + n];
+            {
+                const float w = ws[r];
+                const bool valid = j * 16 + n < nr;
 #pragma unroll
                 for (int i = 0; i < kDlRT; i++) {
                     const v4f c = acc[i];
-                    *reinterpret_cast<float4 *>(A.dnw + (size_t)p * A.ldo + (mt0 + i) * 16 + 4 * q) =
-                        make_float4(c[0] * w, c[1] * w, c[2] * w, c[3] * w);
+                    store_dn16(A, c0 + j * 16 + n, mt0 + i, q, valid, c[0] * w, c[1] * w, c[2] * w, c[3] * w);
                 }
             }
         }
@@ -1963,7 +1989,15 @@ __global__ __launch_bounds__(576) void k_direct_down(DirectArgs A) {
 // ---------------------------------------------------------------------------
 // combine
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_combine(const float *__restrict__ dnw,
+// 4 staged values of row p from column j (f16 + exponent per 16 columns)
+__device__ __forceinline__ float4 load_dn16(const uint16_t *__restrict__ dnh, const uint8_t *__restrict__ dne,
+                                            int D, size_t p, int j) {
+    const uint2 h = *reinterpret_cast<const uint2 *>(dnh + p * D + j);
+    const float sc = __uint_as_float(((uint32_t)dne[p * (D / 16) + (j >> 4)] - 14u) << 23);
+    return make_float4(f16lo(h.x) * sc, f16hi(h.x) * sc, f16lo(h.y) * sc, f16hi(h.y) * sc);
+}
+
+__global__ __launch_bounds__(256) void k_combine(const uint16_t *__restrict__ dnh, const uint8_t *__restrict__ dne,
                                                 const int32_t *__restrict__ pos, int T, int k,
                                                 int D, int has_sh, void *out, int out_fmt) {
     const int t = blockIdx.x;
@@ -1972,11 +2006,11 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ dnw,
         float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
         for (int s = 0; s < k; s++) {
             const int p = pos[(size_t)t * k + s];
-            const float4 v = *reinterpret_cast<const float4 *>(dnw + (size_t)p * D + j);
+            const float4 v = load_dn16(dnh, dne, D, (size_t)p, j);
             a.x += v.x; a.y += v.y; a.z += v.z; a.w += v.w;
         }
         if (has_sh) {
-            const float4 v = *reinterpret_cast<const float4 *>(dnw + (size_t)(n + t) * D + j);
+            const float4 v = load_dn16(dnh, dne, D, (size_t)(n + t), j);
             a.x += v.x; a.y += v.y; a.z += v.z; a.w += v.w;
         }
         if (out_fmt == Q36MOE_FMT_F32) {
@@ -1988,6 +2022,14 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ dnw,
                 make_uint2(lo, hi);
         }
     }
+}
+
+// The staged down rows widened to f32 (the DNW debug tap).
+__global__ __launch_bounds__(256) void k_dn16_expand(const uint16_t *__restrict__ dnh, const uint8_t *__restrict__ dne,
+                                                    int D, float *__restrict__ dst) {
+    const size_t p = blockIdx.x;
+    for (int j = threadIdx.x * 4; j < D; j += 256 * 4)
+        *reinterpret_cast<float4 *>(dst + p * D + j) = load_dn16(dnh, dne, D, p, j);
 }
 
 // ---------------------------------------------------------------------------
@@ -2088,7 +2130,7 @@ struct Scratch {
     uint8_t *hq, *hs, *hs2;
     float *hsf;                     // fp32 scales of int8 h rows (q8_0-split down)
     int8_t *xq8; float *xsf;        // int8 x + fp32 scales (q8_0-split shared expert, sorted path)
-    float *dnw;
+    uint16_t *dnh; uint8_t *dne;    // staged weighted down rows: f16 [rows][D] + exponent per 16 columns
     float *hf;                      // direct path: fp32 SwiGLU rows
 };
 
@@ -2182,7 +2224,7 @@ size_t carve_scratch(uint8_t *base, int max_T, int E, int D, int FF, int K, Scra
     const size_t o_hq = take(rows * FF), o_hs = take(rows * FF / 32), o_hs2 = take(rows * FF / 32);
     const size_t o_hsf = take(rows * FF / 32 * 4);
     const size_t o_xq8 = take((size_t)max_T * D), o_xsf = take((size_t)max_T * D / 32 * 4);
-    const size_t o_dnw = take(rows * D * 4);
+    const size_t o_dnh = take(rows * D * 2), o_dne = take(rows * D / 16);
     const size_t direct_rows = (size_t)(max_T < kDirectMaxT ? max_T : kDirectMaxT) * (K + 1);
     const size_t o_hf = take(direct_rows * FF * 4);
     if (!base) return off;
@@ -2205,7 +2247,8 @@ size_t carve_scratch(uint8_t *base, int max_T, int E, int D, int FF, int K, Scra
     c.hsf = reinterpret_cast<float *>(b + o_hsf);
     c.xq8 = reinterpret_cast<int8_t *>(b + o_xq8);
     c.xsf = reinterpret_cast<float *>(b + o_xsf);
-    c.dnw = reinterpret_cast<float *>(b + o_dnw);
+    c.dnh = reinterpret_cast<uint16_t *>(b + o_dnh);
+    c.dne = b + o_dne;
     c.hf = reinterpret_cast<float *>(b + o_hf);
     return off;
 }
@@ -2516,7 +2559,7 @@ static void launch_stage(const Scratch &c, const Plan &P, int st, hipStream_t s)
                                    s, P.da);
             break;
         case ST_COMBINE:
-            hipLaunchKernelGGL(k_combine, dim3(T), dim3(256), 0, s, c.dnw, c.pos, T, K, D, P.has_sh,
+            hipLaunchKernelGGL(k_combine, dim3(T), dim3(256), 0, s, c.dnh, c.dne, c.pos, T, K, D, P.has_sh,
                                const_cast<void *>(P.out), P.out_fmt);
             break;
         default: break;
@@ -2606,7 +2649,7 @@ static int launch_forward(const Scratch &c, Plan &P, int pm, const q36moe_weight
         GemmArgs &da = P.da;
         da = ga;
         da.M = D;
-        da.bq = c.hq; da.bs2 = c.hs2; da.dnw = c.dnw; da.ldo = D;
+        da.bq = c.hq; da.bs2 = c.hs2; da.dnh = c.dnh; da.dne = c.dne; da.ldo = D;
         da.bsf = c.hsf;
     }
     bind_weights(P, w);
@@ -2761,7 +2804,12 @@ int q36moe_ctx_copy_tap(q36moe_ctx *c, int tap, void *dst, size_t bytes, size_t 
             src = c->s.xsf; sz = T * c->s.D / 32 * 4; break;
         case Q36MOE_TAP_DNW:
             if (c->last_path == 1) return Q36MOE_EINVAL;   // combined in registers
-            src = c->s.dnw; sz = rows * c->s.D * 4; break;
+            sz = rows * c->s.D * 4;
+            if (bytes < sz) return Q36MOE_EINVAL;
+            if (written) *written = sz;
+            hipLaunchKernelGGL(k_dn16_expand, dim3((unsigned)rows), dim3(256), 0, c->stream, c->s.dnh, c->s.dne,
+                               c->s.D, static_cast<float *>(dst));
+            return hip_rc(hipGetLastError());
         default: return Q36MOE_EINVAL;
     }
     if (bytes < sz) return Q36MOE_EINVAL;

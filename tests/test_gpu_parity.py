@@ -9,7 +9,10 @@
          (fp32 vs fp64 accumulation), counted and capped at 1%;
       2. down + combine from the GPU's own h rows vs fp64:
            max relative error  max_i |y_ti - ref_ti| / max_i |ref_ti|   <= 2e-3
-           element-wise  |y_ti - ref_ti| / max(|ref_ti|, 0.05 max_i |ref_ti|) <= 2e-3
+           element-wise  |y_ti - ref_ti| / max(|ref_ti|, 0.05 max_i |ref_ti|) <= 2e-3,
+           less 2^-10 * sum_s |w_s d_s|_i (the combine stages the weighted down
+           rows as f16 with a power-of-two scale per 16 columns: <= 2^-11 of
+           each term)
       3. end to end vs the fp64 oracle, the same two 2e-3 bars, per token:
          a token none of whose h rows has a midpoint flip is held against
          the plain oracle (q36moe_oracle.c, its own fp64 path); a token with
@@ -199,9 +202,23 @@ def layer_w():
     return w, dw
 
 
-def _row_err(y, ref):
+# The down rows are staged (for the combine) as f16 with a power-of-two
+# scale per 16 columns: each staged term carries a rounding of at most 2^-11
+# of itself.  Near outputs where the weighted terms cancel, the element-wise
+# bar admits that rounding -- STAGE_SLACK times the sum of |terms| of the
+# element -- on top of its own 2e-3.
+STAGE_SLACK = 2.0 ** -10
+
+
+def _row_err(y, ref, absterms=None):
+    """(element-wise, normwise) max relative error per row: element-wise
+    |y - ref| (less STAGE_SLACK * absterms when given) over max(|ref|, FLOOR *
+    rowmax); normwise max |y - ref| / max |ref|."""
     scale = np.abs(ref).max(axis=1, keepdims=True)
-    rel = np.abs(y - ref) / np.maximum(np.abs(ref), FLOOR * scale)
+    d = np.abs(y - ref)
+    if absterms is not None:
+        d = np.maximum(d - STAGE_SLACK * absterms, 0.0)
+    rel = d / np.maximum(np.abs(ref), FLOOR * scale)
     return float(rel.max()), float((np.abs(y - ref).max(axis=1) / scale[:, 0]).max())
 
 
@@ -320,16 +337,21 @@ def _check_layer(name, dev, oracle, layer_w, x, lg, shg, sample=None, x_dtype=to
     # stage 2: down + combine from the GPU's own h
     _, ow = oracle.router_topk(lg, 8)
     ref_h = np.zeros((toks.size, x.shape[1]))
+    absterms = np.zeros_like(ref_h)
     for j, t in enumerate(toks):
         for s in range(8):
             p = int(pos[t * 8 + s])
             hd = oracle.dequant_e4m3(hq[p:p + 1], hs[p:p + 1])[0]
-            ref_h[j] += ow[t, s] * oracle.expert_down(w["down"][gi[t, s]], hd)
+            term = ow[t, s] * oracle.expert_down(w["down"][gi[t, s]], hd)
+            ref_h[j] += term
+            absterms[j] += np.abs(term)
         if shg is not None:
             p = T * 8 + int(t)
             hd = oracle.dequant_e4m3(hq[p:p + 1], hs[p:p + 1])[0]
-            ref_h[j] += 1 / (1 + np.exp(-float(shg[t]))) * oracle.expert_down(w["sh_down"], hd)
-    el_h, norm_h = _row_err(y32[toks], ref_h)
+            term = 1 / (1 + np.exp(-float(shg[t]))) * oracle.expert_down(w["sh_down"], hd)
+            ref_h[j] += term
+            absterms[j] += np.abs(term)
+    el_h, norm_h = _row_err(y32[toks], ref_h, absterms)
     # stage 3: end to end, per token: the plain fp64 oracle for tokens without
     # flips, the oracle with the flipped codes substituted for the others
     ref = oracle.moe_forward(w, x, lg, shg, tokens=toks)
@@ -350,7 +372,7 @@ def _check_layer(name, dev, oracle, layer_w, x, lg, shg, sample=None, x_dtype=to
             p = T * 8 + int(t)
             hd = oracle.dequant_e4m3(hrows[p][1][None], hrows[p][2][None])[0]
             ref_sub[j] += 1 / (1 + np.exp(-float(shg[t]))) * oracle.expert_down(w["sh_down"], hd)
-    el, normwise = _row_err(y32[toks], ref_sub)
+    el, normwise = _row_err(y32[toks], ref_sub, absterms)
     _, raw_norm = _row_err(y32[toks], ref)
     _, bf16_norm = _row_err(y16[toks], ref_sub)
     ref32 = oracle.moe_forward(w, x, lg, shg, act_mode=1, tokens=toks)
