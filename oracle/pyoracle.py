@@ -273,7 +273,9 @@ def expert_h_q8(gq, gd, uq, ud, xd):
 
 
 def moe_forward(w, x, logits, shg=None, k=8, scale=1.0, act_mode=0, tokens=None):
-    """double [n_tok, d_model]; act_mode 0 = W4A8, 1 = W4A32."""
+    """double [n_tok, d_model]; act_mode 0 = W4A8 (the build's numerics), 1 =
+    W4A32 (the reference's decode), 2 = e4m3 x with f32 h rounded to fp16 for
+    the down projection (the reference's prefill)."""
     s, keep = _wstruct(w)
     x = np.ascontiguousarray(x, dtype=np.float32)
     logits = np.ascontiguousarray(logits, dtype=np.float32)

@@ -490,7 +490,12 @@ static void quant_roundtrip(const float *v, int K, double *out) {
  * k_expert_gemv2 -> k_silu_mul_slots -> k_expert_gemv
  * (q36_engine.cu:1610-1618) with the activation quantisation of the
  * W4A8 prefill path (q36_engine.cu:2411-2428, :3437-3441) applied to x and
- * to the SwiGLU output when act_mode==0. */
+ * to the SwiGLU output when act_mode==0.  act_mode 1 keeps x and h
+ * unquantised (the reference's decode matvecs, W4A32); act_mode 2 is the
+ * reference's own prefill numerics: x per-32 e4m3 (k_quant_e4m3 ->
+ * k_gemm_expert_mma), h kept in f32 by k_silu_mul and rounded to fp16 by the
+ * MXFP4 down's fp16 tensor-core GEMM (k_gemm_expert_tc with x_by_entry,
+ * q36_engine.cu:3459-3462). */
 static void expert_d(const uint8_t *g, const uint8_t *u, const uint8_t *d,
                      const int8_t *dq, const uint16_t *dd,
                      int D, int FF, const double *xin, int act_mode, double *out) {
@@ -517,6 +522,7 @@ static void expert_d(const uint8_t *g, const uint8_t *u, const uint8_t *d,
         mv_q8_d(dq, dd, D, FF, hd, out);
     } else {
         if (act_mode == 0) quant_roundtrip(hf, FF, hd);
+        else if (act_mode == 2) for (int f = 0; f < FF; f++) hd[f] = or_f16_decode(or_f16_encode(hf[f]));
         else for (int f = 0; f < FF; f++) hd[f] = hf[f];
         mv_d(d, D, FF, hd, out);
     }
@@ -595,7 +601,7 @@ void or_moe_forward(const or_weights *w, const float *x, const float *logits,
         double wt[64];
         int t = tokens ? tokens[i] : i;
         const float *xt = x + (size_t)t * D;
-        if (act_mode == 0) quant_roundtrip(xt, D, xd);
+        if (act_mode == 0 || act_mode == 2) quant_roundtrip(xt, D, xd);
         else for (int j = 0; j < D; j++) xd[j] = xt[j];
         or_router_topk(logits + (size_t)t * ld_logits, 1, E, ld_logits, k, scale, 1, idx, wt);
         double *o = out + (size_t)i * D;

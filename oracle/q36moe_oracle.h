@@ -95,6 +95,9 @@ typedef struct {
  *             (per-32 E8M0 + e4m3), h rounded to fp32 before quantising.
  * act_mode 1: W4A32 -- activations kept unquantised (the reference decode
  *             path, q36_engine.cu:1610-1618), for drift reporting.
+ * act_mode 2: the reference's prefill numerics -- x per-32 e4m3, h kept in
+ *             f32 and rounded to fp16 for the MXFP4 down (k_gemm_expert_tc,
+ *             q36_engine.cu:3459-3462), for drift reporting.
  * Computes the rows listed in `tokens` (n_tok of them; NULL = 0..T-1) and
  * writes out[n_tok][d_model] in double.  shg may be NULL (no shared expert
  * contribution).                                                         */

@@ -1414,6 +1414,36 @@ __device__ __forceinline__ void store_dn16(const GemmArgs &A, int p, int g, int 
     }
 }
 
+// store_dn16 for the 4 row tiles mt0 .. mt0+3 (64 columns) of one MFMA
+// column tile at once: one maximum and one exponent for all 64 (written to
+// each of the 4 groups' exponent bytes), and the routing weight w folded into
+// the scale multiply.  f16 holds every value within 2^-29 of the group
+// maximum at full relative precision, so the wider group rounds the same.
+__device__ __forceinline__ void store_dn16x4(const GemmArgs &A, int p, int mt0, int q, bool valid, const v4f (&c)[4],
+                                             float w) {
+    float a = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        a = fmaxf(a, fmaxf(fmaxf(fabsf(c[i][0]), fabsf(c[i][1])), fmaxf(fabsf(c[i][2]), fabsf(c[i][3]))));
+    a = fmaxf(a, __shfl_xor(a, 16, 64));
+    a = fmaxf(a, __shfl_xor(a, 32, 64));
+    a *= fabsf(w);
+    uint32_t eb = (__float_as_uint(a) >> 23) & 0xffu;
+    eb = eb == 255u ? 255u : eb < 15u ? 15u : eb > 254u ? 254u : eb;
+    const float wm = w * __uint_as_float((268u - eb) << 23);
+    if (valid) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t lo = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(c[i][0] * wm)) |
+                                ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(c[i][1] * wm)) << 16);
+            const uint32_t hi = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(c[i][2] * wm)) |
+                                ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(c[i][3] * wm)) << 16);
+            *reinterpret_cast<uint2 *>(A.dnh + (size_t)p * A.ldo + (mt0 + i) * 16 + 4 * q) = make_uint2(lo, hi);
+        }
+        if (q == 0) *reinterpret_cast<uint32_t *>(A.dne + (size_t)p * (A.ldo / 16) + mt0) = eb * 0x01010101u;
+    }
+}
+
 // byte offset of (row r, 16-byte chunk c) of a staged h row: rows of 512 B,
 // chunk index XORed (low 4 bits) with the row, so the 16 rows of a fragment
 // read fall in 16 distinct bank groups
@@ -1608,15 +1638,7 @@ __global__ __launch_bounds__(64 * kDlW, Q8 ? 2 : 1) void k_down_lds(GemmArgs A) 
                     const v8i av = v8i{(int)f[0], (int)f[1], (int)f[2], (int)f[3], 0, 0, 0, 0};
                     acc[i] = mfma_sel(kt, av, bv[kt], acc[i], (int)sa[i], (int)sbw);
                 }
-            {
-                const float w = ws[r];
-                const bool valid = j * 16 + n < nr;
-#pragma unroll
-                for (int i = 0; i < kDlRT; i++) {
-                    const v4f c = acc[i];
-                    store_dn16(A, c0 + j * 16 + n, mt0 + i, q, valid, c[0] * w, c[1] * w, c[2] * w, c[3] * w);
-                }
-            }
+            store_dn16x4(A, c0 + j * 16 + n, mt0, q, j * 16 + n < nr, acc, ws[r]);
         }
     }
 }

@@ -38,6 +38,7 @@ pytestmark = pytest.mark.gpu
 
 TOL = 2e-3
 FLOOR = 5e-2
+_LAST_METRICS = {}
 
 
 def _metrics(name, **kv):
@@ -375,12 +376,21 @@ def _check_layer(name, dev, oracle, layer_w, x, lg, shg, sample=None, x_dtype=to
     el, normwise = _row_err(y32[toks], ref_sub, absterms)
     _, raw_norm = _row_err(y32[toks], ref)
     _, bf16_norm = _row_err(y16[toks], ref_sub)
+    # distance from the reference's own numeric paths (reported, not a bar):
+    # W4A32 (its decode matvecs) and e4m3 x with fp16 h (its prefill GEMMs)
     ref32 = oracle.moe_forward(w, x, lg, shg, act_mode=1, tokens=toks)
+    refpf = oracle.moe_forward(w, x, lg, shg, act_mode=2, tokens=toks)
     drift = float(np.abs(ref32 - ref).max() / np.abs(ref).max())
+    _, drift_w4a32 = _row_err(y32[toks], ref32)
+    _, drift_prefill = _row_err(y32[toks], refpf)
+    global _LAST_METRICS
+    _LAST_METRICS = dict(e2e_max_rel=normwise, drift_vs_ref_decode_w4a32=drift_w4a32,
+                         drift_vs_ref_prefill_fp16h=drift_prefill)
     _metrics(name, T=int(T), tokens_checked=int(toks.size), h_rows=len(rows), h_flips=int(flips),
              tokens_with_flips=n_flipped_tok, stage2_max_rel=norm_h, stage2_elementwise=el_h,
              e2e_max_rel=normwise, e2e_elementwise=el, e2e_unsubstituted_max_rel=raw_norm,
-             bf16_max_rel=bf16_norm, distinct_experts=int(np.unique(gi).size), w4a32_drift=drift)
+             bf16_max_rel=bf16_norm, distinct_experts=int(np.unique(gi).size), w4a32_drift=drift,
+             drift_vs_ref_decode_w4a32=drift_w4a32, drift_vs_ref_prefill_fp16h=drift_prefill)
     assert flips <= 0.01 * len(rows) * hq.shape[1]
     assert norm_h <= TOL and el_h <= TOL, f"{name}: down/combine error {norm_h:.3g} / {el_h:.3g}"
     assert normwise <= TOL and el <= TOL, f"{name}: end-to-end error {normwise:.3g} / {el:.3g}"
@@ -681,3 +691,23 @@ def test_forward_strided_shared_gate(dev, layer_w, T, path):
     yn = moe.MoELayer(T).forward(dw, x, rt[:, :256].contiguous(), None, out_dtype=torch.float32)
     torch.cuda.synchronize()
     assert not torch.equal(ya, yn)
+
+
+@pytest.mark.parametrize("cfg,path", [("decode1", 2), ("ragged64", 0), ("prefill4096", 0), ("mixed", 0)])
+def test_drift_from_reference_numerics(dev, oracle, layer_w, cfg, path):
+    """Distance of the build (W4A8: e4m3 x and h) from the reference's own
+    numeric paths, reported (stdout and Q36_METRICS_FILE) with a loose sanity
+    bound, on a configuration that also passes the parity bars of
+    _check_layer: W4A32, the reference's decode matvecs
+    (q36_engine.cu:1610-1618), and e4m3 x with f32 h rounded to fp16, its
+    prefill GEMMs (q36_engine.cu:3437-3462).  The north star mandates FP8
+    activations for both GEMMs, so this is a stated number, not a bar; the
+    per-32 e4m3 of h (relative step up to 2^-3) is what separates them."""
+    x, lg, shg = synth.config_inputs(cfg, 5)
+    T = x.shape[0]
+    sample = None if T <= 64 else np.sort(np.random.default_rng(51).choice(T, 32, replace=False))
+    _check_layer(f"drift_{cfg}", dev, oracle, layer_w, x, lg, shg, sample=sample, path=path)
+    m = _LAST_METRICS
+    print(f"drift {cfg}: vs W4A32 {m['drift_vs_ref_decode_w4a32']:.2e}, "
+          f"vs e4m3-x/fp16-h {m['drift_vs_ref_prefill_fp16h']:.2e} (parity e2e {m['e2e_max_rel']:.2e})")
+    assert m["drift_vs_ref_decode_w4a32"] < 0.15 and m["drift_vs_ref_prefill_fp16h"] < 0.15

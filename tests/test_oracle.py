@@ -301,7 +301,7 @@ def _numpy_layer(oracle, w, x, lg, shg, k, act_mode):
     G = np.stack([_deq_matrix(oracle, w["gate"][e]) for e in range(E)])
     U = np.stack([_deq_matrix(oracle, w["up"][e]) for e in range(E)])
     Dn = np.stack([_deq_matrix(oracle, w["down"][e]) for e in range(E)])
-    if act_mode == 0:
+    if act_mode in (0, 2):
         xq, xs = oracle.quant_e4m3(x)
         xd = oracle.dequant_e4m3(xq, xs)
     else:
@@ -322,13 +322,15 @@ def _numpy_layer(oracle, w, x, lg, shg, k, act_mode):
             if act_mode == 0:
                 hq, hs = oracle.quant_e4m3(h[None])
                 hd = oracle.dequant_e4m3(hq, hs)[0]
+            elif act_mode == 2:   # the reference's prefill: f32 h rounded to fp16 (numpy's RNE)
+                hd = h.astype(np.float16).astype(np.float64)
             else:
                 hd = h.astype(np.float64)
             out[t] += wv * (d_ @ hd)
     return out
 
 
-@pytest.mark.parametrize("act_mode", [0, 1])
+@pytest.mark.parametrize("act_mode", [0, 1, 2])
 def test_layer_vs_numpy(oracle, act_mode):
     from q36_amd import synth
     w = synth.expert_weights(11, n_expert=6, d_model=512, d_ff=512, shared=True)
