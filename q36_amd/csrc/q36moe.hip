@@ -817,7 +817,7 @@ __device__ __forceinline__ int gd_boff(int r, int c) {
 namespace gdma {
 constexpr int RT = 4, W = 4, TOK = kGdTok;
 static_assert(TOK == 16 * 2 * 5, "column tiles per wave: at most 5 (the largest body instantiated)");
-constexpr int STA = 3, STB = 2;
+constexpr int STA = 4, STB = 2;   // A stage of step kt: kt % 4, static inside a 4-step group
 struct Lds {
     __align__(16) uint8_t a[STA][2 * RT * 1024];
     __align__(16) uint8_t b[STB][TOK * 128];
@@ -825,11 +825,13 @@ struct Lds {
 };
 static_assert(sizeof(Lds) * 2 <= 160 * 1024, "two workgroups per CU");
 
-__device__ __forceinline__ void wait_vm(int n) {
-    if (n == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    else asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
-}
-
+// The K loop runs as 4 groups of 4 steps: 3 iterations of a runtime loop
+// whose body has no conditions (stage slots are the step within the group,
+// every load is issued unconditionally), then the last group as a static
+// copy that stops the staging.  x row groups: the tile's column tiles need
+// 4*NJ groups of 8 rows at most, NJ per wave (rows past the tile repeat its
+// last row); a wave with fewer column tiles than its neighbours still
+// covers its groups (groups w + 4i, i < NJ, reach past 2*ntt - 1).
 template <int NJ>
 __device__ __forceinline__ void body(const GemmArgs &A, Lds &L, const uint8_t *Wg, const uint8_t *Wu,
                                      int mt0, int p0, int p1, bool hq8) {
@@ -843,9 +845,7 @@ __device__ __forceinline__ void body(const GemmArgs &A, Lds &L, const uint8_t *W
     // w + 4i (8 rows each) holding rows of the tile.  Sources are a uniform
     // base plus a 32-bit per-lane offset (the saddr form of the load).
     const uint32_t aoff = (uint32_t)(mt0 + wave) * NKT * 1024 + lane * 16;
-    const int nrg = (ntok + 7) >> 3;
-    const int nbw = nrg > wave ? (nrg - wave + W - 1) / W : 0;
-    constexpr int NBI = TOK / 8 / W;
+    constexpr int NBI = NJ > 0 ? NJ : 1;
     uint32_t boff[NBI];
 #pragma unroll
     for (int i = 0; i < NBI; i++) {
@@ -860,8 +860,7 @@ __device__ __forceinline__ void body(const GemmArgs &A, Lds &L, const uint8_t *W
     };
     auto issue_b = [&](int kt, int slot) {
 #pragma unroll
-        for (int i = 0; i < NBI; i++)
-            if (i < nbw) dma16(A.bq + (boff[i] + kt * 128), &L.b[slot][(wave + W * i) * 1024]);
+        for (int i = 0; i < NBI; i++) dma16(A.bq + (boff[i] + kt * 128), &L.b[slot][(wave + W * i) * 1024]);
     };
     const size_t nib = (size_t)512 * KD / 2;
     dma16(Wg + nib + ((size_t)(mt0 + wave) * 64 + lane) * 16, &L.sc[wave * 1024]);
@@ -873,7 +872,7 @@ __device__ __forceinline__ void body(const GemmArgs &A, Lds &L, const uint8_t *W
         const int r = min(16 * (wt + 2 * j) + n, ntok - 1);
         sb[j] = *reinterpret_cast<const u32x4 *>(A.bs2 + (size_t)A.row_tok[p0 + r] * (KD / 32) + q * 16);
     }
-    // step kt issues B(kt+1) then A(kt+2) after its MFMAs; when step kt
+    // step kt issues B(kt+1) then A(kt+2) after its barrier; when step kt
     // needs B(kt), only A(kt+1) was issued after it
     issue_a(0, 0);
     issue_b(0, 0);
@@ -886,11 +885,10 @@ __device__ __forceinline__ void body(const GemmArgs &A, Lds &L, const uint8_t *W
         for (int j = 0; j < NJ; j++) acc[a][j] = v4f{0.f, 0.f, 0.f, 0.f};
     uint32_t sa[4];
     uint32_t sbg[NJ1];
-    int sla = 0;          // A stage of the current step
-#pragma unroll 1
-    for (int g = 0; g < NKT / 4; g++) {
+    auto group = [&](int g, auto LASTC) {
+        constexpr bool LAST = decltype(LASTC)::value;
 #pragma unroll
-        for (int j = 0; j < NJ; j++) sbg[j] = g == 0 ? sb[j][0] : g == 1 ? sb[j][1] : g == 2 ? sb[j][2] : sb[j][3];
+        for (int j = 0; j < NJ; j++) sbg[j] = (g & 2) ? ((g & 1) ? sb[j][3] : sb[j][2]) : ((g & 1) ? sb[j][1] : sb[j][0]);
         static_for<0, 4>([&](auto S) {
             constexpr int st = decltype(S)::value;
             const int kt = 4 * g + st;
@@ -901,8 +899,14 @@ __device__ __forceinline__ void body(const GemmArgs &A, Lds &L, const uint8_t *W
             for (int a = 0; a < 4; a++)
 #pragma unroll
                 for (int j = 0; j < NJ; j++) asm volatile("" : "+v"(acc[a][j]));
-            wait_vm(kt + 1 < NKT ? 2 : 0);
+            if constexpr (LAST && st == 3) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            else asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
             dma_barrier();
+            // restage the slots read in the previous step (free: every wave
+            // has passed this barrier) before this step's MFMAs
+            if constexpr (!(LAST && st == 3)) issue_b(kt + 1, (st + 1) & 1);
+            if constexpr (!(LAST && st >= 2)) issue_a(kt + 2, (st + 2) & 3);
+            __builtin_amdgcn_sched_barrier(0);
             if constexpr (st == 0) {
 #pragma unroll
                 for (int a = 0; a < 4; a++) {
@@ -916,7 +920,7 @@ __device__ __forceinline__ void body(const GemmArgs &A, Lds &L, const uint8_t *W
 #pragma unroll
             for (int a = 0; a < 4; a++) {
                 const int slot = (a < 2 ? 0 : RT) + 2 * wa + (a & 1);
-                af[a] = *reinterpret_cast<const u32x4 *>(&L.a[sla][slot * 1024 + lane * 16]);
+                af[a] = *reinterpret_cast<const u32x4 *>(&L.a[st][slot * 1024 + lane * 16]);
             }
 #pragma unroll
             for (int j = 0; j < NJ; j++) {
@@ -938,12 +942,11 @@ __device__ __forceinline__ void body(const GemmArgs &A, Lds &L, const uint8_t *W
                     __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
                 }
             }
-            // restage the slots read in the previous step
-            if (kt + 1 < NKT) issue_b(kt + 1, (st + 1) & 1);
-            if (kt + 2 < NKT) issue_a(kt + 2, sla == 0 ? 2 : sla - 1);
-            sla = sla == 2 ? 0 : sla + 1;
         });
-    }
+    };
+#pragma unroll 1
+    for (int g = 0; g < NKT / 4 - 1; g++) group(g, std::false_type{});
+    group(NKT / 4 - 1, std::true_type{});
 
     // SwiGLU of gate tile i and up tile i (i = 0, 1: one 32-row h block)
 #pragma unroll
