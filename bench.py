@@ -125,12 +125,29 @@ def kernel_bytes(stage, T, U, shared, dn_q8=False, sh_q8=False):
         # down weights, h in, weighted rows out (f16 + an exponent byte per 16)
         dn = U * (Q8_MAT_BYTES if dn_q8 else MAT_BYTES) + (sh_mat if shared else 0)
         return dn + hq + P * (D * 2 + D // 16)
+    if stage == "expert":
+        # one kernel per skinny tile: gate/up and down weights, x in, h out
+        # (the tap copy; down reads it from LDS), weighted rows out
+        return (U * 3 * MAT_BYTES + (3 * sh_mat if shared else 0) + xq + hq
+                + P * (D * 2 + D // 16))
     raise ValueError(stage)
+
+
+def kernels_of(path):
+    """The grouped-GEMM kernels of a path: one per skinny tile on the
+    one-kernel skinny path (3), else gate/up and down."""
+    return ("expert",) if path == 3 else ("gateup", "down")
+
+
+def kernel_us(st_us, kernel):
+    """Replay-timed duration of a kernel: the fused skinny kernel is the
+    gateup stage's launch."""
+    return st_us["gateup"] if kernel == "expert" else st_us[kernel]
 
 
 def kernel_flops(stage, T, shared):
     P = T * K + (T if shared else 0)
-    return P * (2 * D * 2 * FF if stage == "gateup" else 2 * FF * D)
+    return P * {"gateup": 2 * D * 2 * FF, "down": 2 * FF * D, "expert": 3 * 2 * FF * D}[stage]
 
 
 def measured_traffic(config, stage):
@@ -329,6 +346,8 @@ class Bench:
         if path == 1:
             for st in ("route", "scan", "combine"):
                 st_us[st] = 0.0
+        if path == 3:             # gate/up and down in one kernel (the gateup stage)
+            st_us["down"] = 0.0
         self.step(0)              # `out` holds a real result again
         torch.cuda.synchronize()
         return U, path, st_us
@@ -337,14 +356,16 @@ class Bench:
         T, shared = self.T, self.shared
         by, fl = algorithmic(T, U, shared, dn_q8, sh_q8)
         r = {"tokens": T, "us_per_layer": ms_layer * 1e3, "tokens_per_s": T / (ms_layer * 1e-3),
-             "distinct_experts": U, "path": {0: "sorted_fat", 1: "direct", 2: "sorted_skinny"}.get(path, path),
+             "distinct_experts": U,
+             "path": {0: "sorted_fat", 1: "direct", 2: "sorted_skinny", 3: "sorted_fused"}.get(path, path),
              "layer_bytes": by, "layer_hbm_frac": by / (ms_layer * 1e-3) / 1e9 / HBM_PEAK_GBS,
              "layer_flops": fl, "layer_mfma_frac": fl / (ms_layer * 1e-3) / 1e12 / MFMA_FP8_PEAK_TFS,
              "stage_us": st_us}
-        for st in ("gateup", "down"):
+        for st in kernels_of(path):
+            us = kernel_us(st_us, st)
             kf, kb = kernel_flops(st, T, shared), kernel_bytes(st, T, U, shared, dn_q8, sh_q8)
-            r[st] = {"us": st_us[st], "mfma_frac": kf / (st_us[st] * 1e-6) / 1e12 / MFMA_FP8_PEAK_TFS,
-                     "hbm_frac": kb / (st_us[st] * 1e-6) / 1e9 / HBM_PEAK_GBS, "flops": kf, "bytes": kb}
+            r[st] = {"us": us, "mfma_frac": kf / (us * 1e-6) / 1e12 / MFMA_FP8_PEAK_TFS,
+                     "hbm_frac": kb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, "flops": kf, "bytes": kb}
         return r
 
 
@@ -437,21 +458,21 @@ def main():
 
     U, path, st_us = B.stage_times()
     head = B.summary(ms, U, path, st_us, dn_q8, sh_q8)
-    dom = "gateup" if st_us["gateup"] >= st_us["down"] else "down"
+    dom = max(kernels_of(path), key=lambda k: kernel_us(st_us, k))
     prefill = T >= 256
     if prefill:
         fl = kernel_flops(dom, T, shared)
-        ach = fl / (st_us[dom] * 1e-6) / 1e12
+        ach = fl / (kernel_us(st_us, dom) * 1e-6) / 1e12
         roof = {"bound": "mfma", "achieved": ach, "peak": MFMA_FP8_PEAK_TFS, "unit": "TFLOP/s",
                 "frac": ach / MFMA_FP8_PEAK_TFS, "traffic": None, "kernel": dom,
-                "kernel_us": st_us[dom], "flops_per_launch": fl,
+                "kernel_us": kernel_us(st_us, dom), "flops_per_launch": fl,
                 "layer_mfma_frac": head["layer_mfma_frac"], "layer_hbm_frac": head["layer_hbm_frac"]}
     else:
         by = kernel_bytes(dom, T, U, shared, dn_q8, sh_q8)
-        ach = by / (st_us[dom] * 1e-6) / 1e9
+        ach = by / (kernel_us(st_us, dom) * 1e-6) / 1e9
         roof = {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": ach / HBM_PEAK_GBS, "traffic": None, "kernel": dom,
-                "kernel_us": st_us[dom], "bytes_per_launch": by,
+                "kernel_us": kernel_us(st_us, dom), "bytes_per_launch": by,
                 "layer_hbm_frac": head["layer_hbm_frac"], "layer_bytes": head["layer_bytes"]}
     roof["traffic"] = None if host_up else measured_traffic(args.config, dom)
 
@@ -482,7 +503,7 @@ def main():
         "distinct_experts": U,
         "stage_us": st_us,
         "roofline": roof,
-        "grouped_gemms": {st: head[st] for st in ("gateup", "down")},
+        "grouped_gemms": {st: head[st] for st in kernels_of(path)},
     }
     # the other BASELINE configurations, measured in the same run on the same
     # weight layers: a HIP graph of one forward per layer, median of replays

@@ -238,11 +238,17 @@ int q36moe_forward_q8(q36moe_ctx *c, const q36moe_weights *w, const uint8_t *xq,
  * expert tile, weights staged through LDS) or skinny tiles (up to 32 rows,
  * weights streamed straight into registers); the direct path (no sort,
  * slots combined in registers) serves T <= 16 as two kernels (gate/up, then
- * down).  mode 0 picks the direct path for T <= 16, skinny tiles while
- * T*k <= 8*n_expert and fat tiles above; 1 forces sorted with fat tiles,
- * 4 sorted with skinny tiles, 2 direct (EINVAL from forward when T > 16).
- * Mode 3 (a one-kernel decode variant, measured slower) no longer exists:
- * EINVAL.  last_path: 0 sorted (fat), 1 direct, 2 sorted (skinny).  With the
+ * down).  Skinny tiles run either as one kernel per tile (gate/up, h kept
+ * in LDS, down) or as separate gate/up and down kernels; the one-kernel
+ * form needs MXFP4 down and shared-expert matrices.  mode 0 picks the
+ * direct path for T <= 16, skinny tiles (one kernel per tile where it
+ * applies) while T*k <= 8*n_expert and fat tiles above; 1 forces sorted with
+ * fat tiles, 4 sorted with skinny tiles as two kernels, 5 sorted with
+ * skinny tiles in one kernel per tile (two kernels for an int8 down or
+ * shared expert), 2 direct (EINVAL from forward when T > 16).  Mode 3 (a
+ * one-kernel decode variant, measured slower) no longer exists: EINVAL.
+ * last_path: 0 sorted (fat), 1 direct, 2 sorted (skinny, two kernels),
+ * 3 sorted (skinny, one kernel per tile).  With the
  * direct path the PERM/POS taps are the identity (rows in entry order) and
  * the EOFF/DNW taps are unavailable. */
 int q36moe_ctx_set_path(q36moe_ctx *c, int mode);

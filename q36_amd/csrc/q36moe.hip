@@ -800,6 +800,11 @@ __device__ __forceinline__ void dma16(const void *g, void *lds) {
 // for the stage about to be read is wait_vm's, and this wave's LDS reads of
 // the previous stage are complete before any wave passes the barrier and
 // restages that slot.
+// Workgroup barrier for LDS data only: __syncthreads() also waits for every
+// outstanding global load (vmcnt(0)), which drains prefetched weights.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
 __device__ __forceinline__ void dma_barrier() {
     // the scheduler may move MFMAs across an asm barrier: pin them (and all
     // else) to their step, or every step's fragments stay live at once
@@ -1647,6 +1652,308 @@ __global__ __launch_bounds__(64 * kDlW, Q8 ? 2 : 1) void k_down_lds(GemmArgs A) 
 }
 
 // ---------------------------------------------------------------------------
+// skinny tiles: the whole expert in one workgroup
+// ---------------------------------------------------------------------------
+// Workgroup = one skinny tile (expert e, sorted rows p0..p1, at most 32):
+// gate/up over all 512 rows of gate and up, SwiGLU and the e4m3
+// quantisation of h into LDS, then the down projection over all 2048 output
+// rows, staged weighted exactly as k_down_lds stages them.  h makes no round
+// trip through HBM between two launches, and one expert's down weights
+// stream while other workgroups are still in their gate/up.
+//   8 waves; wave w owns gate and up row tiles 4w..4w+3 (h rows 64w..64w+63,
+//   two quantisation blocks, one after the other) and down row tiles
+//   16w..16w+15.  Each step loads 8 KiB per wave -- two consecutive K-steps
+//   (2 KiB, contiguous in the packed layout) of 4 row tiles -- two steps
+//   ahead into three register buffers; 16 gate/up steps (8 per h block),
+//   then 8 down steps, all unrolled.  With one workgroup per CU a CU keeps
+//   ~128 KiB in flight; loads into VGPRs held HBM near its read rate from
+//   150 CUs, where direct-to-LDS staging topped out near 28 GB/s per CU.
+//   Runs of 2 KiB read ~5% slower than 8 KiB ones, but each B fragment read
+//   from LDS then feeds 4 MFMAs (with 8-KiB runs of one row tile, 1).
+//   x rows of the tile sit in LDS (2 KiB each, 16-byte chunk index XORed in
+//   its low 4 bits with the row, so a fragment read's 16 rows hit 16 bank
+//   groups); h rows in the dl_boff layout of k_down_lds.
+constexpr int kSxW = 8;
+constexpr int kSxRT = 1;   // row tiles per gate/up step
+constexpr int kBufFlags = 0x00020000;   // buffer resource word 3 (raw, 32-bit data format)
+struct SxLds {
+    __align__(16) uint8_t x[kSkTok * 2048];
+    __align__(16) uint8_t h[kSkTok * 512];
+    uint32_t hs[kSkTok][4];   // h scale dwords by lane group (lane-group-major order)
+    float ws[kSkTok];         // routing weight of each row
+};
+
+__device__ __forceinline__ int sx_off(int r, int c) { return r * 2048 + ((c & ~15) | ((c ^ r) & 15)) * 16; }
+
+template <int NJ, int RT>
+__device__ __forceinline__ void skinny_expert(const GemmArgs &G, const GemmArgs &Dn, int e, int p0, int p1,
+                                              SxLds &L) {
+    // RT row tiles per gate/up step, 8 / RT consecutive K-steps of each
+    static_assert(RT == 1 || RT == 2 || RT == 4, "row tiles per step");
+    constexpr int RD = RT == 4 ? 4 : 2;   // down row tiles per step (K = 4 K-steps)
+    constexpr int KG = 2048, NKG = KG / 128, KD = 512, NKD = KD / 128;
+    constexpr int NSG = 16, NSD = 8;   // gate/up and down steps
+    const int tid = threadIdx.x, lane = tid & 63, q = lane >> 4, n = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nr = p1 - p0;
+    const uint8_t *Wg = e < G.E ? G.wa + (size_t)e * G.wstride : G.sa;
+    const uint8_t *Wu = e < G.E ? G.wb + (size_t)e * G.wstride : G.sb;
+    const uint8_t *Wd = e < Dn.E ? Dn.wa + (size_t)e * Dn.wstride : Dn.sa;
+    const int nibg = 512 * KG / 2, nibd = 2048 * KD / 2;
+    const uint32_t lo16 = (uint32_t)lane * 16;
+    // Buffer loads: one offset VGPR (the lane's) for every load, the
+    // fragment's offset in an SGPR; with plain pointers the compiler keeps a
+    // 64-bit address per fragment live across the unrolled steps.
+    const __amdgpu_buffer_rsrc_t rg = __builtin_amdgcn_make_buffer_rsrc((void *)Wg, (short)0, (int)G.wstride, kBufFlags);
+    const __amdgpu_buffer_rsrc_t ru = __builtin_amdgcn_make_buffer_rsrc((void *)Wu, (short)0, (int)G.wstride, kBufFlags);
+    const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc((void *)Wd, (short)0, (int)Dn.wstride, kBufFlags);
+    // A step's operands: 8 weight fragments -- RT row tiles x 8/RT
+    // consecutive K-steps (contiguous in the packed layout) -- and the row
+    // tiles' scale dwords (byte kt & 3 of dword kt >> 2 in gate/up, byte kd
+    // in down).  Gate/up: h block s >> 3, its row tiles a = 0..3 (gate rr0,
+    // up rr0, gate rr1, up rr1; rr = row tile within the block) in groups of
+    // RT, each group over the 16 K-steps.  Down: pass d >> 1 over row
+    // tiles 16w + 4 pass .. +3 in two steps (RD row tiles, 8/RD K-steps).
+    struct Step { u32x4 f[8]; uint32_t sc[4]; };
+    auto load = [&](auto S, Step &b) {
+        constexpr int st = decltype(S)::value;
+        if constexpr (st < NSG) {
+            constexpr int blk = st >> 3, m = st & 7, KS = 8 / RT;
+            constexpr int a0 = (m / (16 / KS)) * RT, kt0 = (m % (16 / KS)) * KS;
+#pragma unroll
+            for (int ai = 0; ai < RT; ai++) {
+                const int a = a0 + ai;
+                const __amdgpu_buffer_rsrc_t r = (a & 1) ? ru : rg;
+                const int mt = 4 * wave + 2 * blk + (a >> 1);
+#pragma unroll
+                for (int k = 0; k < KS; k++)
+                    b.f[KS * ai + k] = __builtin_amdgcn_raw_buffer_load_b128(r, lo16, (mt * NKG + kt0 + k) * 1024, 0);
+                if constexpr (KS <= 4)
+                    b.sc[ai] = __builtin_amdgcn_raw_buffer_load_b32(r, lo16, nibg + mt * 1024 + 4 * (kt0 >> 2), 0);
+                else {
+                    b.sc[2 * ai] = __builtin_amdgcn_raw_buffer_load_b32(r, lo16, nibg + mt * 1024 + 4 * (kt0 >> 2), 0);
+                    b.sc[2 * ai + 1] = __builtin_amdgcn_raw_buffer_load_b32(r, lo16, nibg + mt * 1024 + 4 * (kt0 >> 2) + 4, 0);
+                }
+            }
+        } else {
+            constexpr int d = st - NSG, KS = 8 / RD, ps = d >> 1, g = d & 1;
+#pragma unroll
+            for (int ai = 0; ai < RD; ai++) {
+                const int mt = 16 * wave + 4 * ps + (RD == 4 ? ai : 2 * g + ai);
+#pragma unroll
+                for (int k = 0; k < KS; k++)
+                    b.f[KS * ai + k] = __builtin_amdgcn_raw_buffer_load_b128(
+                        rd, lo16, (mt * NKD + (RD == 4 ? 2 * g : 0) + k) * 1024, 0);
+                b.sc[ai] = __builtin_amdgcn_raw_buffer_load_b32(rd, (uint32_t)lane * 4, nibd + mt * 256, 0);
+            }
+        }
+    };
+    // Prologue, in this order (sched barriers keep it): weight step 0; the
+    // x rows of the tile (rows past the tile repeat its last row; never
+    // stored), their B scales and routing weights; weight step 1.  Waiting
+    // for the x rows (loads complete in order) then leaves step 1 in flight.
+    Step bs[3];   // three step buffers, loads two steps ahead of the MFMAs
+    load(std::integral_constant<int, 0>{}, bs[0]);
+    __builtin_amdgcn_sched_barrier(0);
+    const int xr_r = tid >> 4, xr_c = tid & 15;
+    u32x4 xv[8];
+    {
+        const int tok = G.row_tok[p0 + min(xr_r, nr - 1)];
+        const uint8_t *xr = G.bq + (size_t)tok * KG;
+#pragma unroll
+        for (int u = 0; u < 8; u++) xv[u] = *reinterpret_cast<const u32x4 *>(xr + (xr_c + 16 * u) * 16);
+    }
+    u32x4 sb[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const int tok = G.row_tok[p0 + min(16 * j + n, nr - 1)];
+        sb[j] = *reinterpret_cast<const u32x4 *>(G.bs2 + (size_t)tok * (KG / 32) + q * 16);
+    }
+    const float wrow = G.row_w[p0 + min(tid & (kSkTok - 1), nr - 1)];
+    __builtin_amdgcn_sched_barrier(0);
+    load(std::integral_constant<int, 1>{}, bs[1]);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < 8; u++) *reinterpret_cast<u32x4 *>(&L.x[sx_off(xr_r, xr_c + 16 * u)]) = xv[u];
+    if (tid < kSkTok) L.ws[tid] = wrow;
+    lds_barrier();
+
+    v4f acc[4][NJ];
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int j = 0; j < NJ; j++) acc[a][j] = v4f{0.f, 0.f, 0.f, 0.f};
+    // LDS byte offsets of this lane's B fragment halves (hh = 0: K 16q..,
+    // hh = 1: K 64+16q..) for K-steps of parity par, column tile 0: the
+    // swizzled chunk's low 4 bits depend only on (par, hh, q) ^ n, so K-step
+    // kt adds (kt >> 1) * 256 and column tile j adds j rows (immediates)
+    int xo[2][2], ho[2][2];
+#pragma unroll
+    for (int par = 0; par < 2; par++)
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+            const int lo = ((8 * par + 4 * hh + q) ^ n) & 15;
+            xo[par][hh] = n * 2048 + lo * 16;   // = sx_off(n, 8 * par + 4 * hh + q)
+            ho[par][hh] = n * 512 + lo * 16;    // = dl_boff(n, 8 * par + 4 * hh + q)
+        }
+    // B fragment of K-step kt (x) or kd (h) for column tile j
+    auto xfrag = [&](int kt, int j) {
+        const int o = j * 16 * 2048 + (kt >> 1) * 256;
+        const u32x4 b0 = *reinterpret_cast<const u32x4 *>(&L.x[xo[kt & 1][0] + o]);
+        const u32x4 b1 = *reinterpret_cast<const u32x4 *>(&L.x[xo[kt & 1][1] + o]);
+        return v8i{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
+    };
+    auto hfrag = [&](int kd, int j) {
+        const int o = j * 16 * 512 + (kd >> 1) * 256;
+        const u32x4 b0 = *reinterpret_cast<const u32x4 *>(&L.h[ho[kd & 1][0] + o]);
+        const u32x4 b1 = *reinterpret_cast<const u32x4 *>(&L.h[ho[kd & 1][1] + o]);
+        return v8i{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
+    };
+    // per K-step of the step: its B fragment (read once) against the RT row
+    // tiles
+    auto gu_step = [&](auto S, const Step &b) {
+        constexpr int st = decltype(S)::value, m = st & 7, KS = 8 / RT;
+        constexpr int a0 = (m / (16 / KS)) * RT, kt0 = (m % (16 / KS)) * KS;
+        static_for<0, KS>([&](auto K) {
+            constexpr int k = decltype(K)::value, kt = kt0 + k, sel = kt & 3;
+#pragma unroll
+            for (int j = 0; j < NJ; j++) {
+                const v8i bv = xfrag(kt, j);
+#pragma unroll
+                for (int ai = 0; ai < RT; ai++) {
+                    const u32x4 fr = b.f[KS * ai + k];
+                    const v8i av = v8i{(int)fr[0], (int)fr[1], (int)fr[2], (int)fr[3], 0, 0, 0, 0};
+                    const int sa = KS <= 4 ? (int)b.sc[ai] : (int)b.sc[2 * ai + (k >> 2)];
+                    acc[a0 + ai][j] = mfma_f4xf8<sel, sel>(av, bv, acc[a0 + ai][j], sa, (int)sb[j][kt >> 2]);
+                }
+            }
+        });
+    };
+    uint32_t hsv[NJ];   // h scale dword of this lane's column in each column tile
+    auto dn_step = [&](auto S, const Step &b) {
+        constexpr int d = decltype(S)::value - NSG, KS = 8 / RD, g = d & 1;
+        constexpr int a0 = RD == 4 ? 0 : 2 * g, kd0 = RD == 4 ? 2 * g : 0;
+        static_for<0, KS>([&](auto K) {
+            constexpr int k = decltype(K)::value, kd = kd0 + k;
+#pragma unroll
+            for (int j = 0; j < NJ; j++) {
+                const v8i bv = hfrag(kd, j);
+#pragma unroll
+                for (int ai = 0; ai < RD; ai++) {
+                    const u32x4 fr = b.f[KS * ai + k];
+                    const v8i av = v8i{(int)fr[0], (int)fr[1], (int)fr[2], (int)fr[3], 0, 0, 0, 0};
+                    acc[a0 + ai][j] = mfma_f4xf8<kd, kd>(av, bv, acc[a0 + ai][j], (int)b.sc[ai], (int)hsv[j]);
+                }
+            }
+        });
+    };
+    // SwiGLU of h block 2w+blk: gate row tiles 4w+2blk+rr in acc[2rr], up in
+    // acc[2rr+1]
+    auto swiglu = [&](int blk) {
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            const int r = 16 * j + n, p = p0 + r;
+            const bool valid = r < nr;
+            float h[2][4];
+#pragma unroll
+            for (int rr = 0; rr < 2; rr++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) h[rr][i] = silu(acc[2 * rr][j][i]) * acc[2 * rr + 1][j][i];
+            float amax = 0.0f;
+#pragma unroll
+            for (int rr = 0; rr < 2; rr++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) amax = fmaxf(amax, fabsf(h[rr][i]));
+            amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+            amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+            const int e2 = quant_exp(amax);
+            const float mul = inv_scale(e2);
+            const int ffb = 64 * wave + 32 * blk, b = ffb / 32;
+#pragma unroll
+            for (int rr = 0; rr < 2; rr++) {
+                const uint32_t c = e4m3x4(h[rr][0] * mul, h[rr][1] * mul, h[rr][2] * mul, h[rr][3] * mul);
+                *reinterpret_cast<uint32_t *>(&L.h[dl_boff(r, (ffb >> 4) + rr) + 4 * q]) = c;
+                if (valid) *reinterpret_cast<uint32_t *>(G.hq + (size_t)p * KD + ffb + 16 * rr + 4 * q) = c;
+            }
+            if (q == 0) {
+                reinterpret_cast<uint8_t *>(L.hs[r])[(b & 3) * 4 + (b >> 2)] = (uint8_t)(127 + e2);
+                if (valid) {
+                    G.hs[(size_t)p * (KD / 32) + b] = (uint8_t)(127 + e2);
+                    G.hs2[(size_t)p * (KD / 32) + (b & 3) * 4 + (b >> 2)] = (uint8_t)(127 + e2);
+                }
+            }
+#pragma unroll
+            for (int a = 0; a < 4; a++) acc[a][j] = v4f{0.f, 0.f, 0.f, 0.f};
+        }
+    };
+    // down row tiles mt0 .. mt0+3 finished (acc[0..3]): weight, stage as
+    // f16 + exponent, clear
+    auto dn_store = [&](int mt0) {
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            const int r = 16 * j + n;
+            const v4f c4[4] = {acc[0][j], acc[1][j], acc[2][j], acc[3][j]};
+            store_dn16x4(Dn, p0 + r, mt0, q, r < nr, c4, L.ws[r]);
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+        }
+    };
+    static_for<0, NSG + NSD>([&](auto S) {
+        constexpr int st = decltype(S)::value;
+        auto &ac = acc;   // named here: an asm operand alone does not capture it
+        // one step per scheduling region: otherwise later steps' loads are
+        // hoisted and every step's fragments are live at once
+        __builtin_amdgcn_sched_barrier(0);
+        // issue step st+2 into the buffer step st-1 used, then compute step st
+        if constexpr (st + 2 < NSG + NSD) load(std::integral_constant<int, st + 2>{}, bs[(st + 2) % 3]);
+        // order inside the step: the next step's loads first, then per
+        // K-step and column tile its B fragment read and 4 MFMAs
+        if constexpr (st + 2 < NSG + NSD) {
+            constexpr int nl = st + 2 < NSG ? 8 + (RT == 1 ? 2 : RT) : 8 + RD;
+            __builtin_amdgcn_sched_group_barrier(0x020, nl, 0);
+        }
+        // B fragment i+1 is read before the MFMAs of fragment i issue
+        constexpr int rts = st < NSG ? RT : RD, nfr = 8 / rts * NJ;
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+        for (int i = 0; i < nfr; i++) {
+            if (i + 1 < nfr) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, rts, 0);
+        }
+        if constexpr (st < NSG) {
+            gu_step(S, bs[st % 3]);
+            if constexpr ((st & 7) == 7) swiglu(st >> 3);
+            if constexpr (st == NSG - 1) {
+                lds_barrier();   // every wave's h rows in LDS
+#pragma unroll
+                for (int j = 0; j < NJ; j++) hsv[j] = L.hs[16 * j + n][q];
+            }
+        } else {
+            dn_step(S, bs[st % 3]);
+            // two steps per pass of 4 row tiles
+            if constexpr (((st - NSG) & 1) == 1) dn_store(16 * wave + 4 * ((st - NSG) >> 1));
+        }
+        // pin this step's MFMAs here: without a use the compiler sinks them
+        // to the end and keeps every step's fragments live
+#pragma unroll
+        for (int a = 0; a < 4; a++)
+#pragma unroll
+            for (int j = 0; j < NJ; j++) asm volatile("" : "+v"(ac[a][j]));
+    });
+}
+
+__global__ __launch_bounds__(64 * kSxW) void k_skinny_expert(GemmArgs G, GemmArgs Dn) {
+    __shared__ SxLds L;
+    const int ti = blockIdx.x;
+    if (ti >= *G.ntiles) return;
+    const int4 tile = G.tiles[ti];
+    const int e = __builtin_amdgcn_readfirstlane(tile.x);
+    const int p0 = __builtin_amdgcn_readfirstlane(tile.y), p1 = __builtin_amdgcn_readfirstlane(tile.z);
+    if (p1 - p0 <= 16) skinny_expert<1, kSxRT>(G, Dn, e, p0, p1, L);
+    else skinny_expert<2, kSxRT>(G, Dn, e, p0, p1, L);
+}
+
+// ---------------------------------------------------------------------------
 // direct path for small batches (decode): no sort, two kernels
 // ---------------------------------------------------------------------------
 struct DirectArgs {
@@ -2132,7 +2439,7 @@ struct q36moe_weights {
 // Kernel arguments of the last forward; the weights are bound per launch so
 // a stage can be replayed over other weight sets (q36moe_ctx_replay).
 struct Plan {
-    int T, has_sh, direct, skinny, tiles, nb;
+    int T, has_sh, direct, skinny, fused, tiles, nb;
     RouteArgs ra;
     ScanArgs sa;
     GemmArgs ga, da;
@@ -2165,7 +2472,8 @@ struct q36moe_ctx {
     Scratch s;
     void *base;
     const uint8_t *tap_xq, *tap_xs;   // where the last forward's quantised x is
-    int path_mode;                  // 0 auto, 1 sorted (fat tiles), 2 direct, 4 sorted (skinny tiles)
+    int path_mode;                  // 0 auto, 1 sorted (fat tiles), 2 direct, 4 sorted (skinny tiles, two
+                                    // kernels), 5 sorted (skinny tiles, one kernel per tile)
     int last_T, last_sh, last_path;
     int timing;
     Plan *plan;                     // kernel arguments of the last forward
@@ -2566,7 +2874,9 @@ static void launch_stage(const Scratch &c, const Plan &P, int st, hipStream_t s)
             hipLaunchKernelGGL(k_scatter, dim3(P.nb), dim3(256), 0, s, P.sa);
             break;
         case ST_GATEUP:
-            if (P.skinny) {
+            if (P.fused) {
+                hipLaunchKernelGGL(k_skinny_expert, dim3(P.tiles), dim3(64 * kSxW), 0, s, P.ga, P.da);
+            } else if (P.skinny) {
                 hipLaunchKernelGGL(k_skinny_gateup, dim3(P.tiles * 16), dim3(64 * kSkW), 0, s, P.ga);
                 if (P.ga.shq8)
                     hipLaunchKernelGGL(k_shared_gateup_q8, dim3((T + kShTok - 1) / kShTok, kShRb), dim3(256), 0, s,
@@ -2576,6 +2886,7 @@ static void launch_stage(const Scratch &c, const Plan &P, int st, hipStream_t s)
                                    dim3(64 * gdma::W), 0, s, P.ga);
             break;
         case ST_DOWN:
+            if (P.fused) break;   // in k_skinny_expert
             if (P.da.hq8 || P.da.shq8)
                 hipLaunchKernelGGL(k_down_lds<true>, dim3(P.tiles * (D / (16 * kDlRT * kDlW))), dim3(64 * kDlW), 0, s,
                                    P.da);
@@ -2631,7 +2942,7 @@ static int launch_forward(const Scratch &c, Plan &P, int pm, const q36moe_weight
     const int tpb = T <= kRouteSmallT ? kRouteTPBSmall : kRouteTPB;
     const int nb = (T + tpb - 1) / tpb;
 
-    const bool direct = pm == 2 ? (T <= kDirectMaxT) : (pm == 1 || pm == 4) ? false : (T <= kDirectMaxT);
+    const bool direct = pm == 2 ? (T <= kDirectMaxT) : (pm == 1 || pm == 4 || pm == 5) ? false : (T <= kDirectMaxT);
     if (pm == 2 && !direct) return Q36MOE_EINVAL;
     const bool shq8 = has_sh && w->sh_q8;
     // a q8_0-split shared expert quantises x itself (int8 + fp32 per 32):
@@ -2639,7 +2950,10 @@ static int launch_forward(const Scratch &c, Plan &P, int pm, const q36moe_weight
     if (shq8 && x_fmt == kFmtE4M3) return Q36MOE_EINVAL;
     // sorted path: skinny tiles (<= 32 rows) while the average expert has at
     // most kSkinnyRows rows, else fat tiles of up to kGdTok rows
-    const bool skinny = pm == 4 || (pm == 0 && (size_t)n <= (size_t)kSkinnyRows * E);
+    const bool skinny = pm == 4 || pm == 5 || (pm == 0 && (size_t)n <= (size_t)kSkinnyRows * E);
+    // skinny tiles in one kernel per tile (k_skinny_expert) when every
+    // matrix is MXFP4; the int8 down or shared expert keeps two kernels
+    const bool fused = skinny && pm != 4 && !w->dn_q8 && !shq8;
     const int tn = skinny ? kSkTok : kGdTok;
     // a q8_0-split shared expert's down is VALU-heavy: its rows go in small
     // tiles so the work spreads over many workgroups instead of trailing
@@ -2648,7 +2962,7 @@ static int launch_forward(const Scratch &c, Plan &P, int pm, const q36moe_weight
     tiles = (tiles + 7) & ~7;   // whole groups of 8 for the XCD-major tile order
 
     P = Plan{};
-    P.T = T; P.has_sh = has_sh; P.direct = direct; P.skinny = skinny;
+    P.T = T; P.has_sh = has_sh; P.direct = direct; P.skinny = skinny; P.fused = fused;
     P.tiles = tiles; P.nb = nb; P.out = out; P.out_fmt = out_fmt;
     if (direct) {
         P.di = DirectArgs{logits, ld_logits, T, E, K, scale, x, x_fmt, shg, ld_shg,
@@ -2701,7 +3015,7 @@ static int forward_impl(q36moe_ctx *c, const q36moe_weights *w, const void *x, i
     *c->plan = P;
     c->last_T = T;
     c->last_sh = P.has_sh;
-    c->last_path = P.direct ? 1 : P.skinny ? 2 : 0;
+    c->last_path = P.direct ? 1 : P.fused ? 3 : P.skinny ? 2 : 0;
     // the sorted path reads pre-quantised codes in place; the direct path
     // copies every token's codes into the context
     const bool in_place = !P.direct && x_fmt == kFmtE4M3;
@@ -2844,7 +3158,7 @@ int q36moe_ctx_copy_tap(q36moe_ctx *c, int tap, void *dst, size_t bytes, size_t 
 }
 
 int q36moe_ctx_set_path(q36moe_ctx *c, int mode) {
-    if (!c || mode < 0 || mode > 4 || mode == 3) return Q36MOE_EINVAL;
+    if (!c || mode < 0 || mode > 5 || mode == 3) return Q36MOE_EINVAL;
     c->path_mode = mode;
     return Q36MOE_OK;
 }

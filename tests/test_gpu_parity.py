@@ -247,7 +247,7 @@ def _check_routing(layer, oracle, lg, E=256, k=8):
     np.testing.assert_array_equal(gi, oi)
     gw = layer.tap(moe.TAP_TOPK_W).cpu().double().numpy()
     assert np.abs(gw - ow).max() <= 2e-6
-    if layer.last_path in (0, 2):   # sorted paths: offsets and permutation bit-exact
+    if layer.last_path in (0, 2, 3):   # sorted paths: offsets and permutation bit-exact
         off, perm, pos = oracle.sort_entries(gi, E)
         np.testing.assert_array_equal(layer.tap(moe.TAP_EOFF).cpu().numpy(), off)
         np.testing.assert_array_equal(layer.tap(moe.TAP_PERM).cpu().numpy(), perm)
@@ -317,7 +317,7 @@ def _check_layer(name, dev, oracle, layer_w, x, lg, shg, sample=None, x_dtype=to
     w, dw = layer_w
     T = x.shape[0]
     layer, y32, y16 = _run_layer(dev, dw, x, lg, shg, x_dtype=x_dtype, path=path)
-    name = f"{name}/{({1: 'direct', 2: 'sorted_skinny'}).get(layer.last_path, 'sorted')}"
+    name = f"{name}/{({1: 'direct', 2: 'sorted_skinny', 3: 'sorted_fused'}).get(layer.last_path, 'sorted')}"
     gi = _check_routing(layer, oracle, lg)
     oq, os_ = oracle.quant_e4m3(x)
     np.testing.assert_array_equal(layer.tap(moe.TAP_XQ).cpu().numpy(), oq)
@@ -398,7 +398,7 @@ def _check_layer(name, dev, oracle, layer_w, x, lg, shg, sample=None, x_dtype=to
 
 
 PATHS = [pytest.param(1, id="sorted"), pytest.param(4, id="sorted_skinny"),
-         pytest.param(2, id="direct")]
+         pytest.param(5, id="sorted_fused"), pytest.param(2, id="direct")]
 
 
 @pytest.mark.parametrize("path", PATHS)
@@ -411,7 +411,8 @@ def test_forward_decode1(dev, oracle, layer_w, path):
 # the automatic choice), with Zipf routing on every other case and the
 # shared expert on some: (T, path, zipf, shared).
 SWEEP = [(3, 2, False, True), (9, 4, True, False), (17, 0, False, False), (31, 1, True, True),
-         (100, 4, False, True), (257, 0, True, False), (1000, 1, False, False), (2049, 0, True, True)]
+         (48, 5, True, True), (100, 4, False, True), (200, 5, False, False), (257, 0, True, False),
+         (1000, 1, False, False), (2049, 0, True, True)]
 
 
 @pytest.mark.parametrize("T,path,zipf,shared", SWEEP, ids=[f"T{c[0]}_p{c[1]}" for c in SWEEP])
@@ -447,7 +448,7 @@ def test_direct_equals_sorted_inputs(dev, layer_w, T):
     rng = np.random.default_rng(900 + T)
     x, lg = synth.hidden(rng, T), synth.normal_logits(rng, T)
     outs, taps = [], []
-    for path in (1, 2, 4):
+    for path in (1, 2, 4, 5):
         layer, y32, _ = _run_layer(dev, dw, x, lg, None, path=path)
         outs.append(y32)
         taps.append([layer.tap(m).cpu().numpy() for m in (moe.TAP_TOPK_IDX, moe.TAP_TOPK_W,
@@ -460,7 +461,8 @@ def test_direct_equals_sorted_inputs(dev, layer_w, T):
         assert normwise <= TOL
 
 
-@pytest.mark.parametrize("path", [pytest.param(0, id="auto_skinny"), pytest.param(1, id="sorted")])
+@pytest.mark.parametrize("path", [pytest.param(0, id="auto_fused"), pytest.param(4, id="sorted_skinny"),
+                                  pytest.param(1, id="sorted")])
 def test_forward_ragged64_zipf(dev, oracle, layer_w, path):
     x, lg, _ = synth.config_inputs("ragged64", 2)
     _check_layer("ragged64", dev, oracle, layer_w, x, lg, None, path=path)
@@ -641,7 +643,7 @@ def test_add_rmsnorm_quant(dev, oracle, T, with_a):
     np.testing.assert_array_equal(xs.cpu().numpy(), os_)
 
 
-@pytest.mark.parametrize("T,path", [(1, 0), (5, 2), (40, 4), (40, 1), (600, 0)])
+@pytest.mark.parametrize("T,path", [(1, 0), (5, 2), (40, 4), (40, 5), (40, 1), (600, 0)])
 def test_forward_q8_equals_forward(dev, layer_w, T, path):
     """The pre-quantised entry gives bit-identical results (outputs and
     routing/quantisation taps) to forward on the x it was quantised from, on
@@ -663,13 +665,13 @@ def test_forward_q8_equals_forward(dev, layer_w, T, path):
         np.testing.assert_array_equal(la.tap(tap).cpu().numpy(), lb.tap(tap).cpu().numpy())
 
 
-@pytest.mark.parametrize("T,path", [(1, 2), (5, 2), (40, 4), (600, 1)])
+@pytest.mark.parametrize("T,path", [(1, 2), (5, 2), (40, 5), (600, 1)])
 def test_forward_strided_shared_gate(dev, layer_w, T, path):
     """The reference's batched decode keeps the shared-gate logit in column
     256 of each 257-wide router row (q36_engine.cu:2092-2095): forward takes
     logits = rows[:, :256] and shg = rows[:, 256] (stride 257) directly and
-    gives the same bits as the gathered contiguous copy, on the direct, skinny
-    and fat paths."""
+    gives the same bits as the gathered contiguous copy, on the direct,
+    skinny (one kernel per tile) and fat paths."""
     _, dw = layer_w
     rng = np.random.default_rng(1200 + T)
     rows = np.concatenate([synth.normal_logits(rng, T), rng.standard_normal((T, 1)).astype(np.float32)], axis=1)
