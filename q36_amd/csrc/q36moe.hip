@@ -1662,14 +1662,17 @@ __global__ __launch_bounds__(64 * kDlW, Q8 ? 2 : 1) void k_down_lds(GemmArgs A) 
 // stream while other workgroups are still in their gate/up.
 //   8 waves; wave w owns gate and up row tiles 4w..4w+3 (h rows 64w..64w+63,
 //   two quantisation blocks, one after the other) and down row tiles
-//   16w..16w+15.  Each step loads 8 KiB per wave -- two consecutive K-steps
-//   (2 KiB, contiguous in the packed layout) of 4 row tiles -- two steps
-//   ahead into three register buffers; 16 gate/up steps (8 per h block),
-//   then 8 down steps, all unrolled.  With one workgroup per CU a CU keeps
-//   ~128 KiB in flight; loads into VGPRs held HBM near its read rate from
-//   150 CUs, where direct-to-LDS staging topped out near 28 GB/s per CU.
-//   Runs of 2 KiB read ~5% slower than 8 KiB ones, but each B fragment read
-//   from LDS then feeds 4 MFMAs (with 8-KiB runs of one row tile, 1).
+//   16w..16w+15.  Each step loads 8 KiB per wave, contiguous in the packed
+//   layout, two steps ahead into three register buffers: 16 gate/up steps
+//   (8 per h block), then 8 down steps, all unrolled.  With one workgroup
+//   per CU a CU keeps ~128 KiB in flight; loads into VGPRs held HBM near
+//   its read rate from 150 CUs, where direct-to-LDS staging topped out near
+//   28 GB/s per CU.  The kernel is bound by the weight stream (without its
+//   MFMAs it takes as long), and the stream by the length of the runs it
+//   reads: RT row tiles x 8/RT K-steps per step measured 51 / 53 / 60 us at
+//   decode32 for RT = 1 / 2 / 4 (8 / 4 / 2 KiB runs); 16 KiB steps (one
+//   whole row tile) 51.6.  RT = 1 is used, although each B fragment read
+//   from LDS then feeds only NJ MFMAs.
 //   x rows of the tile sit in LDS (2 KiB each, 16-byte chunk index XORed in
 //   its low 4 bits with the row, so a fragment read's 16 rows hit 16 bank
 //   groups); h rows in the dl_boff layout of k_down_lds.
@@ -2329,30 +2332,52 @@ __device__ __forceinline__ float4 load_dn16(const uint16_t *__restrict__ dnh, co
     return make_float4(f16lo(h.x) * sc, f16hi(h.x) * sc, f16lo(h.y) * sc, f16hi(h.y) * sc);
 }
 
+// Combine: token t's weighted rows summed in slot order (then the shared
+// row), 8 columns per thread; every slot's load is issued before the first
+// add, so a token costs one round trip after its slot positions.  Block
+// (t, column block of 8 * blockDim.x).
 __global__ __launch_bounds__(256) void k_combine(const uint16_t *__restrict__ dnh, const uint8_t *__restrict__ dne,
                                                 const int32_t *__restrict__ pos, int T, int k,
                                                 int D, int has_sh, void *out, int out_fmt) {
     const int t = blockIdx.x;
+    const int j = (blockIdx.y * blockDim.x + threadIdx.x) * 8;
+    if (j >= D) return;
     const int n = T * k;
-    for (int j = threadIdx.x * 4; j < D; j += 256 * 4) {
-        float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (int s = 0; s < k; s++) {
-            const int p = pos[(size_t)t * k + s];
-            const float4 v = load_dn16(dnh, dne, D, (size_t)p, j);
-            a.x += v.x; a.y += v.y; a.z += v.z; a.w += v.w;
+    uint4 hv[kMaxTopK + 1];
+    uint32_t ev[kMaxTopK + 1];
+    const int ns = k + (has_sh ? 1 : 0);
+#pragma unroll
+    for (int s = 0; s < kMaxTopK + 1; s++) {
+        if (s < ns) {
+            const size_t p = s < k ? (size_t)pos[(size_t)t * k + s] : (size_t)(n + t);
+            hv[s] = *reinterpret_cast<const uint4 *>(dnh + p * D + j);
+            ev[s] = dne[p * (D / 16) + (j >> 4)];
         }
-        if (has_sh) {
-            const float4 v = load_dn16(dnh, dne, D, (size_t)(n + t), j);
-            a.x += v.x; a.y += v.y; a.z += v.z; a.w += v.w;
+    }
+    float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < kMaxTopK + 1; s++) {
+        if (s < ns) {
+            const float sc = __uint_as_float((ev[s] - 14u) << 23);
+            const uint32_t w[4] = {hv[s].x, hv[s].y, hv[s].z, hv[s].w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                a[2 * i] += f16lo(w[i]) * sc;
+                a[2 * i + 1] += f16hi(w[i]) * sc;
+            }
         }
-        if (out_fmt == Q36MOE_FMT_F32) {
-            *reinterpret_cast<float4 *>(static_cast<float *>(out) + (size_t)t * D + j) = a;
-        } else {
-            const uint32_t lo = f32_to_bf16(a.x) | (f32_to_bf16(a.y) << 16);
-            const uint32_t hi = f32_to_bf16(a.z) | (f32_to_bf16(a.w) << 16);
-            *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(out) + (size_t)t * D + j) =
-                make_uint2(lo, hi);
-        }
+    }
+    if (out_fmt == Q36MOE_FMT_F32) {
+        float4 *o = reinterpret_cast<float4 *>(static_cast<float *>(out) + (size_t)t * D + j);
+        o[0] = make_float4(a[0], a[1], a[2], a[3]);
+        o[1] = make_float4(a[4], a[5], a[6], a[7]);
+    } else {
+        uint4 o;
+        o.x = f32_to_bf16(a[0]) | (f32_to_bf16(a[1]) << 16);
+        o.y = f32_to_bf16(a[2]) | (f32_to_bf16(a[3]) << 16);
+        o.z = f32_to_bf16(a[4]) | (f32_to_bf16(a[5]) << 16);
+        o.w = f32_to_bf16(a[6]) | (f32_to_bf16(a[7]) << 16);
+        *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(out) + (size_t)t * D + j) = o;
     }
 }
 
@@ -2895,7 +2920,9 @@ static void launch_stage(const Scratch &c, const Plan &P, int st, hipStream_t s)
                                    s, P.da);
             break;
         case ST_COMBINE:
-            hipLaunchKernelGGL(k_combine, dim3(T), dim3(256), 0, s, c.dnh, c.dne, c.pos, T, K, D, P.has_sh,
+            // small batches: 64-thread blocks, so the work spreads over more CUs
+            hipLaunchKernelGGL(k_combine, dim3(T, T < 256 ? D / 512 : D / 2048), dim3(T < 256 ? 64 : 256), 0, s, c.dnh,
+                               c.dne, c.pos, T, K, D, P.has_sh,
                                const_cast<void *>(P.out), P.out_fmt);
             break;
         default: break;
