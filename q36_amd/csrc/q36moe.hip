@@ -1684,6 +1684,27 @@ struct SxLds {
     __align__(16) uint8_t h[kSkTok * 512];
     uint32_t hs[kSkTok][4];   // h scale dwords by lane group (lane-group-major order)
     float ws[kSkTok];         // routing weight of each row
+    int tok[kSkTok];          // token of each row (rows past the tile repeat its last)
+    // tile discovery: per-expert counts, their exclusive prefixes, tiles per
+    // expert and theirs, per-wave counts, the tile found
+    int cnt[kMaxExperts], off[kMaxExperts + 1], ntl[kMaxExperts], toff[kMaxExperts + 1];
+    int wsum[kSxW];
+    int sel;
+};
+
+// Tile discovery for k_skinny_expert (in place of k_scatter): every
+// workgroup counts the routed entries per expert from the top-k indices,
+// scans the counts into offsets and 32-row tiles, finds its own tile and
+// gathers that tile's entries in entry order -- the stable sorted order of
+// k_scatter, so perm / pos / e_off come out identical.  At most
+// kSxDiscoverMax routed entries (4 per thread).
+constexpr int kSxDiscoverMax = 4 * 64 * kSxW;
+struct SxArgs {
+    const int32_t *idx; const float *wt;   // top-k routing of each entry
+    const float *shg; int ld_shg;          // shared-gate logits (shared tiles), or null
+    int32_t *perm, *pos, *e_off;           // sorted order out (taps; pos feeds the combine)
+    int T, k, E;
+    int discover;                          // 0: tiles from k_scatter
 };
 
 __device__ __forceinline__ int sx_off(int r, int c) { return r * 2048 + ((c & ~15) | ((c ^ r) & 15)) * 16; }
@@ -1752,16 +1773,16 @@ __device__ __forceinline__ void skinny_expert(const GemmArgs &G, const GemmArgs 
         }
     };
     // Prologue, in this order (sched barriers keep it): weight step 0; the
-    // x rows of the tile (rows past the tile repeat its last row; never
-    // stored), their B scales and routing weights; weight step 1.  Waiting
-    // for the x rows (loads complete in order) then leaves step 1 in flight.
+    // x rows of the tile (L.tok: rows past the tile repeat its last row,
+    // never stored) and their B scales; weight step 1.  Waiting for the x
+    // rows (loads complete in order) then leaves step 1 in flight.
     Step bs[3];   // three step buffers, loads two steps ahead of the MFMAs
     load(std::integral_constant<int, 0>{}, bs[0]);
     __builtin_amdgcn_sched_barrier(0);
     const int xr_r = tid >> 4, xr_c = tid & 15;
     u32x4 xv[8];
     {
-        const int tok = G.row_tok[p0 + min(xr_r, nr - 1)];
+        const int tok = L.tok[xr_r];
         const uint8_t *xr = G.bq + (size_t)tok * KG;
 #pragma unroll
         for (int u = 0; u < 8; u++) xv[u] = *reinterpret_cast<const u32x4 *>(xr + (xr_c + 16 * u) * 16);
@@ -1769,16 +1790,14 @@ __device__ __forceinline__ void skinny_expert(const GemmArgs &G, const GemmArgs 
     u32x4 sb[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
-        const int tok = G.row_tok[p0 + min(16 * j + n, nr - 1)];
+        const int tok = L.tok[16 * j + n];
         sb[j] = *reinterpret_cast<const u32x4 *>(G.bs2 + (size_t)tok * (KG / 32) + q * 16);
     }
-    const float wrow = G.row_w[p0 + min(tid & (kSkTok - 1), nr - 1)];
     __builtin_amdgcn_sched_barrier(0);
     load(std::integral_constant<int, 1>{}, bs[1]);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int u = 0; u < 8; u++) *reinterpret_cast<u32x4 *>(&L.x[sx_off(xr_r, xr_c + 16 * u)]) = xv[u];
-    if (tid < kSkTok) L.ws[tid] = wrow;
     lds_barrier();
 
     v4f acc[4][NJ];
@@ -1945,13 +1964,111 @@ __device__ __forceinline__ void skinny_expert(const GemmArgs &G, const GemmArgs 
     });
 }
 
-__global__ __launch_bounds__(64 * kSxW) void k_skinny_expert(GemmArgs G, GemmArgs Dn) {
+// Finds this workgroup's tile (expert e, sorted rows p0..p1) from the top-k
+// indices and fills L.tok / L.ws with its rows; false past the last tile.
+__device__ bool sx_discover(const SxArgs &X, SxLds &L, int ti, int &e_out, int &p0_out, int &p1_out) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n = X.T * X.k, E = X.E;
+    for (int e = tid; e < E; e += 64 * kSxW) L.cnt[e] = 0;
+    int ev[4];
+    float wv[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int i = tid + 64 * kSxW * u;
+        ev[u] = i < n ? X.idx[i] : -1;
+        wv[u] = i < n ? X.wt[i] : 0.0f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+        if (ev[u] >= 0) atomicAdd(&L.cnt[ev[u]], 1);
+    __syncthreads();
+    for (int e = tid; e < E; e += 64 * kSxW) L.ntl[e] = (L.cnt[e] + kSkTok - 1) / kSkTok;
+    __syncthreads();
+    if (wave == 0) wave_scan256(L.cnt, E, L.off, &L.off[E]);
+    else if (wave == 1) wave_scan256(L.ntl, E, L.toff, &L.toff[E]);
+    __syncthreads();
+    const int nrt = L.toff[E];
+    const int nsh = X.shg ? (X.T + kSkTok - 1) / kSkTok : 0;
+    if (ti >= nrt + nsh) return false;
+    if (ti == 0)
+        for (int e = tid; e <= E; e += 64 * kSxW) X.e_off[e] = L.off[e];
+    int e, p0, p1;
+    if (ti < nrt) {
+        for (int ee = tid; ee < E; ee += 64 * kSxW)
+            if (L.ntl[ee] > 0 && ti >= L.toff[ee] && ti < L.toff[ee] + L.ntl[ee]) L.sel = ee;
+        __syncthreads();
+        e = __builtin_amdgcn_readfirstlane(L.sel);
+        const int rank0 = (ti - L.toff[e]) * kSkTok;
+        p0 = L.off[e] + rank0;
+        p1 = min(p0 + kSkTok, L.off[e] + L.cnt[e]);
+        // ranks of the expert's entries in entry order, 512 entries a round
+        int base = 0;
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            if (64 * kSxW * u >= n) break;   // uniform
+            const bool f = ev[u] == e;
+            const uint64_t m = __ballot(f);
+            if (lane == 0) L.wsum[wave] = __popcll(m);
+            __syncthreads();
+            int pre = 0, tot = 0;
+#pragma unroll
+            for (int w = 0; w < kSxW; w++) {
+                pre += w < wave ? L.wsum[w] : 0;
+                tot += L.wsum[w];
+            }
+            const int rank = base + pre +
+                             (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+            if (f && rank >= rank0 && rank < rank0 + (p1 - p0)) {
+                const int r = rank - rank0, i = tid + 64 * kSxW * u;
+                L.tok[r] = i / X.k;
+                L.ws[r] = wv[u];
+                X.pos[i] = p0 + r;
+                X.perm[p0 + r] = i;
+            }
+            base += tot;
+            __syncthreads();   // wsum is rewritten next round
+        }
+    } else {   // shared-expert rows: token order
+        e = E;
+        const int r0 = (ti - nrt) * kSkTok;
+        p0 = n + r0;
+        p1 = min(n + X.T, p0 + kSkTok);
+        if (tid < p1 - p0) {
+            const int t = r0 + tid;
+            L.tok[tid] = t;
+            L.ws[tid] = 1.0f / (1.0f + expf(-X.shg[(size_t)t * X.ld_shg]));
+        }
+        __syncthreads();
+    }
+    const int nr = p1 - p0;
+    if (tid >= nr && tid < kSkTok) L.tok[tid] = L.tok[nr - 1];
+    __syncthreads();
+    e_out = e;
+    p0_out = __builtin_amdgcn_readfirstlane(p0);
+    p1_out = __builtin_amdgcn_readfirstlane(p1);
+    return true;
+}
+
+__global__ __launch_bounds__(64 * kSxW) void k_skinny_expert(GemmArgs G, GemmArgs Dn, SxArgs X) {
     __shared__ SxLds L;
     const int ti = blockIdx.x;
-    if (ti >= *G.ntiles) return;
-    const int4 tile = G.tiles[ti];
-    const int e = __builtin_amdgcn_readfirstlane(tile.x);
-    const int p0 = __builtin_amdgcn_readfirstlane(tile.y), p1 = __builtin_amdgcn_readfirstlane(tile.z);
+    int e, p0, p1;
+    if (X.discover) {
+        if (!sx_discover(X, L, ti, e, p0, p1)) return;
+    } else {
+        if (ti >= *G.ntiles) return;
+        const int4 tile = G.tiles[ti];
+        e = __builtin_amdgcn_readfirstlane(tile.x);
+        p0 = __builtin_amdgcn_readfirstlane(tile.y);
+        p1 = __builtin_amdgcn_readfirstlane(tile.z);
+        if (threadIdx.x < kSkTok) {
+            const int r = min((int)threadIdx.x, p1 - p0 - 1);
+            L.tok[threadIdx.x] = G.row_tok[p0 + r];
+            L.ws[threadIdx.x] = G.row_w[p0 + r];
+        }
+        __syncthreads();
+    }
     if (p1 - p0 <= 16) skinny_expert<1, kSxRT>(G, Dn, e, p0, p1, L);
     else skinny_expert<2, kSxRT>(G, Dn, e, p0, p1, L);
 }
@@ -2468,6 +2585,7 @@ struct Plan {
     RouteArgs ra;
     ScanArgs sa;
     GemmArgs ga, da;
+    SxArgs sx;
     DirectArgs di;
     const void *out; int out_fmt;
 };
@@ -2894,13 +3012,14 @@ static void launch_stage(const Scratch &c, const Plan &P, int st, hipStream_t s)
                 hipLaunchKernelGGL(k_route<kRouteTPBSmall>, dim3(P.nb), dim3(64 * kRouteTPBSmall), 0, s, P.ra);
             break;
         case ST_SCAN:
+            if (P.fused && P.sx.discover) break;   // k_skinny_expert finds its own tile
             if (!P.sa.inline_cols)
                 hipLaunchKernelGGL(k_colscan, dim3((c.E + kColExp - 1) / kColExp), dim3(256), 0, s, P.sa);
             hipLaunchKernelGGL(k_scatter, dim3(P.nb), dim3(256), 0, s, P.sa);
             break;
         case ST_GATEUP:
             if (P.fused) {
-                hipLaunchKernelGGL(k_skinny_expert, dim3(P.tiles), dim3(64 * kSxW), 0, s, P.ga, P.da);
+                hipLaunchKernelGGL(k_skinny_expert, dim3(P.tiles), dim3(64 * kSxW), 0, s, P.ga, P.da, P.sx);
             } else if (P.skinny) {
                 hipLaunchKernelGGL(k_skinny_gateup, dim3(P.tiles * 16), dim3(64 * kSkW), 0, s, P.ga);
                 if (P.ga.shq8)
@@ -3017,6 +3136,8 @@ static int launch_forward(const Scratch &c, Plan &P, int pm, const q36moe_weight
         da.M = D;
         da.bq = c.hq; da.bs2 = c.hs2; da.dnh = c.dnh; da.dne = c.dne; da.ldo = D;
         da.bsf = c.hsf;
+        P.sx = SxArgs{c.topk_idx, c.topk_w, shg, ld_shg, c.perm, c.pos, c.e_off, T, K, E,
+                      fused && n <= kSxDiscoverMax ? 1 : 0};
     }
     bind_weights(P, w);
     if (!direct && shq8) {   // k_route also writes the int8 x the shared expert reads
