@@ -410,9 +410,11 @@ def test_forward_decode1(dev, oracle, layer_w, path):
 # Batch sizes between the named configurations, each on a forced path (0 =
 # the automatic choice), with Zipf routing on every other case and the
 # shared expert on some: (T, path, zipf, shared).
+# Path 5 at T=256 has exactly the most routed entries (2048) the one-kernel
+# skinny path discovers its tiles for; at T=300 it takes them from k_scatter.
 SWEEP = [(3, 2, False, True), (9, 4, True, False), (17, 0, False, False), (31, 1, True, True),
-         (48, 5, True, True), (100, 4, False, True), (200, 5, False, False), (257, 0, True, False),
-         (1000, 1, False, False), (2049, 0, True, True)]
+         (48, 5, True, True), (100, 4, False, True), (200, 5, False, False), (256, 5, True, True),
+         (257, 0, True, False), (300, 5, False, True), (1000, 1, False, False), (2049, 0, True, True)]
 
 
 @pytest.mark.parametrize("T,path,zipf,shared", SWEEP, ids=[f"T{c[0]}_p{c[1]}" for c in SWEEP])
