@@ -645,6 +645,48 @@ def test_add_rmsnorm_quant(dev, oracle, T, with_a):
     np.testing.assert_array_equal(xs.cpu().numpy(), os_)
 
 
+@pytest.fixture(scope="module")
+def layer_w64():
+    w = synth.expert_weights(2031, n_expert=64, shared=True)
+    dw = moe.MoEWeights.upload(w["gate"], w["up"], w["down"], w["sh_gate"], w["sh_up"], w["sh_down"])
+    return w, dw
+
+
+@pytest.mark.parametrize("T", [5, 24, 40])
+def test_forward_64_experts_top4(dev, oracle, layer_w64, T):
+    """A layer of 64 experts with top-4 routing (the library takes any
+    n_expert <= 256 and top_k <= 8) on every path that serves T: routing,
+    sort and output against the oracle.  The output bar is the 1e-2
+    backstop (h midpoint flips move a token by up to ~2e-3 of its row max);
+    the 2e-3 bars are held on the 256-expert layers above."""
+    w, dw = layer_w64
+    E, k = 64, 4
+    rng = np.random.default_rng(1300 + T)
+    x = synth.hidden(rng, T)
+    lg = synth.normal_logits(rng, T, n_expert=E)
+    shg = rng.standard_normal(T).astype(np.float32)
+    ref = oracle.moe_forward(w, x, lg, shg, k=k)
+    oi, _ = oracle.router_topk(lg, k, n_expert=E)
+    off, perm, pos = oracle.sort_entries(oi, E)
+    paths = [0, 1, 4, 5] + ([2] if T <= 16 else [])
+    seen = set()
+    for path in paths:
+        layer = moe.MoELayer(T, n_expert=E, top_k=k)
+        layer.set_path(path)
+        y = layer.forward(dw, torch.from_numpy(x).to(dev), torch.from_numpy(lg).to(dev),
+                          torch.from_numpy(shg).to(dev), out_dtype=torch.float32)
+        layer.check()
+        seen.add(layer.last_path)
+        np.testing.assert_array_equal(layer.tap(moe.TAP_TOPK_IDX).cpu().numpy(), oi)
+        if layer.last_path != 1:
+            np.testing.assert_array_equal(layer.tap(moe.TAP_EOFF).cpu().numpy(), off)
+            np.testing.assert_array_equal(layer.tap(moe.TAP_PERM).cpu().numpy(), perm)
+            np.testing.assert_array_equal(layer.tap(moe.TAP_POS).cpu().numpy(), pos)
+        _, normwise = _row_err(y.cpu().numpy().astype(np.float64), ref)
+        assert normwise <= 1e-2, f"path {path} (ran {layer.last_path}): {normwise:.3g}"
+    assert 3 in seen and 2 in seen and 0 in seen
+
+
 @pytest.mark.parametrize("T,path", [(1, 0), (5, 2), (40, 4), (40, 5), (40, 1), (600, 0)])
 def test_forward_q8_equals_forward(dev, layer_w, T, path):
     """The pre-quantised entry gives bit-identical results (outputs and
