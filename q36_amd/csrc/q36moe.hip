@@ -1699,12 +1699,14 @@ struct SxLds {
 // k_scatter, so perm / pos / e_off come out identical.  At most
 // kSxDiscoverMax routed entries (4 per thread).
 constexpr int kSxDiscoverMax = 4 * 64 * kSxW;
+constexpr int kSxTok = 16;   // rows per discovered tile
 struct SxArgs {
     const int32_t *idx; const float *wt;   // top-k routing of each entry
     const float *shg; int ld_shg;          // shared-gate logits (shared tiles), or null
     int32_t *perm, *pos, *e_off;           // sorted order out (taps; pos feeds the combine)
     int T, k, E;
     int discover;                          // 0: tiles from k_scatter
+    int tn;                                // rows per discovered tile (<= kSkTok)
 };
 
 __device__ __forceinline__ int sx_off(int r, int c) { return r * 2048 + ((c & ~15) | ((c ^ r) & 15)) * 16; }
@@ -1983,13 +1985,14 @@ __device__ bool sx_discover(const SxArgs &X, SxLds &L, int ti, int &e_out, int &
     for (int u = 0; u < 4; u++)
         if (ev[u] >= 0) atomicAdd(&L.cnt[ev[u]], 1);
     __syncthreads();
-    for (int e = tid; e < E; e += 64 * kSxW) L.ntl[e] = (L.cnt[e] + kSkTok - 1) / kSkTok;
+    const int tn = X.tn;
+    for (int e = tid; e < E; e += 64 * kSxW) L.ntl[e] = (L.cnt[e] + tn - 1) / tn;
     __syncthreads();
     if (wave == 0) wave_scan256(L.cnt, E, L.off, &L.off[E]);
     else if (wave == 1) wave_scan256(L.ntl, E, L.toff, &L.toff[E]);
     __syncthreads();
     const int nrt = L.toff[E];
-    const int nsh = X.shg ? (X.T + kSkTok - 1) / kSkTok : 0;
+    const int nsh = X.shg ? (X.T + tn - 1) / tn : 0;
     if (ti >= nrt + nsh) return false;
     if (ti == 0)
         for (int e = tid; e <= E; e += 64 * kSxW) X.e_off[e] = L.off[e];
@@ -1999,9 +2002,9 @@ __device__ bool sx_discover(const SxArgs &X, SxLds &L, int ti, int &e_out, int &
             if (L.ntl[ee] > 0 && ti >= L.toff[ee] && ti < L.toff[ee] + L.ntl[ee]) L.sel = ee;
         __syncthreads();
         e = __builtin_amdgcn_readfirstlane(L.sel);
-        const int rank0 = (ti - L.toff[e]) * kSkTok;
+        const int rank0 = (ti - L.toff[e]) * tn;
         p0 = L.off[e] + rank0;
-        p1 = min(p0 + kSkTok, L.off[e] + L.cnt[e]);
+        p1 = min(p0 + tn, L.off[e] + L.cnt[e]);
         // ranks of the expert's entries in entry order, 512 entries a round
         int base = 0;
 #pragma unroll
@@ -2031,9 +2034,9 @@ __device__ bool sx_discover(const SxArgs &X, SxLds &L, int ti, int &e_out, int &
         }
     } else {   // shared-expert rows: token order
         e = E;
-        const int r0 = (ti - nrt) * kSkTok;
+        const int r0 = (ti - nrt) * tn;
         p0 = n + r0;
-        p1 = min(n + X.T, p0 + kSkTok);
+        p1 = min(n + X.T, p0 + tn);
         if (tid < p1 - p0) {
             const int t = r0 + tid;
             L.tok[tid] = t;
@@ -3137,7 +3140,11 @@ static int launch_forward(const Scratch &c, Plan &P, int pm, const q36moe_weight
         da.bq = c.hq; da.bs2 = c.hs2; da.dnh = c.dnh; da.dne = c.dne; da.ldo = D;
         da.bsf = c.hsf;
         P.sx = SxArgs{c.topk_idx, c.topk_w, shg, ld_shg, c.perm, c.pos, c.e_off, T, K, E,
-                      fused && n <= kSxDiscoverMax ? 1 : 0};
+                      fused && n <= kSxDiscoverMax ? 1 : 0, kSxTok};
+        if (P.sx.discover) {   // grid for tiles of kSxTok rows
+            int t = n / kSxTok + (n < E ? n : E) + (has_sh ? (T + kSxTok - 1) / kSxTok : 0);
+            P.tiles = (t + 7) & ~7;
+        }
     }
     bind_weights(P, w);
     if (!direct && shq8) {   // k_route also writes the int8 x the shared expert reads
