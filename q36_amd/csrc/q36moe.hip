@@ -1654,7 +1654,8 @@ __global__ __launch_bounds__(64 * kDlW, Q8 ? 2 : 1) void k_down_lds(GemmArgs A) 
 // ---------------------------------------------------------------------------
 // skinny tiles: the whole expert in one workgroup
 // ---------------------------------------------------------------------------
-// Workgroup = one skinny tile (expert e, sorted rows p0..p1, at most 32):
+// Workgroup = one skinny tile (expert e, sorted rows p0..p1: at most 16 when
+// the kernel finds its tiles itself, 32 from k_scatter):
 // gate/up over all 512 rows of gate and up, SwiGLU and the e4m3
 // quantisation of h into LDS, then the down projection over all 2048 output
 // rows, staged weighted exactly as k_down_lds stages them.  h makes no round
