@@ -1712,9 +1712,9 @@ struct SxArgs {
 
 __device__ __forceinline__ int sx_off(int r, int c) { return r * 2048 + ((c & ~15) | ((c ^ r) & 15)) * 16; }
 
-template <int NJ, int RT>
+template <int NJ, int RT, class Prep>
 __device__ __forceinline__ void skinny_expert(const GemmArgs &G, const GemmArgs &Dn, int e, int p0, int p1,
-                                              SxLds &L) {
+                                              SxLds &L, Prep &&prep) {
     // RT row tiles per gate/up step, 8 / RT consecutive K-steps of each
     static_assert(RT == 1 || RT == 2 || RT == 4, "row tiles per step");
     constexpr int RD = RT == 4 ? 4 : 2;   // down row tiles per step (K = 4 K-steps)
@@ -1776,11 +1776,13 @@ __device__ __forceinline__ void skinny_expert(const GemmArgs &G, const GemmArgs 
         }
     };
     // Prologue, in this order (sched barriers keep it): weight step 0; the
-    // x rows of the tile (L.tok: rows past the tile repeat its last row,
-    // never stored) and their B scales; weight step 1.  Waiting for the x
+    // tile's rows (prep); the x rows of the tile (L.tok: rows past the tile
+    // repeat its last row, never stored) and their B scales; weight step 1.  Waiting for the x
     // rows (loads complete in order) then leaves step 1 in flight.
     Step bs[3];   // three step buffers, loads two steps ahead of the MFMAs
     load(std::integral_constant<int, 0>{}, bs[0]);
+    __builtin_amdgcn_sched_barrier(0);
+    prep();   // the tile's rows into L.tok / L.ws, while step 0 is in flight
     __builtin_amdgcn_sched_barrier(0);
     const int xr_r = tid >> 4, xr_c = tid & 15;
     u32x4 xv[8];
@@ -1968,13 +1970,13 @@ __device__ __forceinline__ void skinny_expert(const GemmArgs &G, const GemmArgs 
 }
 
 // Finds this workgroup's tile (expert e, sorted rows p0..p1) from the top-k
-// indices and fills L.tok / L.ws with its rows; false past the last tile.
-__device__ bool sx_discover(const SxArgs &X, SxLds &L, int ti, int &e_out, int &p0_out, int &p1_out) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+// indices; false past the last tile.  ev / wv keep this thread's entries
+// for sx_gather.
+__device__ bool sx_find(const SxArgs &X, SxLds &L, int ti, int &e_out, int &p0_out, int &p1_out, int (&ev)[4],
+                        float (&wv)[4]) {
+    const int tid = threadIdx.x, wave = tid >> 6;
     const int n = X.T * X.k, E = X.E;
     for (int e = tid; e < E; e += 64 * kSxW) L.cnt[e] = 0;
-    int ev[4];
-    float wv[4];
 #pragma unroll
     for (int u = 0; u < 4; u++) {
         const int i = tid + 64 * kSxW * u;
@@ -2003,9 +2005,28 @@ __device__ bool sx_discover(const SxArgs &X, SxLds &L, int ti, int &e_out, int &
             if (L.ntl[ee] > 0 && ti >= L.toff[ee] && ti < L.toff[ee] + L.ntl[ee]) L.sel = ee;
         __syncthreads();
         e = __builtin_amdgcn_readfirstlane(L.sel);
-        const int rank0 = (ti - L.toff[e]) * tn;
-        p0 = L.off[e] + rank0;
+        p0 = L.off[e] + (ti - L.toff[e]) * tn;
         p1 = min(p0 + tn, L.off[e] + L.cnt[e]);
+    } else {   // shared-expert rows
+        e = E;
+        p0 = n + (ti - nrt) * tn;
+        p1 = min(n + X.T, p0 + tn);
+    }
+    e_out = e;
+    p0_out = __builtin_amdgcn_readfirstlane(p0);
+    p1_out = __builtin_amdgcn_readfirstlane(p1);
+    return true;
+}
+
+// Fills L.tok / L.ws with the rows of the tile sx_find found and writes
+// their pos / perm.  It runs while the first weight step is in flight, so
+// its barriers wait on LDS only.
+__device__ void sx_gather(const SxArgs &X, SxLds &L, int e, int p0, int p1, const int (&ev)[4],
+                          const float (&wv)[4]) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n = X.T * X.k;
+    if (e < X.E) {
+        const int rank0 = p0 - L.off[e];
         // ranks of the expert's entries in entry order, 512 entries a round
         int base = 0;
 #pragma unroll
@@ -2014,7 +2035,7 @@ __device__ bool sx_discover(const SxArgs &X, SxLds &L, int ti, int &e_out, int &
             const bool f = ev[u] == e;
             const uint64_t m = __ballot(f);
             if (lane == 0) L.wsum[wave] = __popcll(m);
-            __syncthreads();
+            lds_barrier();
             int pre = 0, tot = 0;
 #pragma unroll
             for (int w = 0; w < kSxW; w++) {
@@ -2031,27 +2052,20 @@ __device__ bool sx_discover(const SxArgs &X, SxLds &L, int ti, int &e_out, int &
                 X.perm[p0 + r] = i;
             }
             base += tot;
-            __syncthreads();   // wsum is rewritten next round
+            lds_barrier();   // wsum is rewritten next round
         }
     } else {   // shared-expert rows: token order
-        e = E;
-        const int r0 = (ti - nrt) * tn;
-        p0 = n + r0;
-        p1 = min(n + X.T, p0 + tn);
+        const int r0 = p0 - n;
         if (tid < p1 - p0) {
             const int t = r0 + tid;
             L.tok[tid] = t;
             L.ws[tid] = 1.0f / (1.0f + expf(-X.shg[(size_t)t * X.ld_shg]));
         }
-        __syncthreads();
+        lds_barrier();
     }
     const int nr = p1 - p0;
     if (tid >= nr && tid < kSkTok) L.tok[tid] = L.tok[nr - 1];
-    __syncthreads();
-    e_out = e;
-    p0_out = __builtin_amdgcn_readfirstlane(p0);
-    p1_out = __builtin_amdgcn_readfirstlane(p1);
-    return true;
+    lds_barrier();
 }
 
 __global__ __launch_bounds__(64 * kSxW) void k_skinny_expert(GemmArgs G, GemmArgs Dn, SxArgs X) {
@@ -2059,22 +2073,29 @@ __global__ __launch_bounds__(64 * kSxW) void k_skinny_expert(GemmArgs G, GemmArg
     const int ti = blockIdx.x;
     int e, p0, p1;
     if (X.discover) {
-        if (!sx_discover(X, L, ti, e, p0, p1)) return;
+        int ev[4];
+        float wv[4];
+        if (!sx_find(X, L, ti, e, p0, p1, ev, wv)) return;
+        auto prep = [&]() { sx_gather(X, L, e, p0, p1, ev, wv); };
+        if (p1 - p0 <= 16) skinny_expert<1, kSxRT>(G, Dn, e, p0, p1, L, prep);
+        else skinny_expert<2, kSxRT>(G, Dn, e, p0, p1, L, prep);
     } else {
         if (ti >= *G.ntiles) return;
         const int4 tile = G.tiles[ti];
         e = __builtin_amdgcn_readfirstlane(tile.x);
         p0 = __builtin_amdgcn_readfirstlane(tile.y);
         p1 = __builtin_amdgcn_readfirstlane(tile.z);
-        if (threadIdx.x < kSkTok) {
-            const int r = min((int)threadIdx.x, p1 - p0 - 1);
-            L.tok[threadIdx.x] = G.row_tok[p0 + r];
-            L.ws[threadIdx.x] = G.row_w[p0 + r];
-        }
-        __syncthreads();
+        auto prep = [&]() {
+            if (threadIdx.x < kSkTok) {
+                const int r = min((int)threadIdx.x, p1 - p0 - 1);
+                L.tok[threadIdx.x] = G.row_tok[p0 + r];
+                L.ws[threadIdx.x] = G.row_w[p0 + r];
+            }
+            __syncthreads();
+        };
+        if (p1 - p0 <= 16) skinny_expert<1, kSxRT>(G, Dn, e, p0, p1, L, prep);
+        else skinny_expert<2, kSxRT>(G, Dn, e, p0, p1, L, prep);
     }
-    if (p1 - p0 <= 16) skinny_expert<1, kSxRT>(G, Dn, e, p0, p1, L);
-    else skinny_expert<2, kSxRT>(G, Dn, e, p0, p1, L);
 }
 
 // ---------------------------------------------------------------------------
