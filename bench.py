@@ -78,6 +78,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--path", type=int, default=0, help="q36moe_ctx_set_path mode (0 auto)")
+    ap.add_argument("--tokens", type=int, default=None,
+                    help="override the configuration's token count (path threshold measurements)")
     ap.add_argument("--graph", type=int, default=1,
                     help="1: time the K steps as one HIP graph (how a model's layer loop runs "
                          "when captured); 0: eager launches only")
@@ -382,6 +384,11 @@ def main():
         copy_reference(args.copy_mib)
         return
 
+    if args.tokens is not None:
+        if args.tokens < 1:
+            print(json.dumps({"error": "--tokens must be >= 1"}))
+            sys.exit(2)
+        CONFIGS[args.config] = dict(CONFIGS[args.config], T=args.tokens)
     cfg = CONFIGS[args.config]
     T, shared = cfg["T"], cfg["shared"]
     steps = args.steps if args.steps is not None else cfg["steps"]

@@ -1287,6 +1287,7 @@ __global__ __launch_bounds__(256) void k_add_rmsnorm_quant(float *__restrict__ h
 // projection of skinny tiles runs in k_down_lds, as for fat tiles.
 constexpr int kSkTok = 32;     // rows per skinny tile (two 16-row column tiles)
 constexpr int kSkinnyRows = 8; // auto mode: skinny while T*k <= kSkinnyRows * n_expert
+constexpr int kSxFusedRows = 16; // ... and to kSxFusedRows * n_expert on the one-kernel skinny path
 constexpr int kSkW = 8;        // waves per workgroup
 
 template <int NJ>
@@ -1707,9 +1708,10 @@ struct SxLds {
 // scans the counts into offsets and 32-row tiles, finds its own tile and
 // gathers that tile's entries in entry order -- the stable sorted order of
 // k_scatter, so perm / pos / e_off come out identical.  At most
-// kSxDiscoverMax routed entries (4 per thread).
-constexpr int kSxDiscoverMax = 4 * 64 * kSxW;
-constexpr int kSxTok = 16;   // rows per discovered tile
+// kSxDiscoverMax routed entries (kSxEnt per thread).
+constexpr int kSxEnt = 8;
+constexpr int kSxDiscoverMax = kSxEnt * 64 * kSxW;
+constexpr int kSxTok = 16;   // rows per discovered tile while T*k <= kSkinnyRows * E; 32 above
 struct SxArgs {
     const int32_t *idx; const float *wt;   // top-k routing of each entry
     const float *shg; int ld_shg;          // shared-gate logits (shared tiles), or null
@@ -1981,20 +1983,20 @@ __device__ __forceinline__ void skinny_expert(const GemmArgs &G, const GemmArgs 
 // Finds this workgroup's tile (expert e, sorted rows p0..p1) from the top-k
 // indices; false past the last tile.  ev / wv keep this thread's entries
 // for sx_gather.
-__device__ bool sx_find(const SxArgs &X, SxLds &L, int ti, int &e_out, int &p0_out, int &p1_out, int (&ev)[4],
-                        float (&wv)[4]) {
+__device__ bool sx_find(const SxArgs &X, SxLds &L, int ti, int &e_out, int &p0_out, int &p1_out, int (&ev)[kSxEnt],
+                        float (&wv)[kSxEnt]) {
     const int tid = threadIdx.x, wave = tid >> 6;
     const int n = X.T * X.k, E = X.E;
     for (int e = tid; e < E; e += 64 * kSxW) L.cnt[e] = 0;
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
+    for (int u = 0; u < kSxEnt; u++) {
         const int i = tid + 64 * kSxW * u;
         ev[u] = i < n ? X.idx[i] : -1;
         wv[u] = i < n ? X.wt[i] : 0.0f;
     }
     __syncthreads();
 #pragma unroll
-    for (int u = 0; u < 4; u++)
+    for (int u = 0; u < kSxEnt; u++)
         if (ev[u] >= 0) atomicAdd(&L.cnt[ev[u]], 1);
     __syncthreads();
     const int tn = X.tn;
@@ -2030,8 +2032,8 @@ __device__ bool sx_find(const SxArgs &X, SxLds &L, int ti, int &e_out, int &p0_o
 // Fills L.tok / L.ws with the rows of the tile sx_find found and writes
 // their pos / perm.  It runs while the first weight step is in flight, so
 // its barriers wait on LDS only.
-__device__ void sx_gather(const SxArgs &X, SxLds &L, int e, int p0, int p1, const int (&ev)[4],
-                          const float (&wv)[4]) {
+__device__ void sx_gather(const SxArgs &X, SxLds &L, int e, int p0, int p1, const int (&ev)[kSxEnt],
+                          const float (&wv)[kSxEnt]) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = X.T * X.k;
     if (e < X.E) {
@@ -2039,7 +2041,7 @@ __device__ void sx_gather(const SxArgs &X, SxLds &L, int e, int p0, int p1, cons
         // ranks of the expert's entries in entry order, 512 entries a round
         int base = 0;
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
+        for (int u = 0; u < kSxEnt; u++) {
             if (64 * kSxW * u >= n) break;   // uniform
             const bool f = ev[u] == e;
             const uint64_t m = __ballot(f);
@@ -2082,8 +2084,8 @@ __global__ __launch_bounds__(64 * kSxW) void k_skinny_expert(GemmArgs G, GemmArg
     const int ti = blockIdx.x;
     int e, p0, p1;
     if (X.discover) {
-        int ev[4];
-        float wv[4];
+        int ev[kSxEnt];
+        float wv[kSxEnt];
         if (!sx_find(X, L, ti, e, p0, p1, ev, wv)) return;
         auto prep = [&]() { sx_gather(X, L, e, p0, p1, ev, wv); };
         // an expert with one tile streams its weights once (non-temporal);
@@ -3138,10 +3140,14 @@ static int launch_forward(const Scratch &c, Plan &P, int pm, const q36moe_weight
     if (shq8 && x_fmt == kFmtE4M3) return Q36MOE_EINVAL;
     // sorted path: skinny tiles (<= 32 rows) while the average expert has at
     // most kSkinnyRows rows, else fat tiles of up to kGdTok rows
-    const bool skinny = pm == 4 || pm == 5 || (pm == 0 && (size_t)n <= (size_t)kSkinnyRows * E);
+    // the one-kernel skinny path (every matrix MXFP4) serves twice the rows
+    // per expert: it beat fat tiles up to 512 tokens (T=384: 96 vs 103 us)
+    const bool fusable = !w->dn_q8 && !shq8;
+    const size_t skinny_rows = (size_t)(fusable ? kSxFusedRows : kSkinnyRows) * E;
+    const bool skinny = pm == 4 || pm == 5 || (pm == 0 && (size_t)n <= skinny_rows);
     // skinny tiles in one kernel per tile (k_skinny_expert) when every
     // matrix is MXFP4; the int8 down or shared expert keeps two kernels
-    const bool fused = skinny && pm != 4 && !w->dn_q8 && !shq8;
+    const bool fused = skinny && pm != 4 && fusable;
     const int tn = skinny ? kSkTok : kGdTok;
     // a q8_0-split shared expert's down is VALU-heavy: its rows go in small
     // tiles so the work spreads over many workgroups instead of trailing
@@ -3178,10 +3184,14 @@ static int launch_forward(const Scratch &c, Plan &P, int pm, const q36moe_weight
         da.M = D;
         da.bq = c.hq; da.bs2 = c.hs2; da.dnh = c.dnh; da.dne = c.dne; da.ldo = D;
         da.bsf = c.hsf;
+        // discovered tiles: 16 rows while the average expert has at most
+        // kSkinnyRows, else 32 (a second column tile, not a second stream of
+        // the same weights)
+        const int stn = (size_t)n <= (size_t)kSkinnyRows * E ? kSxTok : kSkTok;
         P.sx = SxArgs{c.topk_idx, c.topk_w, shg, ld_shg, c.perm, c.pos, c.e_off, T, K, E,
-                      fused && n <= kSxDiscoverMax ? 1 : 0, kSxTok};
-        if (P.sx.discover) {   // grid for tiles of kSxTok rows
-            int t = n / kSxTok + (n < E ? n : E) + (has_sh ? (T + kSxTok - 1) / kSxTok : 0);
+                      fused && n <= kSxDiscoverMax ? 1 : 0, stn};
+        if (P.sx.discover) {   // grid for tiles of stn rows
+            int t = n / stn + (n < E ? n : E) + (has_sh ? (T + stn - 1) / stn : 0);
             P.tiles = (t + 7) & ~7;
         }
     }
