@@ -1711,7 +1711,7 @@ struct SxLds {
 // kSxDiscoverMax routed entries (kSxEnt per thread).
 constexpr int kSxEnt = 8;
 constexpr int kSxDiscoverMax = kSxEnt * 64 * kSxW;
-constexpr int kSxTok = 16;   // rows per discovered tile while T*k <= kSkinnyRows * E; 32 above
+constexpr int kSxTok = 16;   // rows per discovered tile while T*k <= 4 * E; kSkTok above
 struct SxArgs {
     const int32_t *idx; const float *wt;   // top-k routing of each entry
     const float *shg; int ld_shg;          // shared-gate logits (shared tiles), or null
@@ -3184,10 +3184,11 @@ static int launch_forward(const Scratch &c, Plan &P, int pm, const q36moe_weight
         da.M = D;
         da.bq = c.hq; da.bs2 = c.hs2; da.dnh = c.dnh; da.dne = c.dne; da.ldo = D;
         da.bsf = c.hsf;
-        // discovered tiles: 16 rows while the average expert has at most
-        // kSkinnyRows, else 32 (a second column tile, not a second stream of
-        // the same weights)
-        const int stn = (size_t)n <= (size_t)kSkinnyRows * E ? kSxTok : kSkTok;
+        // discovered tiles: 16 rows while the average expert has at most 4
+        // (T <= 128 at 256 experts, top-8), else 32: a second column tile
+        // rather than a second stream of the same weights, and no more tiles
+        // than CUs (T=256: 100.5 -> 85.5 us)
+        const int stn = (size_t)n <= (size_t)4 * E ? kSxTok : kSkTok;
         P.sx = SxArgs{c.topk_idx, c.topk_w, shg, ld_shg, c.perm, c.pos, c.e_off, T, K, E,
                       fused && n <= kSxDiscoverMax ? 1 : 0, stn};
         if (P.sx.discover) {   // grid for tiles of stn rows
