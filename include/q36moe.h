@@ -242,7 +242,8 @@ int q36moe_forward_q8(q36moe_ctx *c, const q36moe_weights *w, const uint8_t *xq,
  * in LDS, down) or as separate gate/up and down kernels; the one-kernel
  * form needs MXFP4 down and shared-expert matrices.  mode 0 picks the
  * direct path for T <= 16, skinny tiles (one kernel per tile where it
- * applies) while T*k <= 8*n_expert and fat tiles above; 1 forces sorted with
+ * applies) while T*k <= 8*n_expert (16*n_expert when the one-kernel form
+ * applies) and fat tiles above; 1 forces sorted with
  * fat tiles, 4 sorted with skinny tiles as two kernels, 5 sorted with
  * skinny tiles in one kernel per tile (two kernels for an int8 down or
  * shared expert), 2 direct (EINVAL from forward when T > 16).  Mode 3 (a

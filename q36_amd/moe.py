@@ -378,7 +378,8 @@ class MoELayer:
     PATH_AUTO, PATH_SORTED, PATH_DIRECT, PATH_SORTED_SKINNY, PATH_SORTED_FUSED = 0, 1, 2, 4, 5
 
     def set_path(self, mode):
-        """0 auto (direct for T <= 16, skinny tiles while T*k <= 8*n_expert),
+        """0 auto (direct for T <= 16, skinny tiles while T*k <= 8*n_expert --
+        16*n_expert in one kernel per tile for MXFP4 layers),
         1 sorted (fat tiles), 2 direct, 4 sorted (skinny tiles, gate/up and
         down as two kernels), 5 sorted (skinny tiles, one kernel per tile;
         layers with an int8 down or shared expert take 4); 3 is refused
