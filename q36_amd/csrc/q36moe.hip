@@ -460,6 +460,7 @@ struct RouteArgs {
     int32_t *blk_cnt; int32_t *rank;
     const uint8_t *xs_in;     // scales of pre-quantised x (x_fmt kFmtE4M3)
     int8_t *xq8; float *xsf;  // int8 x + fp32 scales per 32 for a q8_0-split shared expert, or null
+    int counts;               // write blk_cnt / rank (0: the one-kernel skinny path sorts itself)
 };
 
 // One wavefront per token, TPB tokens per workgroup: top-k routing,
@@ -478,8 +479,10 @@ __global__ __launch_bounds__(64 * TPB) void k_route(RouteArgs A) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int t0 = blockIdx.x * TPB;
     const int nb32 = A.D / 32;
-    for (int e = threadIdx.x; e < A.E; e += 64 * TPB) tmask[e] = 0u;
-    __syncthreads();
+    if (A.counts) {   // uniform
+        for (int e = threadIdx.x; e < A.E; e += 64 * TPB) tmask[e] = 0u;
+        __syncthreads();
+    }
     const int t = t0 + wave;
     if (t < A.T) {
         // x of the token (kRouteD values, 8 per lane per pass) is loaded
@@ -494,8 +497,10 @@ __global__ __launch_bounds__(64 * TPB) void k_route(RouteArgs A) {
         if (lane < A.k) {
             A.idx[(size_t)t * A.k + lane] = P.idx;
             A.wt[(size_t)t * A.k + lane] = P.w;
-            ent[wave * A.k + lane] = P.idx;
-            atomicOr(&tmask[P.idx], 1u << wave);
+            if (A.counts) {
+                ent[wave * A.k + lane] = P.idx;
+                atomicOr(&tmask[P.idx], 1u << wave);
+            }
         }
         if (preq) {
             // codes stay where the caller put them; only the lane-group-major
@@ -526,6 +531,7 @@ __global__ __launch_bounds__(64 * TPB) void k_route(RouteArgs A) {
         }
         }
     }
+    if (!A.counts) return;
     __syncthreads();
     const int ntok = min(TPB, A.T - t0);
     if (threadIdx.x < ntok * A.k) {
@@ -3165,7 +3171,7 @@ static int launch_forward(const Scratch &c, Plan &P, int pm, const q36moe_weight
                           c.hq, c.hs, out, out_fmt, xs_in, 0, 0, c.hsf};
     } else {
         P.ra = RouteArgs{logits, ld_logits, T, E, K, scale, x, x_fmt, D, nb,
-                         c.topk_idx, c.topk_w, c.xq, c.xs, c.xs2, c.blk_cnt, c.rank, xs_in};
+                         c.topk_idx, c.topk_w, c.xq, c.xs, c.xs2, c.blk_cnt, c.rank, xs_in, nullptr, nullptr, 1};
         P.sa = ScanArgs{c.blk_cnt, nb, tpb, nb <= kScanInlineBlocks ? 1 : 0, E, T, K, c.topk_idx, c.topk_w, c.rank,
                         shg, ld_shg, tn, tn_sh, c.blk_off, c.tot, c.e_off, c.perm, c.pos, c.row_tok, c.row_w,
                         c.tiles, c.ntiles};
@@ -3191,7 +3197,8 @@ static int launch_forward(const Scratch &c, Plan &P, int pm, const q36moe_weight
         const int stn = (size_t)n <= (size_t)4 * E ? kSxTok : kSkTok;
         P.sx = SxArgs{c.topk_idx, c.topk_w, shg, ld_shg, c.perm, c.pos, c.e_off, T, K, E,
                       fused && n <= kSxDiscoverMax ? 1 : 0, stn};
-        if (P.sx.discover) {   // grid for tiles of stn rows
+        if (P.sx.discover) {   // grid for tiles of stn rows; no counts for a scatter
+            P.ra.counts = 0;
             int t = n / stn + (n < E ? n : E) + (has_sh ? (T + stn - 1) / stn : 0);
             P.tiles = (t + 7) & ~7;
         }
