@@ -519,12 +519,16 @@ def main():
         B.setup(c, args.seed + 17)
         for i in range(3):
             B.step(i)
-        g = B.graph(0, args.layers)
+        # as many forwards per graph as the configuration's own run (at most
+        # 1000): a replay's launch and cache-flush overhead spread over only
+        # 40 forwards added ~4 us per layer at decode32
+        n_c = max(args.layers, min(CONFIGS[c]["steps"], 1000))
+        g = B.graph(0, n_c)
         B.time_replays(g, 1)
         rms = B.time_replays(g, 3)
         del g
         U_c, path_c, st_c = B.stage_times(budget_us=5e4)
-        cfgs[c] = B.summary(float(np.median(rms)) / args.layers, U_c, path_c, st_c)
+        cfgs[c] = B.summary(float(np.median(rms)) / n_c, U_c, path_c, st_c)
     if cfgs:
         res["configs"] = cfgs
     if not args.no_cpu and not host_up:
