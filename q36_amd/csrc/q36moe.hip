@@ -1689,7 +1689,9 @@ __global__ __launch_bounds__(64 * kDlW, Q8 ? 2 : 1) void k_down_lds(GemmArgs A) 
 //   reads: RT row tiles x 8/RT K-steps per step measured 51 / 53 / 60 us at
 //   decode32 for RT = 1 / 2 / 4 (8 / 4 / 2 KiB runs); 16 KiB steps (one
 //   whole row tile) 51.6.  RT = 1 is used, although each B fragment read
-//   from LDS then feeds only NJ MFMAs.
+//   from LDS then feeds only NJ MFMAs.  An expert with a single tile loads
+//   its weights non-temporal (NT).  The kernel serves up to 512 tokens at
+//   256 experts, where its tiles still fit one workgroup per CU.
 //   x rows of the tile sit in LDS (2 KiB each, 16-byte chunk index XORed in
 //   its low 4 bits with the row, so a fragment read's 16 rows hit 16 bank
 //   groups); h rows in the dl_boff layout of k_down_lds.
@@ -1711,7 +1713,7 @@ struct SxLds {
 
 // Tile discovery for k_skinny_expert (in place of k_scatter): every
 // workgroup counts the routed entries per expert from the top-k indices,
-// scans the counts into offsets and 32-row tiles, finds its own tile and
+// scans the counts into offsets and tiles of tn rows, finds its own tile and
 // gathers that tile's entries in entry order -- the stable sorted order of
 // k_scatter, so perm / pos / e_off come out identical.  At most
 // kSxDiscoverMax routed entries (kSxEnt per thread).
