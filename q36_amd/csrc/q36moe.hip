@@ -193,9 +193,10 @@ __device__ __forceinline__ uint32_t logit_key(float f) {
 //      max) * scale, the reference's exp(l-m)/sum_all renormalised over the
 //      picks (q36_ops.cuh:424-430), in which the full denominator cancels;
 //      the sum runs in slot order as the reference's renormalisation does.
-// `lds` is kRouteLds words private to the wave: [0,8) pick keys, [8,16) pick
-// indices, then up to 256 (key, index) candidates.
-constexpr int kRouteLds = 2 * kMaxTopK + 2 * (kMaxExperts + 8);
+// `lds` is kRouteLds words private to the wave (16-byte aligned): [0,8) pick
+// keys, [8,16) pick indices, then up to 256 (key, index) candidates and 16
+// zero pads.
+constexpr int kRouteLds = 2 * kMaxTopK + 2 * (kMaxExperts + 16);
 
 struct Pick {
     int idx;     // expert index of pick `lane` (lanes < k)
@@ -218,8 +219,13 @@ __device__ __forceinline__ uint32_t group8_max(uint32_t v) {
     return v;
 }
 
-__device__ __forceinline__ Pick route_pick(const float *__restrict__ l, int E, int k, float scale,
-                                           uint32_t *lds) {
+// Steps 1-3: the picks' keys go to lds[0, k) and their indices to
+// lds[kMaxTopK, kMaxTopK + k), in slot order.  Returns, in every lane, the
+// expert index of slot `want` (wave-uniform; -1 for none), taken from the
+// ranking lanes by ballot so a caller that needs one slot does not wait for
+// the pick writes.  The writes are made visible by route_sync().
+__device__ __forceinline__ int route_rank(const float *__restrict__ l, int E, int k,
+                                          uint32_t *lds, int want) {
     const int lane = __lane_id();
     // the four loads are unconditional and independent (a guarded load
     // would be sunk into a branch and waited on one at a time)
@@ -254,42 +260,71 @@ __device__ __forceinline__ Pick route_pick(const float *__restrict__ l, int E, i
         if (c) cand[pos] = ((uint64_t)key[j] << 32) | (uint32_t)~(uint32_t)(lane + 64 * j);
         nc += __popcll(sel);
     }
-    // padded to a multiple of 8 with 0, which outranks nothing
-    if (lane < 8) cand[nc + lane] = 0ull;
+    // padded to a multiple of 16 with 0, which outranks nothing
+    if (lane < 16) cand[nc + lane] = 0ull;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // 3. rank each candidate; ranks below k are the picks
+    // 3. rank each candidate; ranks below k are the picks, 16 candidates
+    //    read per pass (32 per pass measured the same).
+    int e = 0;
     for (int c0 = 0; c0 < nc; c0 += 64) {
         const int ci = c0 + lane;
         const uint64_t mo = cand[ci < nc ? ci : 0];
         int r = 0;
-        for (int d = 0; d < nc; d += 8) {
-            uint64_t o[8];
+        for (int d = 0; d < nc; d += 16) {
+            uint64_t o[16];
 #pragma unroll
-            for (int u = 0; u < 8; u++) o[u] = cand[d + u];
+            for (int u = 0; u < 16; u++) o[u] = cand[d + u];
 #pragma unroll
-            for (int u = 0; u < 8; u++) r += o[u] > mo;
+            for (int u = 0; u < 16; u++) r += o[u] > mo;
         }
-        if (ci < nc && r < k) {
+        const bool pick = ci < nc && r < k;
+        if (pick) {
             lds[r] = (uint32_t)(mo >> 32);
             lds[kMaxTopK + r] = ~(uint32_t)mo;
         }
+        const uint64_t m = __ballot(pick && r == want);
+        if (m) e = (int)~(uint32_t)__builtin_amdgcn_readlane((uint32_t)mo, __builtin_ctzll(m));
     }
+    return e;
+}
+
+__device__ __forceinline__ void route_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // 4. weights
-    const int me = lane < k ? lane : 0;
-    const float vmax = key_val(lds[0]);
+}
+
+// Step 4, after route_sync(): the weight of slot `slot` (any lane may ask
+// for any slot < k).  All eight pick keys are read at once; slots >= k add
+// an exact 0 so the sum runs over slots 0..k-1 in order.
+__device__ __forceinline__ float route_weight(const uint32_t *lds, int k, float scale, int slot) {
+    const uint4 a = *reinterpret_cast<const uint4 *>(lds);
+    const uint4 b = *reinterpret_cast<const uint4 *>(lds + 4);
+    const uint32_t kk[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    const float vmax = key_val(kk[0]);
     float wsum = 0.0f;
+    uint32_t mine = kk[0];
 #pragma unroll
-    for (int q = 0; q < kMaxTopK; q++)
-        if (q < k) wsum += fast_exp(key_val(lds[q]) - vmax);
+    for (int q = 0; q < kMaxTopK; q++) {
+        const float t = fast_exp(key_val(kk[q]) - vmax);
+        wsum += q < k ? t : 0.0f;
+        mine = q == slot ? kk[q] : mine;
+    }
+    return fast_exp(key_val(mine) - vmax) * __builtin_amdgcn_rcpf(wsum) * scale;
+}
+
+__device__ __forceinline__ Pick route_pick(const float *__restrict__ l, int E, int k, float scale,
+                                           uint32_t *lds) {
+    const int lane = __lane_id();
+    route_rank(l, E, k, lds, -1);
+    route_sync();
+    const int me = lane < k ? lane : 0;
     Pick P;
     P.idx = (int)lds[kMaxTopK + me];
     P.slot = me;
-    P.w = fast_exp(key_val(lds[me]) - vmax) * __builtin_amdgcn_rcpf(wsum) * scale;
+    P.w = route_weight(lds, k, scale, me);
     return P;
 }
 
@@ -474,7 +509,7 @@ template <int TPB>
 __global__ __launch_bounds__(64 * TPB) void k_route(RouteArgs A) {
     __shared__ uint32_t tmask[kMaxExperts];
     __shared__ int ent[TPB * kMaxTopK];
-    __shared__ uint32_t rlds[TPB][kRouteLds];
+    __shared__ __align__(16) uint32_t rlds[TPB][kRouteLds];
     static_assert(TPB <= 32, "token mask");
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int t0 = blockIdx.x * TPB;
@@ -545,7 +580,7 @@ __global__ __launch_bounds__(64 * TPB) void k_route(RouteArgs A) {
 
 __global__ __launch_bounds__(256) void k_topk(const float *logits, int T, int E, int ld, int k,
                                              float scale, int renorm, int32_t *idx, float *wt) {
-    __shared__ uint32_t rlds[4][kRouteLds];
+    __shared__ __align__(16) uint32_t rlds[4][kRouteLds];
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= T) return;
     route_token(logits + (size_t)t * ld, E, k, scale, renorm, idx + (size_t)t * k, wt + (size_t)t * k,
@@ -2160,7 +2195,7 @@ struct DirectGateupLds {
     uint8_t sxs[kDD / 32];
     float sxf[kDD / 32];                  // int8 x scales (q8_0-split shared expert)
     float red[4][2][32];                  // per wave: gate / up partial sums of up to 2 row tiles
-    uint32_t rlds[4][kRouteLds];
+    __align__(16) uint32_t rlds[4][kRouteLds];
 };
 
 // Shared-expert entry of the direct path when its matrices are q8_0-split
@@ -2277,11 +2312,9 @@ __device__ __forceinline__ void direct_gateup_body(const DirectArgs &A, int i, i
     float wgt = 0.0f;
     if (routed) {
         // every wave routes the token (no barrier needed to share the result)
-        const Pick P = route_pick(A.logits + (size_t)t * A.ld, A.E, A.k, A.scale, rlds[wave]);
-        const uint64_t m = __ballot(lane < A.k && P.slot == s);
-        const int L = __builtin_ctzll(m);
-        e = __builtin_amdgcn_readlane(P.idx, L);
-        wgt = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(P.w), L));
+        // the expert index comes straight from the ranking lanes; the weight
+        // (a further LDS round trip) is read after the weight loads issue
+        e = route_rank(A.logits + (size_t)t * A.ld, A.E, A.k, rlds[wave], s);
     } else {
         wgt = 1.0f / (1.0f + expf(-A.shg[(size_t)t * A.ld_shg]));
     }
@@ -2301,6 +2334,10 @@ __device__ __forceinline__ void direct_gateup_body(const DirectArgs &A, int i, i
         const size_t so = nib + ((size_t)(ft0 + u) * 64 + lane) * (kDD / 128) + wave * 4;
         sag[u] = *reinterpret_cast<const int *>(Wg + so);
         sau[u] = *reinterpret_cast<const int *>(Wu + so);
+    }
+    if (routed) {
+        route_sync();
+        wgt = route_weight(rlds[wave], A.k, A.scale, s);
     }
 
     if (A.x_fmt == kFmtE4M3) {
