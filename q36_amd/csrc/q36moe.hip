@@ -826,7 +826,7 @@ __device__ __forceinline__ v4f mfma_sel(int sel, const v8i &a, const v8i &b, con
 // per-step barrier the other keeps the matrix pipes busy.  Per K-step of 128
 // the workgroup stages 8 A tiles (8 KiB of E2M1 fragments, contiguous in the
 // packed layout) and the tile's B rows (128 B of each e4m3 x row) with
-// global_load_lds_dwordx4: the data goes from L2 to LDS without passing
+// buffer_load_dwordx4 ... lds: the data goes from L2 to LDS without passing
 // through VGPRs, and 8 lanes cover one 128-byte x row.  A streams from HBM
 // with three stages (two K-steps in flight); B mostly hits L2 and has two.
 // Waves form a 2 x 2 grid: wave w computes gate and up tiles 2(w&1)..+1
@@ -835,8 +835,18 @@ __device__ __forceinline__ v4f mfma_sel(int sel, const v8i &a, const v8i &b, con
 // lanes of a fragment read hit 16 distinct bank groups.
 constexpr int kGdTok = 160;                      // rows per fat tile (10 column tiles)
 
-__device__ __forceinline__ void dma16(const void *g, void *lds) {
-    __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 0);
+// Direct-to-LDS loads are issued in their buffer (MUBUF) form, not as
+// global_load_lds: the global form is a FLAT instruction that may access
+// LDS, and while one is outstanding the compiler's wait counting treats the
+// LDS counter as out of order, so every later LDS fragment read was waited
+// on with lgkmcnt(0) (all reads of the step) instead of the count of reads
+// issued after it.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t dma_src(const void *base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, 0x7ffffffe, 0x00020000);
+}
+template <int AUX = 0>
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t off, void *lds) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 16, off, 0, 0, AUX);
 }
 
 // Barrier for the staging pipeline.  A fence-based barrier would make the
@@ -857,9 +867,14 @@ __device__ __forceinline__ void lds_barrier() {
 }
 __device__ __forceinline__ void dma_barrier() {
     // the scheduler may move MFMAs across an asm barrier: pin them (and all
-    // else) to their step, or every step's fragments stay live at once
+    // else) to their step, or every step's fragments stay live at once.
+    // The wait is the builtin (lgkmcnt(0) only), not inline asm: the
+    // compiler's wait counting does not see inside asm, so after an asm
+    // wait it still counted earlier scalar loads as outstanding and put a
+    // full lgkmcnt(0) before the first fragment use of every step.
     __builtin_amdgcn_sched_barrier(0);
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // gfx9 encoding: vmcnt 63, expcnt 7, lgkmcnt 0
+    __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
 }
 
@@ -909,17 +924,18 @@ __device__ __forceinline__ void body(const GemmArgs &A, Lds &L, const uint8_t *W
         const int r = min(2 * m + (s >> 3), ntok - 1);
         boff[i] = (uint32_t)A.row_tok[p0 + r] * KD + (s & 7) * 16;
     }
+    const __amdgpu_buffer_rsrc_t rg = dma_src(Wg), ru = dma_src(Wu), rb = dma_src(A.bq);
     auto issue_a = [&](int kt, int slot) {
-        __builtin_amdgcn_global_load_lds(Wg + (aoff + kt * 1024), &L.a[slot][wave * 1024], 16, 0, kNt);
-        __builtin_amdgcn_global_load_lds(Wu + (aoff + kt * 1024), &L.a[slot][(RT + wave) * 1024], 16, 0, kNt);
+        dma16<kNt>(rg, aoff + kt * 1024, &L.a[slot][wave * 1024]);
+        dma16<kNt>(ru, aoff + kt * 1024, &L.a[slot][(RT + wave) * 1024]);
     };
     auto issue_b = [&](int kt, int slot) {
 #pragma unroll
-        for (int i = 0; i < NBI; i++) dma16(A.bq + (boff[i] + kt * 128), &L.b[slot][(wave + W * i) * 1024]);
+        for (int i = 0; i < NBI; i++) dma16(rb, boff[i] + kt * 128, &L.b[slot][(wave + W * i) * 1024]);
     };
-    const size_t nib = (size_t)512 * KD / 2;
-    dma16(Wg + nib + ((size_t)(mt0 + wave) * 64 + lane) * 16, &L.sc[wave * 1024]);
-    dma16(Wu + nib + ((size_t)(mt0 + wave) * 64 + lane) * 16, &L.sc[(RT + wave) * 1024]);
+    const uint32_t nib = (uint32_t)512 * KD / 2;
+    dma16(rg, nib + ((uint32_t)(mt0 + wave) * 64 + lane) * 16, &L.sc[wave * 1024]);
+    dma16(ru, nib + ((uint32_t)(mt0 + wave) * 64 + lane) * 16, &L.sc[(RT + wave) * 1024]);
     constexpr int NJ1 = NJ > 0 ? NJ : 1;
     u32x4 sb[NJ1];
 #pragma unroll
@@ -927,11 +943,15 @@ __device__ __forceinline__ void body(const GemmArgs &A, Lds &L, const uint8_t *W
         const int r = min(16 * (wt + 2 * j) + n, ntok - 1);
         sb[j] = *reinterpret_cast<const u32x4 *>(A.bs2 + (size_t)A.row_tok[p0 + r] * (KD / 32) + q * 16);
     }
-    // step kt issues B(kt+1) then A(kt+2) after its barrier; when step kt
-    // needs B(kt), only A(kt+1) was issued after it
+    // step kt issues B(kt+1) then A(kt+3) after its barrier (A's slot kt+3
+    // is the one step kt-1 read; three steps cover the HBM latency of the
+    // weights, two did not: with A staged two steps ahead the kernel took
+    // 88 us, 66 without A's loads at all); when step kt needs B(kt), only
+    // A(kt+2) was issued after it
     issue_a(0, 0);
     issue_b(0, 0);
     issue_a(1, 1);
+    issue_a(2, 2);
 
     v4f acc[4][NJ1];
 #pragma unroll
@@ -954,13 +974,14 @@ __device__ __forceinline__ void body(const GemmArgs &A, Lds &L, const uint8_t *W
             for (int a = 0; a < 4; a++)
 #pragma unroll
                 for (int j = 0; j < NJ; j++) asm volatile("" : "+v"(acc[a][j]));
-            if constexpr (LAST && st == 3) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            // the last steps issue no A after their B: wait for everything
+            if constexpr (LAST && st >= 2) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             else asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
             dma_barrier();
             // restage the slots read in the previous step (free: every wave
             // has passed this barrier) before this step's MFMAs
             if constexpr (!(LAST && st == 3)) issue_b(kt + 1, (st + 1) & 1);
-            if constexpr (!(LAST && st >= 2)) issue_a(kt + 2, (st + 2) & 3);
+            if constexpr (!(LAST && st >= 1)) issue_a(kt + 3, (st + 3) & 3);
             __builtin_amdgcn_sched_barrier(0);
             if constexpr (st == 0) {
 #pragma unroll
@@ -970,30 +991,37 @@ __device__ __forceinline__ void body(const GemmArgs &A, Lds &L, const uint8_t *W
                 }
             }
             // A fragments first (4, held for the step), then column tile j's
-            // B fragment is read while the MFMAs of tile j-1 run
+            // B fragment is read while the MFMAs of tiles j-2 and j-1 run
+            // (LDS latency under load is longer than one tile's 4 MFMAs)
             u32x4 af[4];
 #pragma unroll
             for (int a = 0; a < 4; a++) {
                 const int slot = (a < 2 ? 0 : RT) + 2 * wa + (a & 1);
                 af[a] = *reinterpret_cast<const u32x4 *>(&L.a[st][slot * 1024 + lane * 16]);
             }
-#pragma unroll
-            for (int j = 0; j < NJ; j++) {
+            auto read_b = [&](int j) {
                 const int r = 16 * (wt + 2 * j) + n;
                 const u32x4 b0 = *reinterpret_cast<const u32x4 *>(&L.b[st & 1][gd_boff(r, q)]);
                 const u32x4 b1 = *reinterpret_cast<const u32x4 *>(&L.b[st & 1][gd_boff(r, 4 + q)]);
-                const v8i bv = v8i{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
+                return v8i{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
+            };
+            v8i bq[NJ1 + 1];
+#pragma unroll
+            for (int j = 0; j < NJ; j++) {
+                if (j == 0) bq[0] = read_b(0);
+                if (j == 0 && NJ > 1) bq[1] = read_b(1);
+                if (j + 2 < NJ) bq[j + 2] = read_b(j + 2);
 #pragma unroll
                 for (int a = 0; a < 4; a++) {
                     const v8i av = v8i{(int)af[a][0], (int)af[a][1], (int)af[a][2], (int)af[a][3], 0, 0, 0, 0};
-                    acc[a][j] = mfma_f4xf8<st, st>(av, bv, acc[a][j], (int)sa[a], (int)sbg[j]);
+                    acc[a][j] = mfma_f4xf8<st, st>(av, bq[j], acc[a][j], (int)sa[a], (int)sbg[j]);
                 }
             }
             if constexpr (NJ > 0) {
-                __builtin_amdgcn_sched_group_barrier(0x100, 4 + 2 + (st == 0 ? 4 : 0), 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 4 + 2 + (NJ > 1 ? 2 : 0) + (st == 0 ? 4 : 0), 0);
 #pragma unroll
                 for (int j = 0; j < NJ; j++) {
-                    if (j + 1 < NJ) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+                    if (j + 2 < NJ) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
                     __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
                 }
             }
@@ -1516,13 +1544,14 @@ __device__ __forceinline__ void stage_h_rows(const uint8_t *bq, int c0, int nr, 
     const int lane = threadIdx.x & 63;
     const int npair = __builtin_amdgcn_readfirstlane((nr + 1) >> 1);
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const __amdgpu_buffer_rsrc_t rq = dma_src(bq);
 #pragma unroll
     for (int u = 0; u < kDlRows / 2 / kDlW; u++) {
         const int pr = wv + kDlW * u;
         if (pr < npair) {
             const int r = 2 * pr + (lane >> 5), ph = lane & 31;
             const int c = (ph & 16) | ((ph ^ r) & 15);       // logical chunk in this slot
-            dma16(bq + (size_t)(c0 + min(r, nr - 1)) * KD + c * 16, &sb[pr * 1024]);
+            dma16(rq, (uint32_t)(c0 + min(r, nr - 1)) * KD + c * 16, &sb[pr * 1024]);
         }
     }
 }
