@@ -211,6 +211,18 @@ __device__ __forceinline__ float key_val(uint32_t kk) {
     return __uint_as_float((kk & 0x80000000u) ? (kk & 0x7fffffffu) : ~kk);
 }
 
+// max of a over lanes l, l^16, l^32, l^48, in every lane: v_permlane16_swap
+// / v_permlane32_swap put the two rows (halves) of each pair side by side
+// in two registers -- VALU work, where a shuffle is an LDS round trip
+// (ds_bpermute).  Same result as fmaxf with __shfl_xor 16 then 32 (fmaxf is
+// commutative, NaN included).
+__device__ __forceinline__ float max_rows4(float a) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(a), false, false);
+    a = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(a), false, false);
+    return fmaxf(__uint_as_float(t[0]), __uint_as_float(t[1]));
+}
+
 // max over each aligned group of 8 lanes, in every lane of the group
 __device__ __forceinline__ uint32_t group8_max(uint32_t v) {
     v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xf, 0xf, false));   // quad xor 1
@@ -776,8 +788,7 @@ __device__ __forceinline__ void store_h_block(const GemmArgs &A, bool q8, int p,
     for (int r = 0; r < 2; r++)
 #pragma unroll
         for (int i = 0; i < 4; i++) amax = fmaxf(amax, fabsf(h[r][i]));
-    amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+    amax = max_rows4(amax);
     const int b = ffb / 32, nb = A.ldo / 32;
     if (q8) {
         const float inv = q8b_inv(amax);
@@ -1486,8 +1497,7 @@ constexpr int kDlRows = 128;             // B rows staged per chunk
 __device__ __forceinline__ void store_dn16(const GemmArgs &A, int p, int g, int q, bool valid, float v0, float v1,
                                            float v2, float v3) {
     float a = fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3)));
-    a = fmaxf(a, __shfl_xor(a, 16, 64));
-    a = fmaxf(a, __shfl_xor(a, 32, 64));
+    a = max_rows4(a);
     uint32_t eb = (__float_as_uint(a) >> 23) & 0xffu;
     eb = eb == 255u ? 255u : eb < 15u ? 15u : eb > 254u ? 254u : eb;
     const float mul = __uint_as_float((268u - eb) << 23);
@@ -1512,8 +1522,7 @@ __device__ __forceinline__ void store_dn16x4(const GemmArgs &A, int p, int mt0, 
 #pragma unroll
     for (int i = 0; i < 4; i++)
         a = fmaxf(a, fmaxf(fmaxf(fabsf(c[i][0]), fabsf(c[i][1])), fmaxf(fabsf(c[i][2]), fabsf(c[i][3]))));
-    a = fmaxf(a, __shfl_xor(a, 16, 64));
-    a = fmaxf(a, __shfl_xor(a, 32, 64));
+    a = max_rows4(a);
     a *= fabsf(w);
     uint32_t eb = (__float_as_uint(a) >> 23) & 0xffu;
     eb = eb == 255u ? 255u : eb < 15u ? 15u : eb > 254u ? 254u : eb;
@@ -1974,8 +1983,7 @@ __device__ __forceinline__ void skinny_expert(const GemmArgs &G, const GemmArgs 
             for (int rr = 0; rr < 2; rr++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) amax = fmaxf(amax, fabsf(h[rr][i]));
-            amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
-            amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+            amax = max_rows4(amax);
             const int e2 = quant_exp(amax);
             const float mul = inv_scale(e2);
             const int ffb = 64 * wave + 32 * blk, b = ffb / 32;
