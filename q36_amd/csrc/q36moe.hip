@@ -211,6 +211,13 @@ __device__ __forceinline__ float key_val(uint32_t kk) {
     return __uint_as_float((kk & 0x80000000u) ? (kk & 0x7fffffffu) : ~kk);
 }
 
+// max of a over the 4 lanes of its quad (lanes 4j..4j+3), in every lane:
+// DPP quad permutes (xor 1, xor 2) instead of two LDS shuffles.
+__device__ __forceinline__ float max_quad(float a) {
+    a = fmaxf(a, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0xB1, 0xf, 0xf, false)));
+    return fmaxf(a, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x4E, 0xf, 0xf, false)));
+}
+
 // max of a over lanes l, l^16, l^32, l^48, in every lane: v_permlane16_swap
 // / v_permlane32_swap put the two rows (halves) of each pair side by side
 // in two registers -- VALU work, where a shuffle is an LDS round trip
@@ -417,8 +424,7 @@ __device__ __forceinline__ uint8_t quant8_lane(const float (&v)[8], int lane, ui
     float a = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; i++) a = fmaxf(a, fabsf(v[i]));
-    a = fmaxf(a, __shfl_xor(a, 1, 64));
-    a = fmaxf(a, __shfl_xor(a, 2, 64));
+    a = max_quad(a);
     const int e2 = quant_exp(a);
     const float mul = inv_scale(e2);
     const uint32_t w0 = e4m3x4(v[0] * mul, v[1] * mul, v[2] * mul, v[3] * mul);
@@ -568,8 +574,7 @@ __global__ __launch_bounds__(64 * TPB) void k_route(RouteArgs A) {
                 float a = 0.0f;
 #pragma unroll
                 for (int i = 0; i < 8; i++) a = fmaxf(a, fabsf(v[i]));
-                a = fmaxf(a, __shfl_xor(a, 1, 64));
-                a = fmaxf(a, __shfl_xor(a, 2, 64));
+                a = max_quad(a);
                 const float inv = q8b_inv(a);
                 *reinterpret_cast<uint2 *>(A.xq8 + o) =
                     make_uint2(q8b4(v[0], v[1], v[2], v[3], inv), q8b4(v[4], v[5], v[6], v[7], inv));
@@ -667,12 +672,16 @@ __device__ __forceinline__ void wave_scan256(const int *v, int n, int *out, int 
         a[j] = (4 * lane + j < n) ? v[4 * lane + j] : 0;
         s += a[j];
     }
+    // inclusive scan over the wave: row_shr 1/2/4/8 within each 16-lane row
+    // (lanes without a source add 0), then the rows' totals by row_bcast15
+    // (rows 1, 3) and row_bcast31 (rows 2, 3) -- DPP moves, not LDS shuffles
     int inc = s;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int y = __shfl_up(inc, o, 64);
-        if (lane >= o) inc += y;
-    }
+    inc += __builtin_amdgcn_update_dpp(0, inc, 0x111, 0xf, 0xf, false);
+    inc += __builtin_amdgcn_update_dpp(0, inc, 0x112, 0xf, 0xf, false);
+    inc += __builtin_amdgcn_update_dpp(0, inc, 0x114, 0xf, 0xf, false);
+    inc += __builtin_amdgcn_update_dpp(0, inc, 0x118, 0xf, 0xf, false);
+    inc += __builtin_amdgcn_update_dpp(0, inc, 0x142, 0xa, 0xf, false);
+    inc += __builtin_amdgcn_update_dpp(0, inc, 0x143, 0xc, 0xf, false);
     int run = inc - s;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
@@ -2264,8 +2273,7 @@ __device__ __forceinline__ void direct_shared_q8(const DirectArgs &A, int t, int
     float amax = 0.0f;
 #pragma unroll
     for (int u = 0; u < 8; u++) amax = fmaxf(amax, fabsf(v[u]));
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+    amax = max_quad(amax);
     const float inv = q8b_inv(amax);
     *reinterpret_cast<uint2 *>(sx + wave * 512 + lane * 8) =
         make_uint2(q8b4(v[0], v[1], v[2], v[3], inv), q8b4(v[4], v[5], v[6], v[7], inv));
@@ -2493,8 +2501,7 @@ __global__ __launch_bounds__(576) void k_direct_down(DirectArgs A) {
         float amax = 0.0f;
 #pragma unroll
         for (int u = 0; u < 8; u++) amax = fmaxf(amax, fabsf(hv[u]));
-        amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-        amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+        amax = max_quad(amax);
         const float inv = q8b_inv(amax);
         const uint2 hc = make_uint2(q8b4(hv[0], hv[1], hv[2], hv[3], inv), q8b4(hv[4], hv[5], hv[6], hv[7], inv));
         *reinterpret_cast<uint2 *>(&sh[wave][lane * 8]) = hc;
