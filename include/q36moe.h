@@ -68,7 +68,11 @@ extern "C" {
 #define Q36MOE_TAP_HS        8  /* u8    [T*k+T][d_ff/32] E8M0          */
 #define Q36MOE_TAP_DNW       9  /* f32   [T*k+T][d_model] w * down rows
                                    (staged as f16 with a power-of-two
-                                   scale per 16 columns; widened here)  */
+                                   scale per 16 columns; widened here);
+                                   rows in sorted order, or in entry
+                                   order (t*k+s, then n+t for the shared
+                                   expert) when last_path is 3 and
+                                   T*k <= 4096 (tiles found in-kernel) */
 #define Q36MOE_TAP_HSF      10  /* f32   [T*k+T][d_ff/32] int8 h scales
                                    (q8_0-split down; HQ then holds int8) */
 #define Q36MOE_TAP_XQ8      11  /* i8    [T][d_model] int8 x of a q8_0-split

@@ -1786,6 +1786,7 @@ struct SxLds {
     uint32_t hs[kSkTok][4];   // h scale dwords by lane group (lane-group-major order)
     float ws[kSkTok];         // routing weight of each row
     int tok[kSkTok];          // token of each row (rows past the tile repeat its last)
+    int ent[kSkTok];          // staging row of each row's down output (see dn_store)
     // tile discovery: per-expert counts, their exclusive prefixes, tiles per
     // expert and theirs, per-wave counts, the tile found
     int cnt[kMaxExperts], off[kMaxExperts + 1], ntl[kMaxExperts], toff[kMaxExperts + 1];
@@ -2020,7 +2021,7 @@ __device__ __forceinline__ void skinny_expert(const GemmArgs &G, const GemmArgs 
         for (int j = 0; j < NJ; j++) {
             const int r = 16 * j + n;
             const v4f c4[4] = {acc[0][j], acc[1][j], acc[2][j], acc[3][j]};
-            store_dn16x4(Dn, p0 + r, mt0, q, r < nr, c4, L.ws[r]);
+            store_dn16x4(Dn, L.ent[r], mt0, q, r < nr, c4, L.ws[r]);
 #pragma unroll
             for (int i = 0; i < 4; i++) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
         }
@@ -2148,6 +2149,7 @@ __device__ void sx_gather(const SxArgs &X, SxLds &L, int e, int p0, int p1, cons
                 const int r = rank - rank0, i = tid + 64 * kSxW * u;
                 L.tok[r] = i / X.k;
                 L.ws[r] = wv[u];
+                L.ent[r] = i;   // staged in entry order: the combine needs no pos
                 X.pos[i] = p0 + r;
                 X.perm[p0 + r] = i;
             }
@@ -2160,6 +2162,7 @@ __device__ void sx_gather(const SxArgs &X, SxLds &L, int e, int p0, int p1, cons
             const int t = r0 + tid;
             L.tok[tid] = t;
             L.ws[tid] = 1.0f / (1.0f + expf(-X.shg[(size_t)t * X.ld_shg]));
+            L.ent[tid] = n + t;
         }
         lds_barrier();
     }
@@ -2198,6 +2201,7 @@ __global__ __launch_bounds__(64 * kSxW) void k_skinny_expert(GemmArgs G, GemmArg
                 const int r = min((int)threadIdx.x, p1 - p0 - 1);
                 L.tok[threadIdx.x] = G.row_tok[p0 + r];
                 L.ws[threadIdx.x] = G.row_w[p0 + r];
+                L.ent[threadIdx.x] = p0 + r;   // sorted order (the combine reads pos)
             }
             __syncthreads();
         };
@@ -2599,7 +2603,9 @@ __global__ __launch_bounds__(256) void k_combine(const uint16_t *__restrict__ dn
 #pragma unroll
     for (int s = 0; s < kMaxTopK + 1; s++) {
         if (s < ns) {
-            const size_t p = s < k ? (size_t)pos[(size_t)t * k + s] : (size_t)(n + t);
+            // pos null: rows staged in entry order (the one-kernel path with
+            // its tiles found in-kernel), so no dependent load of pos
+            const size_t p = s < k ? (pos ? (size_t)pos[(size_t)t * k + s] : (size_t)t * k + s) : (size_t)(n + t);
             hv[s] = *reinterpret_cast<const uint4 *>(dnh + p * D + j);
             ev[s] = dne[p * (D / 16) + (j >> 4)];
         }
@@ -3174,7 +3180,7 @@ static void launch_stage(const Scratch &c, const Plan &P, int st, hipStream_t s)
         case ST_COMBINE:
             // small batches: 64-thread blocks, so the work spreads over more CUs
             hipLaunchKernelGGL(k_combine, dim3(T, T < 256 ? D / 512 : D / 2048), dim3(T < 256 ? 64 : 256), 0, s, c.dnh,
-                               c.dne, c.pos, T, K, D, P.has_sh,
+                               c.dne, P.fused && P.sx.discover ? nullptr : c.pos, T, K, D, P.has_sh,
                                const_cast<void *>(P.out), P.out_fmt);
             break;
         default: break;
