@@ -630,37 +630,53 @@ struct ScanArgs {
 constexpr int kColExp = 8;
 constexpr int kScanInlineBlocks = 64;   // k_scatter does the column scan itself up to this many blocks
 __global__ __launch_bounds__(256) void k_colscan(ScanArgs A) {
-    constexpr int NP = 256 / kColExp;              // partitions per expert
-    __shared__ int part[kColExp][NP + 1];
+    constexpr int NP = 256 / kColExp;              // partitions per expert: one half-wave
+    static_assert(NP == 32, "one expert per half-wave");
+    constexpr int CH = 8;                          // counts held in registers per thread
+    const int lane = threadIdx.x & 63;
     const int el = threadIdx.x / NP, pi = threadIdx.x % NP;
     const int e = blockIdx.x * kColExp + el;
+    const bool ok = e < A.E;
     const int chunk = (A.nb + NP - 1) / NP;
     const int b0 = pi * chunk, b1 = min(A.nb, b0 + chunk);
     const int32_t *cnt = A.blk_cnt + (size_t)e * A.nb;
-    int sum = 0;
-    if (e < A.E)
+    // all of a thread's counts are loaded at once (one memory round trip)
+    int v[CH], sum = 0;
+    if (chunk <= CH) {
+#pragma unroll
+        for (int j = 0; j < CH; j++) {
+            v[j] = ok && b0 + j < b1 ? cnt[b0 + j] : 0;
+            sum += v[j];
+        }
+    } else if (ok) {
         for (int b = b0; b < b1; b++) sum += cnt[b];
-    part[el][pi] = sum;
-    __syncthreads();
-    if (pi == 0) {
-        int run = 0;
-        for (int j = 0; j < NP; j++) {
-            const int v = part[el][j];
-            part[el][j] = run;
-            run += v;
-        }
-        part[el][NP] = run;
     }
-    __syncthreads();
-    if (e < A.E) {
-        int run = part[el][pi];
+    // inclusive scan over the expert's 32 lanes: row_shr 1/2/4/8 inside each
+    // 16-lane row, then row_bcast15 adds row 0's (row 2's) total to row 1 (3)
+    int inc = sum;
+    inc += __builtin_amdgcn_update_dpp(0, inc, 0x111, 0xf, 0xf, false);
+    inc += __builtin_amdgcn_update_dpp(0, inc, 0x112, 0xf, 0xf, false);
+    inc += __builtin_amdgcn_update_dpp(0, inc, 0x114, 0xf, 0xf, false);
+    inc += __builtin_amdgcn_update_dpp(0, inc, 0x118, 0xf, 0xf, false);
+    inc += __builtin_amdgcn_update_dpp(0, inc, 0x142, 0xa, 0xf, false);
+    const int total = __shfl(inc, (lane & 32) | 31, 64);
+    if (!ok) return;
+    int run = inc - sum;
+    if (chunk <= CH) {
+#pragma unroll
+        for (int j = 0; j < CH; j++)
+            if (b0 + j < b1) {
+                A.blk_off[(size_t)e * A.nb + b0 + j] = run;
+                run += v[j];
+            }
+    } else {
         for (int b = b0; b < b1; b++) {
-            const int v = cnt[b];
+            const int c = cnt[b];
             A.blk_off[(size_t)e * A.nb + b] = run;
-            run += v;
+            run += c;
         }
-        if (pi == 0) A.tot[e] = part[el][NP];
     }
+    if (pi == 0) A.tot[e] = total;
 }
 
 // Exclusive scan of v[0..n) (n <= 256) by one wavefront into out (LDS).
@@ -704,6 +720,21 @@ __global__ __launch_bounds__(256) void k_scatter(ScanArgs A) {
     __shared__ int tot[kMaxExperts], off[kMaxExperts + 1], ntile[kMaxExperts], toff[kMaxExperts + 1];
     __shared__ int boff[kMaxExperts];
     const int tid = threadIdx.x, b = blockIdx.x;
+    // this thread's first entry and shared-gate logit are loaded up front,
+    // in flight with the totals and offsets
+    const int n = A.T * A.k;
+    const int i0 = b * A.tpb * A.k, i1 = min(n, i0 + A.tpb * A.k);
+    const int ia = i0 + tid;
+    int ea = 0, ra = 0;
+    float wa = 0.0f;
+    if (ia < i1) {
+        ea = A.idx[ia];
+        ra = A.rank[ia];
+        wa = A.wt[ia];
+    }
+    const int ts = b * A.tpb + tid, ts1 = min(A.T, (b + 1) * A.tpb);
+    float sga = 0.0f;
+    if (A.shg && ts < ts1) sga = A.shg[(size_t)ts * A.ld_shg];
     for (int e = tid; e < A.E; e += 256) {
         if (A.inline_cols) {
             const int32_t *cnt = A.blk_cnt + (size_t)e * A.nb;
@@ -724,20 +755,20 @@ __global__ __launch_bounds__(256) void k_scatter(ScanArgs A) {
     if (tid < 64) wave_scan256(tot, A.E, off, &off[A.E]);
     else if (tid < 128) wave_scan256(ntile, A.E, toff, &toff[A.E]);
     __syncthreads();
-    const int n = A.T * A.k;
-    const int i0 = b * A.tpb * A.k, i1 = min(n, i0 + A.tpb * A.k);
-    for (int i = i0 + tid; i < i1; i += 256) {
-        const int e = A.idx[i];
-        const int p = off[e] + boff[e] + A.rank[i];
+    auto place = [&](int i, int e, int r, float w) {
+        const int p = off[e] + boff[e] + r;
         A.perm[p] = i;
         A.pos[i] = p;
         A.row_tok[p] = i / A.k;
-        A.row_w[p] = A.wt[i];
-    }
+        A.row_w[p] = w;
+    };
+    if (ia < i1) place(ia, ea, ra, wa);
+    for (int i = ia + 256; i < i1; i += 256) place(i, A.idx[i], A.rank[i], A.wt[i]);
     if (A.shg) {
-        for (int t = b * A.tpb + tid; t < min(A.T, (b + 1) * A.tpb); t += 256) {
+        for (int t = ts; t < ts1; t += 256) {
+            const float g = t == ts ? sga : A.shg[(size_t)t * A.ld_shg];
             A.row_tok[n + t] = t;
-            A.row_w[n + t] = 1.0f / (1.0f + expf(-A.shg[(size_t)t * A.ld_shg]));
+            A.row_w[n + t] = 1.0f / (1.0f + expf(-g));
         }
     }
     if (b == 0) {
