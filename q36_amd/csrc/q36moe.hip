@@ -533,6 +533,31 @@ struct RouteArgs {
 // stable order of the sort), from a per-expert mask of the block's tokens.
 // Small batches use 4 tokens per workgroup to spread the quantisation over
 // more CUs; large ones 16, which keeps the per-block count table short.
+// FP8 quantisation of values 512c .. 512c+511 of token t's x (8 per lane,
+// 4 lanes per 32-block): codes, E8M0 scales in both layouts, and the int8 x
+// of a q8_0-split shared expert when A.xq8 is set.
+template <int XF>
+__device__ __forceinline__ void route_quant_pass(const RouteArgs &A, int t, int c, const X8 &xr, int lane) {
+    const int nb32 = A.D / 32;
+    const size_t o = (size_t)t * A.D + c * 512 + lane * 8;
+    const int b = c * 16 + (lane >> 2);
+    float v[8];
+    cvt8(xr, XF, v);
+    const uint8_t sb = quant8_lane(v, lane, A.xq + o, A.xs + (size_t)t * nb32 + b);
+    // lane-group-major copy for the grouped GEMM: [t][b % 4][b / 4]
+    if ((lane & 3) == 0) A.xs2[(size_t)t * nb32 + (b & 3) * (nb32 / 4) + (b >> 2)] = sb;
+    if (A.xq8) {   // the q8_0-split shared expert's int8 x (k_quant_q8b)
+        float a = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) a = fmaxf(a, fabsf(v[i]));
+        a = max_quad(a);
+        const float inv = q8b_inv(a);
+        *reinterpret_cast<uint2 *>(A.xq8 + o) =
+            make_uint2(q8b4(v[0], v[1], v[2], v[3], inv), q8b4(v[4], v[5], v[6], v[7], inv));
+        if ((lane & 3) == 0) A.xsf[(size_t)t * nb32 + b] = a / 127.0f;
+    }
+}
+
 // XF: the x format (A.x_fmt), fixed at compile time so the loads and their
 // waits are branch-free.
 template <int TPB, int XF>
@@ -570,25 +595,7 @@ __global__ __launch_bounds__(64 * TPB) void k_route(RouteArgs A) {
                 A.xs2[(size_t)t * nb32 + (b & 3) * (nb32 / 4) + (b >> 2)] = A.xs_in[(size_t)t * nb32 + b];
         } else {
 #pragma unroll
-        for (int c = 0; c < kRouteD / 512; c++) {
-            const size_t o = (size_t)t * A.D + c * 512 + lane * 8;
-            const int b = c * 16 + (lane >> 2);
-            float v[8];
-            cvt8(xr[c], XF, v);
-            const uint8_t sb = quant8_lane(v, lane, A.xq + o, A.xs + (size_t)t * nb32 + b);
-            // lane-group-major copy for the grouped GEMM: [t][b % 4][b / 4]
-            if ((lane & 3) == 0) A.xs2[(size_t)t * nb32 + (b & 3) * (nb32 / 4) + (b >> 2)] = sb;
-            if (A.xq8) {   // the q8_0-split shared expert's int8 x (k_quant_q8b)
-                float a = 0.0f;
-#pragma unroll
-                for (int i = 0; i < 8; i++) a = fmaxf(a, fabsf(v[i]));
-                a = max_quad(a);
-                const float inv = q8b_inv(a);
-                *reinterpret_cast<uint2 *>(A.xq8 + o) =
-                    make_uint2(q8b4(v[0], v[1], v[2], v[3], inv), q8b4(v[4], v[5], v[6], v[7], inv));
-                if ((lane & 3) == 0) A.xsf[(size_t)t * nb32 + b] = a / 127.0f;
-            }
-        }
+        for (int c = 0; c < kRouteD / 512; c++) route_quant_pass<XF>(A, t, c, xr[c], lane);
         }
         const Pick P = route_pick(lv, A.E, A.k, A.scale, rlds[wave]);
         if (lane < A.k) {
@@ -612,6 +619,36 @@ __global__ __launch_bounds__(64 * TPB) void k_route(RouteArgs A) {
         A.blk_cnt[(size_t)e * A.nb + blockIdx.x] = __popc(tmask[e]);
 }
 
+// k_route without the per-block counts (the one-kernel skinny path sorts
+// itself), one token per workgroup: wave w quantises values 512w .. 512w+511
+// and wave 0 also routes, so each wave has one pass of x in flight instead
+// of four.
+template <int XF>
+__global__ __launch_bounds__(64 * (kRouteD / 512)) void k_route_tok(RouteArgs A) {
+    __shared__ __align__(16) uint32_t rlds[kRouteLds];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int t = blockIdx.x;
+    constexpr bool preq = XF == kFmtE4M3;
+    X8 xr;
+    if constexpr (!preq) xr = load8_raw(A.x, XF, (size_t)t * A.D + wave * 512 + lane * 8);
+    float lv[4];
+    if (wave == 0) route_load(A.logits + (size_t)t * A.ld, A.E, lv);
+    if constexpr (preq) {
+        const int nb32 = A.D / 32;
+        for (int b = threadIdx.x; b < nb32; b += blockDim.x)
+            A.xs2[(size_t)t * nb32 + (b & 3) * (nb32 / 4) + (b >> 2)] = A.xs_in[(size_t)t * nb32 + b];
+    } else {
+        route_quant_pass<XF>(A, t, wave, xr, lane);
+    }
+    if (wave == 0) {
+        const Pick P = route_pick(lv, A.E, A.k, A.scale, rlds);
+        if (lane < A.k) {
+            A.idx[(size_t)t * A.k + lane] = P.idx;
+            A.wt[(size_t)t * A.k + lane] = P.w;
+        }
+    }
+}
+
 template <int TPB>
 static void launch_route_tpb(int nb, hipStream_t s, const RouteArgs &ra) {
     switch (ra.x_fmt) {
@@ -628,6 +665,20 @@ static void launch_route_tpb(int nb, hipStream_t s, const RouteArgs &ra) {
 }
 
 static void launch_route(bool large, int nb, hipStream_t s, const RouteArgs &ra) {
+    if (!ra.counts) {
+        switch (ra.x_fmt) {
+            case Q36MOE_FMT_F32:
+                hipLaunchKernelGGL(k_route_tok<Q36MOE_FMT_F32>, dim3(ra.T), dim3(64 * (kRouteD / 512)), 0, s, ra);
+                break;
+            case Q36MOE_FMT_BF16:
+                hipLaunchKernelGGL(k_route_tok<Q36MOE_FMT_BF16>, dim3(ra.T), dim3(64 * (kRouteD / 512)), 0, s, ra);
+                break;
+            default:
+                hipLaunchKernelGGL(k_route_tok<kFmtE4M3>, dim3(ra.T), dim3(64 * (kRouteD / 512)), 0, s, ra);
+                break;
+        }
+        return;
+    }
     if (large) launch_route_tpb<kRouteTPB>(nb, s, ra);
     else launch_route_tpb<kRouteTPBSmall>(nb, s, ra);
 }
