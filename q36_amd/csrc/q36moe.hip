@@ -620,32 +620,34 @@ __global__ __launch_bounds__(64 * TPB) void k_route(RouteArgs A) {
 }
 
 // k_route without the per-block counts (the one-kernel skinny path sorts
-// itself), one token per workgroup: wave w quantises values 512w .. 512w+511
-// and wave 0 also routes, so each wave has one pass of x in flight instead
-// of four.
+// itself), one token per workgroup: wave w < 4 quantises values 512w ..
+// 512w+511 and wave 4 routes, so the routing chain (logits load, ranking,
+// stores) runs beside the quantisation instead of after a pass of it.
+constexpr int kRouteTokW = kRouteD / 512 + 1;
 template <int XF>
-__global__ __launch_bounds__(64 * (kRouteD / 512)) void k_route_tok(RouteArgs A) {
+__global__ __launch_bounds__(64 * kRouteTokW) void k_route_tok(RouteArgs A) {
     __shared__ __align__(16) uint32_t rlds[kRouteLds];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int t = blockIdx.x;
     constexpr bool preq = XF == kFmtE4M3;
-    X8 xr;
-    if constexpr (!preq) xr = load8_raw(A.x, XF, (size_t)t * A.D + wave * 512 + lane * 8);
-    float lv[4];
-    if (wave == 0) route_load(A.logits + (size_t)t * A.ld, A.E, lv);
-    if constexpr (preq) {
-        const int nb32 = A.D / 32;
-        for (int b = threadIdx.x; b < nb32; b += blockDim.x)
-            A.xs2[(size_t)t * nb32 + (b & 3) * (nb32 / 4) + (b >> 2)] = A.xs_in[(size_t)t * nb32 + b];
-    } else {
-        route_quant_pass<XF>(A, t, wave, xr, lane);
-    }
-    if (wave == 0) {
+    constexpr int RW = kRouteTokW - 1;   // the routing wave
+    if (wave == RW) {
+        float lv[4];
+        route_load(A.logits + (size_t)t * A.ld, A.E, lv);
         const Pick P = route_pick(lv, A.E, A.k, A.scale, rlds);
         if (lane < A.k) {
             A.idx[(size_t)t * A.k + lane] = P.idx;
             A.wt[(size_t)t * A.k + lane] = P.w;
         }
+        return;
+    }
+    if constexpr (preq) {
+        const int nb32 = A.D / 32;
+        for (int b = threadIdx.x; b < nb32; b += 64 * RW)
+            A.xs2[(size_t)t * nb32 + (b & 3) * (nb32 / 4) + (b >> 2)] = A.xs_in[(size_t)t * nb32 + b];
+    } else {
+        const X8 xr = load8_raw(A.x, XF, (size_t)t * A.D + wave * 512 + lane * 8);
+        route_quant_pass<XF>(A, t, wave, xr, lane);
     }
 }
 
@@ -668,13 +670,13 @@ static void launch_route(bool large, int nb, hipStream_t s, const RouteArgs &ra)
     if (!ra.counts) {
         switch (ra.x_fmt) {
             case Q36MOE_FMT_F32:
-                hipLaunchKernelGGL(k_route_tok<Q36MOE_FMT_F32>, dim3(ra.T), dim3(64 * (kRouteD / 512)), 0, s, ra);
+                hipLaunchKernelGGL(k_route_tok<Q36MOE_FMT_F32>, dim3(ra.T), dim3(64 * kRouteTokW), 0, s, ra);
                 break;
             case Q36MOE_FMT_BF16:
-                hipLaunchKernelGGL(k_route_tok<Q36MOE_FMT_BF16>, dim3(ra.T), dim3(64 * (kRouteD / 512)), 0, s, ra);
+                hipLaunchKernelGGL(k_route_tok<Q36MOE_FMT_BF16>, dim3(ra.T), dim3(64 * kRouteTokW), 0, s, ra);
                 break;
             default:
-                hipLaunchKernelGGL(k_route_tok<kFmtE4M3>, dim3(ra.T), dim3(64 * (kRouteD / 512)), 0, s, ra);
+                hipLaunchKernelGGL(k_route_tok<kFmtE4M3>, dim3(ra.T), dim3(64 * kRouteTokW), 0, s, ra);
                 break;
         }
         return;
