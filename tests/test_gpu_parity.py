@@ -515,6 +515,19 @@ def test_forward_bf16_input(dev, oracle, layer_w):
                  path=2)
 
 
+@pytest.mark.parametrize("T,path", [(40, 5), (40, 1), (600, 1)])
+def test_forward_bf16_input_sorted(dev, oracle, layer_w, T, path):
+    """bf16 activations through the routing kernels of the sorted paths (one
+    token per workgroup on the one-kernel skinny path, the per-block counting
+    kernel otherwise), each compiled per input format."""
+    rng = np.random.default_rng(67)
+    x, lg = synth.hidden(rng, T), synth.normal_logits(rng, T)
+    xb = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    sample = None if T <= 64 else list(range(0, T, 37))
+    _check_layer("bf16_in_sorted", dev, oracle, layer_w, xb, lg, None, sample=sample, x_dtype=torch.bfloat16,
+                 path=path)
+
+
 def test_forward_deterministic_and_reusable(dev, layer_w):
     """Two runs give identical bits; a smaller call after a larger one on the
     same context matches a fresh context."""
