@@ -2355,6 +2355,21 @@ struct DirectArgs {
 };
 
 constexpr int kDD = 2048;   // d_model of the instantiated kernels
+
+// Weight loads of the direct kernels: non-temporal while batches are small
+// (each expert's bytes read once), cached from kDirectCachedT tokens, where
+// entries sharing an expert reread its tiles (decode16: 128 entries over ~101
+// experts).  Measured: T = 9 / 10 / 12 / 14 / 16 with cached loads 27.1 /
+// 28.2 / 31.7 / 36.5 / 38.9 us against 26.6 / 28.0 / 31.9 / 36.9 / 39.9
+// non-temporal.
+constexpr int kDirectCachedT = 12;
+// (a template parameter: a per-call select of the two loads measured 0.7 us
+// slower at decode8, where only the non-temporal one runs)
+template <bool CACHED>
+__device__ __forceinline__ u32x4 direct_ld16(const void *p) {
+    if constexpr (CACHED) return *reinterpret_cast<const u32x4 *>(p);
+    else return ldg_nt16(p);
+}
 constexpr int kDF = 512;    // d_ff
 
 // Entry i (token t, slot s; or the shared expert of token t for i >= T*k)
@@ -2453,7 +2468,7 @@ __device__ __forceinline__ void direct_shared_q8(const DirectArgs &A, int t, int
 // weight loads in flight.  Measured (gate/up us, one tile / two): T=2 7.2 /
 // 7.5, T=4 9.8 / 10.0, T=8 16.5 / 15.5, T=16 27.4 / 25.6; four tiles at
 // T=16 25.7.
-template <bool SHQ8 = false, int NFT = 1>
+template <bool SHQ8 = false, int NFT = 1, bool CACHED = false>
 __device__ __forceinline__ void direct_gateup_body(const DirectArgs &A, int i, int ft0,
                                                    DirectGateupLds &L_) {
     static_assert(NFT == 1 || NFT == 2, "row tiles per workgroup");
@@ -2501,8 +2516,8 @@ __device__ __forceinline__ void direct_gateup_body(const DirectArgs &A, int i, i
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const size_t o = ((size_t)(ft0 + u) * (kDD / 128) + wave * 4 + j) * 1024 + (size_t)lane * 16;
-            { const u32x4 t = ldg_nt16(Wg + o); ag[u][j] = make_uint4(t[0], t[1], t[2], t[3]); }
-            { const u32x4 t = ldg_nt16(Wu + o); au[u][j] = make_uint4(t[0], t[1], t[2], t[3]); }
+            { const u32x4 t = direct_ld16<CACHED>(Wg + o); ag[u][j] = make_uint4(t[0], t[1], t[2], t[3]); }
+            { const u32x4 t = direct_ld16<CACHED>(Wu + o); au[u][j] = make_uint4(t[0], t[1], t[2], t[3]); }
         }
         const size_t so = nib + ((size_t)(ft0 + u) * 64 + lane) * (kDD / 128) + wave * 4;
         sag[u] = *reinterpret_cast<const int *>(Wg + so);
@@ -2580,10 +2595,10 @@ __device__ __forceinline__ void direct_gateup_body(const DirectArgs &A, int i, i
     }
 }
 
-template <bool SHQ8, int NFT>
+template <bool SHQ8, int NFT, bool CACHED = false>
 __global__ __launch_bounds__(256) void k_direct_gateup(DirectArgs A) {
     __shared__ DirectGateupLds L_;
-    direct_gateup_body<SHQ8, NFT>(A, blockIdx.x, blockIdx.y * NFT, L_);
+    direct_gateup_body<SHQ8, NFT, CACHED>(A, blockIdx.x, blockIdx.y * NFT, L_);
 }
 
 // Token t x 16 output rows; wave s handles slot s (wave k: shared expert):
@@ -2593,7 +2608,7 @@ __global__ __launch_bounds__(256) void k_direct_gateup(DirectArgs A) {
 // matrix is q8_0-split (the routed slots with dn_q8, the shared expert with
 // sh_q8) quantise h per 32 to int8 with an fp32 scale (k_quant_q8b) and run
 // each 32-block as one int8 MFMA scaled by both scales (k_gemm_expert_i8).
-template <bool Q8>
+template <bool Q8, bool CACHED = false>
 __global__ __launch_bounds__(576) void k_direct_down(DirectArgs A) {
     __shared__ __align__(16) uint8_t sh[kMaxTopK + 1][kDF + 32];
     __shared__ uint8_t shs[kMaxTopK + 1][kDF / 32];
@@ -2643,7 +2658,7 @@ __global__ __launch_bounds__(576) void k_direct_down(DirectArgs A) {
         const size_t nib = (size_t)kDD * kDF / 2;
 #pragma unroll
         for (int j = 0; j < 4; j++)
-            { const u32x4 t = ldg_nt16(W + ((size_t)rt * 4 + j) * 1024 + (size_t)lane * 16); a[j] = make_uint4(t[0], t[1], t[2], t[3]); }
+            { const u32x4 t = direct_ld16<CACHED>(W + ((size_t)rt * 4 + j) * 1024 + (size_t)lane * 16); a[j] = make_uint4(t[0], t[1], t[2], t[3]); }
         sa = *reinterpret_cast<const int *>(W + nib + ((size_t)rt * 64 + lane) * 4);
         quant8_lane(hv, lane, &sh[wave][lane * 8], &shs[wave][lane >> 2]);
         if (rt == 0) {   // quantised h (tap)
@@ -3248,7 +3263,13 @@ static void launch_stage(const Scratch &c, const Plan &P, int st, hipStream_t s)
             // two row tiles per workgroup from kDirect2Tiles tokens on (one
             // routing and twice the loads in flight per workgroup; below
             // that, more workgroups spread a small batch better)
-            if (T >= kDirect2Tiles) {
+            static_assert(kDirectCachedT >= kDirect2Tiles, "cached loads only in the two-tile kernels");
+            if (T >= kDirectCachedT) {
+                if (P.di.sh_q8)
+                    hipLaunchKernelGGL((k_direct_gateup<true, 2, true>), dim3(n, FF / 32), dim3(256), 0, s, P.di);
+                else
+                    hipLaunchKernelGGL((k_direct_gateup<false, 2, true>), dim3(n, FF / 32), dim3(256), 0, s, P.di);
+            } else if (T >= kDirect2Tiles) {
                 if (P.di.sh_q8)
                     hipLaunchKernelGGL((k_direct_gateup<true, 2>), dim3(n, FF / 32), dim3(256), 0, s, P.di);
                 else
@@ -3260,10 +3281,12 @@ static void launch_stage(const Scratch &c, const Plan &P, int st, hipStream_t s)
                     hipLaunchKernelGGL((k_direct_gateup<false, 1>), dim3(n, FF / 16), dim3(256), 0, s, P.di);
             }
         } else if (st == ST_DOWN) {
-            if (P.di.dn_q8 || P.di.sh_q8)
-                hipLaunchKernelGGL(k_direct_down<true>, dim3(D / 16, T), dim3(64 * (K + P.has_sh)), 0, s, P.di);
-            else
-                hipLaunchKernelGGL(k_direct_down<false>, dim3(D / 16, T), dim3(64 * (K + P.has_sh)), 0, s, P.di);
+            const bool q8 = P.di.dn_q8 || P.di.sh_q8, cached = T >= kDirectCachedT;
+            const dim3 g(D / 16, T), b(64 * (K + P.has_sh));
+            if (q8 && cached) hipLaunchKernelGGL((k_direct_down<true, true>), g, b, 0, s, P.di);
+            else if (q8) hipLaunchKernelGGL((k_direct_down<true, false>), g, b, 0, s, P.di);
+            else if (cached) hipLaunchKernelGGL((k_direct_down<false, true>), g, b, 0, s, P.di);
+            else hipLaunchKernelGGL((k_direct_down<false, false>), g, b, 0, s, P.di);
         }
         return;
     }
