@@ -375,7 +375,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; --gpus must be 1 "
-                                   "(expert-parallel sharding is described in DESIGN.md, not run)"}))
+                                   "(expert-parallel sharding over several GPUs is designed, not run)"}))
         sys.exit(2)
     import torch
     from q36_amd import moe
