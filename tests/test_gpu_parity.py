@@ -483,6 +483,15 @@ def test_forward_fat_skewed(dev, oracle, layer_w):
     _check_layer("fat_skewed", dev, oracle, layer_w, x, lg, None, path=1, sample=sample)
 
 
+def test_forward_prefill_past_4096(dev, oracle, layer_w):
+    """T=4500: 282 routing blocks, so each column-scan thread sums 9 blocks
+    (past the 8 it holds in registers) -- the loop form of the scan."""
+    rng = np.random.default_rng(45)
+    x, lg = synth.hidden(rng, 4500), synth.normal_logits(rng, 4500)
+    sample = np.sort(rng.choice(4500, size=32, replace=False))
+    _check_layer("prefill4500", dev, oracle, layer_w, x, lg, None, sample=sample)
+
+
 def test_forward_prefill4096(dev, oracle, layer_w):
     x, lg, _ = synth.config_inputs("prefill4096", 3)
     rng = np.random.default_rng(33)
