@@ -863,11 +863,62 @@ __global__ __launch_bounds__(256) void k_scatter(ScanArgs A) {
     }
     if (b == 0) {
         for (int e = tid; e <= A.E; e += 256) A.e_off[e] = off[e];
-        for (int e = tid; e < A.E; e += 256)
+        // routed tiles in ascending column-tile count (expert order within a
+        // count): the kernels walk the list backwards, so the largest tiles
+        // start first and the small ones fill the tail.  Thread e counts its
+        // expert's tiles per count; each wave scans its 64 experts for all
+        // counts at once (DPP), and the wave totals give the offsets.
+        constexpr int NBK = 10;   // column tiles of the largest (fat) tile
+        static_assert(kMaxExperts <= 256, "one expert per thread");
+        __shared__ int wtot[4][NBK];
+        const int e = tid, lane = tid & 63, wv = tid >> 6;
+        int c[NBK], inc[NBK];
+#pragma unroll
+        for (int k2 = 0; k2 < NBK; k2++) c[k2] = 0;
+        if (e < A.E)
+            for (int j = 0; j < ntile[e]; j++) {
+                const int rows = min(A.tn, tot[e] - j * A.tn);
+                const int k2 = (rows + 15) / 16 - 1;
+#pragma unroll
+                for (int k3 = 0; k3 < NBK; k3++) c[k3] += k3 == k2 ? 1 : 0;
+            }
+#pragma unroll
+        for (int k2 = 0; k2 < NBK; k2++) {
+            int v = c[k2];
+            v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);
+            v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);
+            v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);
+            v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);
+            v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);
+            v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);
+            inc[k2] = v;
+            if (lane == 63) wtot[wv][k2] = v;
+        }
+        __syncthreads();
+        if (e < A.E) {
+            int pos[NBK], base = 0;
+#pragma unroll
+            for (int k2 = 0; k2 < NBK; k2++) {
+                int before = 0, all = 0;
+#pragma unroll
+                for (int w = 0; w < 4; w++) {
+                    before += w < wv ? wtot[w][k2] : 0;
+                    all += wtot[w][k2];
+                }
+                pos[k2] = base + before + inc[k2] - c[k2];
+                base += all;
+            }
             for (int j = 0; j < ntile[e]; j++) {
                 const int p0 = off[e] + j * A.tn;
-                A.tiles[toff[e] + j] = make_int4(e, p0, min(p0 + A.tn, off[e] + tot[e]), 0);
+                const int rows = min(A.tn, tot[e] - j * A.tn);
+                const int k2 = (rows + 15) / 16 - 1;
+                int pp = 0;
+#pragma unroll
+                for (int k3 = 0; k3 < NBK; k3++)
+                    if (k3 == k2) pp = pos[k3]++;
+                A.tiles[pp] = make_int4(e, p0, p0 + rows, 0);
             }
+        }
         const int nsh = A.shg ? (A.T + A.tn_sh - 1) / A.tn_sh : 0;
         for (int j = tid; j < nsh; j += 256) {
             const int p0 = n + j * A.tn_sh;
@@ -975,6 +1026,7 @@ __device__ __forceinline__ v4f mfma_sel(int sel, const v8i &a, const v8i &b, con
 // two rows with the 16-byte slot index XORed by the line index, so the 16
 // lanes of a fragment read hit 16 distinct bank groups.
 constexpr int kGdTok = 160;                      // rows per fat tile (10 column tiles)
+static_assert(kGdTok / 16 <= 10, "k_scatter orders tiles by column-tile count, 1..10");
 
 // Direct-to-LDS loads are issued in their buffer (MUBUF) form, not as
 // global_load_lds: the global form is a FLAT instruction that may access
@@ -1302,10 +1354,12 @@ __global__ __launch_bounds__(256, 2) void k_gateup_dma(GemmArgs A) {
         shared_gateup_q8_body(A, (int)blockIdx.x / kShRb, (int)blockIdx.x % kShRb);
         return;
     }
-    // tiles in reverse list order: the shared expert's tiles, last in the
-    // list and full (kGdTok rows but the last), start first instead of
-    // trailing the routed tiles (mixed: 236.3 -> 232.0 us with the down
-    // kernel reversed as well; no change without a shared expert)
+    // tiles in reverse list order: k_scatter lists the routed tiles in
+    // ascending size and the shared expert's (full) tiles last, so the
+    // largest start first and the smallest fill the tail.  The down kernel
+    // walks the same order.  Reversing alone: mixed 236.3 -> 232.0 us; the
+    // size order on top: prefill4096 206.8 -> 202.8, mixed 222.7 -> 221.0
+    // (another box).
     const int xcd = bid & 7, jx = bid >> 3;
     const int ngrp = (*A.ntiles + 7) >> 3, grp = jx / NRB;
     if (grp >= ngrp) return;
