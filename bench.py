@@ -109,29 +109,31 @@ def make_inputs(cfg_name, T, n, seed, dev):
 
 
 def kernel_bytes(stage, T, U, shared, dn_q8=False, sh_q8=False):
-    """Algorithmic HBM bytes of one launch of a stage.  U = distinct routed
-    experts hit; P = routed (token, slot) rows, plus T shared rows.  A
-    q8_0-split matrix is int8 + f16 per 32; int8 activations carry an fp32
-    scale per 32 (h rows of a q8_0-split down; x of a q8_0-split shared
-    expert, read besides the e4m3 x)."""
+    """(algorithmic, overhead) HBM bytes of one launch of a stage.  U =
+    distinct routed experts hit; P = routed (token, slot) rows, plus T
+    shared rows.  Algorithmic bytes are what the layer must move: the hit
+    experts' weights and the stage's activation input (e4m3 x + E8M0 scales
+    into gate/up, the quantised h rows into the down).  Overhead bytes are
+    this build's own intermediates: h written by gate/up and the staged
+    weighted down rows (f16 + an exponent byte per 16 columns) the combine
+    reads back.  A q8_0-split matrix is int8 + f16 per 32; int8 activations
+    carry an fp32 scale per 32 (h rows of a q8_0-split down; x of a
+    q8_0-split shared expert, read besides the e4m3 x)."""
     P = T * K + (T if shared else 0)
     sh_mat = Q8_MAT_BYTES if sh_q8 else MAT_BYTES
     xq = T * D + T * D // 32 + (T * D + T * D // 8 if sh_q8 else 0)
     hq = T * K * FF + T * K * FF // 32 * (4 if dn_q8 else 1)
     if shared:
         hq += T * FF + T * FF // 32 * (4 if sh_q8 else 1)
+    staged = P * (D * 2 + D // 16)
     if stage == "gateup":
-        # gate+up weights of the hit experts, the activations, h out
-        return U * 2 * MAT_BYTES + (2 * sh_mat if shared else 0) + xq + hq
+        return U * 2 * MAT_BYTES + (2 * sh_mat if shared else 0) + xq, hq
     if stage == "down":
-        # down weights, h in, weighted rows out (f16 + an exponent byte per 16)
         dn = U * (Q8_MAT_BYTES if dn_q8 else MAT_BYTES) + (sh_mat if shared else 0)
-        return dn + hq + P * (D * 2 + D // 16)
+        return dn + hq, staged
     if stage == "expert":
-        # one kernel per skinny tile: gate/up and down weights, x in, h out
-        # (the tap copy; down reads it from LDS), weighted rows out
-        return (U * 3 * MAT_BYTES + (3 * sh_mat if shared else 0) + xq + hq
-                + P * (D * 2 + D // 16))
+        # one kernel per skinny tile: h stays in LDS (the tap copy is written)
+        return U * 3 * MAT_BYTES + (3 * sh_mat if shared else 0) + xq, hq + staged
     raise ValueError(stage)
 
 
@@ -365,9 +367,12 @@ class Bench:
              "stage_us": st_us}
         for st in kernels_of(path):
             us = kernel_us(st_us, st)
-            kf, kb = kernel_flops(st, T, shared), kernel_bytes(st, T, U, shared, dn_q8, sh_q8)
+            kf = kernel_flops(st, T, shared)
+            kb, ko = kernel_bytes(st, T, U, shared, dn_q8, sh_q8)
             r[st] = {"us": us, "mfma_frac": kf / (us * 1e-6) / 1e12 / MFMA_FP8_PEAK_TFS,
-                     "hbm_frac": kb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, "flops": kf, "bytes": kb}
+                     "hbm_frac": kb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, "flops": kf, "bytes": kb,
+                     "overhead_bytes": ko,
+                     "hbm_frac_with_overhead": (kb + ko) / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
         return r
 
 
@@ -475,13 +480,16 @@ def main():
                 "kernel_us": kernel_us(st_us, dom), "flops_per_launch": fl,
                 "layer_mfma_frac": head["layer_mfma_frac"], "layer_hbm_frac": head["layer_hbm_frac"]}
     else:
-        by = kernel_bytes(dom, T, U, shared, dn_q8, sh_q8)
+        by, ovh = kernel_bytes(dom, T, U, shared, dn_q8, sh_q8)
         ach = by / (kernel_us(st_us, dom) * 1e-6) / 1e9
         roof = {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": ach / HBM_PEAK_GBS, "traffic": None, "kernel": dom,
-                "kernel_us": kernel_us(st_us, dom), "bytes_per_launch": by,
+                "kernel_us": kernel_us(st_us, dom), "bytes_per_launch": by, "overhead_bytes_per_launch": ovh,
                 "layer_hbm_frac": head["layer_hbm_frac"], "layer_bytes": head["layer_bytes"]}
     roof["traffic"] = None if host_up else measured_traffic(args.config, dom)
+    if roof["traffic"] is not None:
+        roof["traffic_source"] = ("rocprofv3 FETCH_SIZE + WRITE_SIZE of this kernel and configuration, "
+                                  "scaled by a plain copy's reading (profiles/hbm_traffic.md)")
 
     res = {
         "metric": "MoE layer tokens/s (W4A8, 1 GPU)",

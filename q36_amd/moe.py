@@ -115,15 +115,21 @@ def _dev(t, name, dtype=None):
     return ctypes.c_void_p(t.data_ptr())
 
 
-def _shg(shg):
+def _shg(shg, T):
     """(pointer, element stride) of a [T] f32 GPU tensor of shared-gate
     logits, which may be a strided view such as column 256 of 257-wide
-    router rows; (None, 0) without one."""
+    router rows; (None, 0) without one.  A broadcast view (stride 0) and a
+    length other than T are refused: the kernels read T elements at the
+    stride given."""
     if shg is None:
         return None, 0
     if not isinstance(shg, torch.Tensor) or not shg.is_cuda or shg.dtype != torch.float32 or shg.dim() != 1:
         raise Q36MoEError("shg must be a 1-D float32 GPU tensor")
-    return ctypes.c_void_p(shg.data_ptr()), max(1, shg.stride(0)) if shg.numel() > 1 else 1
+    if shg.shape[0] != T:
+        raise Q36MoEError(f"shg must have T={T} elements, got {shg.shape[0]}")
+    if T > 1 and shg.stride(0) < 1:
+        raise Q36MoEError("shg must have a positive stride (no broadcast views)")
+    return ctypes.c_void_p(shg.data_ptr()), shg.stride(0) if T > 1 else 1
 
 
 def _host_u8(a):
@@ -323,7 +329,7 @@ class MoELayer:
         lp = ctypes.c_void_p(logits.data_ptr()) if T else None
         if T and (not logits.is_cuda or logits.dtype != torch.float32):
             raise Q36MoEError("logits must be a float32 GPU tensor")
-        sp, sld = _shg(shg)
+        sp, sld = _shg(shg, T)
         xp = _dev(x, "x") if T else None
         op = _dev(out, "out") if T else None
         check(lib().q36moe_forward(self._h, weights._h, xp, xf, lp, ld, sp, sld, T, float(scale), op, of),
@@ -344,7 +350,7 @@ class MoELayer:
         if T and (not logits.is_cuda or logits.dtype != torch.float32):
             raise Q36MoEError("logits must be a float32 GPU tensor")
         lp = ctypes.c_void_p(logits.data_ptr()) if T else None
-        sp, sld = _shg(shg)
+        sp, sld = _shg(shg, T)
         qp = _dev(xq, "xq", torch.uint8) if T else None
         sc = _dev(xs, "xs", torch.uint8) if T else None
         op = _dev(out, "out") if T else None
@@ -580,7 +586,7 @@ def forward_noalloc(weights, x, logits, shg=None, top_k=8, scale=1.0, out=None, 
         raise Q36MoEError("logits must be [T, n_expert] with contiguous rows")
     if T and (not logits.is_cuda or logits.dtype != torch.float32):
         raise Q36MoEError("logits must be a float32 GPU tensor")
-    sp, sld = _shg(shg)
+    sp, sld = _shg(shg, T)
     check(lib().q36moe_forward_noalloc(weights._h, _dev(x, "x") if T else None, xf,
                                        ctypes.c_void_p(logits.data_ptr()) if T else None, logits.stride(0),
                                        sp, sld, T, top_k, float(scale), _dev(out, "out") if T else None, of,

@@ -34,6 +34,8 @@ import torch
 
 from q36_amd import moe, synth
 
+import fullcheck
+
 pytestmark = pytest.mark.gpu
 
 TOL = 2e-3
@@ -313,7 +315,10 @@ def _check_h_rows(oracle, w, x, gi, perm, hq, hs, rows, n_expert=256, k=8):
 
 
 def _check_layer(name, dev, oracle, layer_w, x, lg, shg, sample=None, x_dtype=torch.float32,
-                 path=0):
+                 path=0, every_token=False):
+    """Staged parity on the sampled tokens through the C oracle's per-token
+    path; with every_token, also all three stages on every token through the
+    expert-grouped fp64 reference (tests/fullcheck.py)."""
     w, dw = layer_w
     T = x.shape[0]
     layer, y32, y16 = _run_layer(dev, dw, x, lg, shg, x_dtype=x_dtype, path=path)
@@ -394,6 +399,9 @@ def _check_layer(name, dev, oracle, layer_w, x, lg, shg, sample=None, x_dtype=to
     assert flips <= 0.01 * len(rows) * hq.shape[1]
     assert norm_h <= TOL and el_h <= TOL, f"{name}: down/combine error {norm_h:.3g} / {el_h:.3g}"
     assert normwise <= TOL and el <= TOL, f"{name}: end-to-end error {normwise:.3g} / {el:.3g}"
+    if every_token:
+        m = fullcheck.check_every_token(oracle, w, x, lg, shg, y32, gi, pos, hq, hs)
+        _metrics(name + "/every_token", T=int(T), **m)
     return layer
 
 
@@ -410,11 +418,14 @@ def test_forward_decode1(dev, oracle, layer_w, path):
 # Batch sizes between the named configurations, each on a forced path (0 =
 # the automatic choice), with Zipf routing on every other case and the
 # shared expert on some: (T, path, zipf, shared).
-# Path 5 at T=256 has exactly the most routed entries (2048) the one-kernel
-# skinny path discovers its tiles for; at T=300 it takes them from k_scatter.
+# The one-kernel skinny path (path 5) finds its own tiles for up to 4096
+# routed entries (T = 512 at top-8: the case (512, 5) sits on that limit);
+# above it, (600, 5), the tiles come from k_scatter and the kernel writes its
+# rows in sorted order.
 SWEEP = [(3, 2, False, True), (9, 4, True, False), (17, 0, False, False), (31, 1, True, True),
          (48, 5, True, True), (100, 4, False, True), (200, 5, False, False), (256, 5, True, True),
-         (257, 0, True, False), (300, 5, False, True), (1000, 1, False, False), (2049, 0, True, True)]
+         (257, 0, True, False), (300, 5, False, True), (512, 5, True, False), (600, 5, False, True),
+         (1000, 1, False, False), (2049, 0, True, True)]
 
 
 @pytest.mark.parametrize("T,path,zipf,shared", SWEEP, ids=[f"T{c[0]}_p{c[1]}" for c in SWEEP])
@@ -493,17 +504,32 @@ def test_forward_prefill_past_4096(dev, oracle, layer_w):
 
 
 def test_forward_prefill4096(dev, oracle, layer_w):
+    """Every one of the 4,096 tokens through all three stages, plus 48 tokens
+    through the C oracle's per-token path."""
     x, lg, _ = synth.config_inputs("prefill4096", 3)
     rng = np.random.default_rng(33)
     sample = np.sort(rng.choice(4096, size=48, replace=False))
-    _check_layer("prefill4096", dev, oracle, layer_w, x, lg, None, sample=sample)
+    _check_layer("prefill4096", dev, oracle, layer_w, x, lg, None, sample=sample, every_token=True)
 
 
 def test_forward_mixed_shared(dev, oracle, layer_w):
+    """Every one of the 4,006 tokens, shared expert included."""
     x, lg, shg = synth.config_inputs("mixed", 4)
     rng = np.random.default_rng(44)
     sample = np.concatenate([np.arange(6), 6 + np.sort(rng.choice(4000, size=40, replace=False))])
-    _check_layer("mixed", dev, oracle, layer_w, x, lg, shg, sample=sample)
+    _check_layer("mixed", dev, oracle, layer_w, x, lg, shg, sample=sample, every_token=True)
+
+
+@pytest.mark.parametrize("seed", [5001, 5002, 5003])
+def test_forward_mixed_fresh_weights(dev, oracle, seed):
+    """The mixed step names 40 layers of fresh seeded weights: three more
+    weight seeds (with their own shared expert and inputs), every token."""
+    w = synth.expert_weights(seed, shared=True)
+    dw = moe.MoEWeights.upload(w["gate"], w["up"], w["down"], w["sh_gate"], w["sh_up"], w["sh_down"])
+    x, lg, shg = synth.config_inputs("mixed", seed)
+    _check_layer(f"mixed_seed{seed}", dev, oracle, (w, dw), x, lg, shg, sample=np.arange(6),
+                 every_token=True)
+    del dw
 
 
 @pytest.mark.parametrize("path", PATHS)

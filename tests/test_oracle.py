@@ -377,3 +377,66 @@ def test_expert_stages_vs_numpy(oracle):
     hd = rng.standard_normal(64)
     np.testing.assert_allclose(oracle.expert_down(d, hd), _deq_matrix(oracle, d) @ hd, rtol=1e-12,
                                atol=1e-12)
+
+
+# ---------------------------------------------------------------------------
+# the every-token checker of the GPU parity tests (tests/fullcheck.py)
+# ---------------------------------------------------------------------------
+def _fullcheck():
+    import fullcheck   # tests/ is on sys.path under pytest's default import mode
+    return fullcheck
+
+
+@pytest.mark.parametrize("shared", [False, True])
+def test_fullcheck_reference_vs_oracle(oracle, shared):
+    """The expert-grouped fp64 layer equals the C oracle's per-token forward
+    (its own code path: dequant per block, per-token loops)."""
+    from q36_amd import synth
+    fc = _fullcheck()
+    w = synth.expert_weights(31, n_expert=16, d_model=2048, d_ff=512, shared=shared)
+    rng = np.random.default_rng(32)
+    T = 12
+    x = synth.hidden(rng, T)
+    lg = synth.normal_logits(rng, T, 16)
+    shg = rng.standard_normal(T).astype(np.float32) if shared else None
+    got = fc.layer_reference(oracle, w, x, lg, shg, k=4)
+    want = oracle.moe_forward(w, x, lg, shg, k=4)
+    np.testing.assert_allclose(got, want, rtol=1e-9, atol=1e-9 * np.abs(want).max())
+
+
+def test_fullcheck_accepts_oracle_codes_and_rejects_a_wrong_row(oracle):
+    """Fed h codes from the oracle's per-token path (expert_h + quantiser)
+    and the oracle's output, the checker finds no flip and no error; the
+    row's largest code moved by one step (far from a midpoint: the flip
+    allowance is 1e-4 of the block maximum), or 1% taken off a token's
+    output, fails it."""
+    from q36_amd import synth
+    fc = _fullcheck()
+    E, k, T = 16, 4, 10
+    w = synth.expert_weights(33, n_expert=E, d_model=2048, d_ff=512)
+    rng = np.random.default_rng(34)
+    x = synth.hidden(rng, T)
+    lg = synth.normal_logits(rng, T, E)
+    gi, _ = oracle.router_topk(lg, k, n_expert=E)
+    xq, xs = oracle.quant_e4m3(x)
+    xd = oracle.dequant_e4m3(xq, xs)
+    pos = np.arange(T * k, dtype=np.int32)[::-1].copy()      # any bijection of rows
+    hq = np.zeros((T * k, 512), np.uint8)
+    hs = np.zeros((T * k, 16), np.uint8)
+    for t in range(T):
+        for s in range(k):
+            h = oracle.expert_h(w["gate"][gi[t, s]], w["up"][gi[t, s]], xd[t]).astype(np.float32)
+            q, sc = oracle.quant_e4m3(h[None])
+            hq[pos[t * k + s]], hs[pos[t * k + s]] = q[0], sc[0]
+    y = oracle.moe_forward(w, x, lg, k=k).astype(np.float32)
+    m = fc.check_every_token(oracle, w, x, lg, None, y, gi, pos, hq, hs, k=k)
+    assert m["h_flips"] == 0 and m["e2e_max_rel"] < 1e-6
+    bad = hq.copy()
+    col = int(np.argmax(bad[5] & 0x7f))       # the row's largest code: far from any midpoint
+    bad[5, col] ^= 0x01
+    with pytest.raises(AssertionError):
+        fc.check_every_token(oracle, w, x, lg, None, y, gi, pos, bad, hs, k=k)
+    y2 = y.copy()
+    y2[3] -= oracle.moe_forward(w, x[3:4], lg[3:4], k=k)[0].astype(np.float32) * 0.01
+    with pytest.raises(AssertionError):
+        fc.check_every_token(oracle, w, x, lg, None, y2, gi, pos, hq, hs, k=k)
