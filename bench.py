@@ -134,34 +134,24 @@ def kernel_bytes(stage, T, U, shared, dn_q8=False, sh_q8=False):
     if stage == "expert":
         # one kernel per skinny tile: h stays in LDS (the tap copy is written)
         return U * 3 * MAT_BYTES + (3 * sh_mat if shared else 0) + xq, hq + staged
-    if stage == "split":
-        # split decode: gate/up, h and a K-slice of down per workgroup; the
-        # partial down rows (f32, one per entry and 32-row h block) are written
-        return U * 3 * MAT_BYTES + (3 * sh_mat if shared else 0) + xq, hq + P * (FF // 32) * D * 4
-    if stage == "sum":
-        # the partial rows read back, bf16 out
-        return T * D * 2, P * (FF // 32) * D * 4
     raise ValueError(stage)
 
 
 def kernels_of(path):
     """The grouped-GEMM kernels of a path: one per skinny tile on the
-    one-kernel skinny path (3), the expert kernel and the partial-row sum on
-    the split decode (4), else gate/up and down."""
-    return {3: ("expert",), 4: ("split", "sum")}.get(path, ("gateup", "down"))
+    one-kernel skinny path (3), else gate/up and down."""
+    return ("expert",) if path == 3 else ("gateup", "down")
 
 
 def kernel_us(st_us, kernel):
-    """Replay-timed duration of a kernel: the fused skinny kernel and the
-    split decode's expert kernel are the gateup stage's launch, its sum the
-    down stage's."""
-    return st_us[{"expert": "gateup", "split": "gateup", "sum": "down"}.get(kernel, kernel)]
+    """Replay-timed duration of a kernel: the fused skinny kernel is the
+    gateup stage's launch."""
+    return st_us["gateup"] if kernel == "expert" else st_us[kernel]
 
 
 def kernel_flops(stage, T, shared):
     P = T * K + (T if shared else 0)
-    return P * {"gateup": 2 * D * 2 * FF, "down": 2 * FF * D, "expert": 3 * 2 * FF * D,
-                "split": 3 * 2 * FF * D, "sum": 0}[stage]
+    return P * {"gateup": 2 * D * 2 * FF, "down": 2 * FF * D, "expert": 3 * 2 * FF * D}[stage]
 
 
 def measured_traffic(config, stage):
@@ -357,7 +347,7 @@ class Bench:
             torch.cuda.synchronize()
             st_us[st] = 1e3 * e0.elapsed_time(e1) / reps
         # stages without kernels on a path time as the empty-launch floor
-        if path in (1, 4):
+        if path == 1:
             for st in ("route", "scan", "combine"):
                 st_us[st] = 0.0
         if path == 3:             # gate/up and down in one kernel (the gateup stage)
@@ -371,8 +361,7 @@ class Bench:
         by, fl = algorithmic(T, U, shared, dn_q8, sh_q8)
         r = {"tokens": T, "us_per_layer": ms_layer * 1e3, "tokens_per_s": T / (ms_layer * 1e-3),
              "distinct_experts": U,
-             "path": {0: "sorted_fat", 1: "direct", 2: "sorted_skinny", 3: "sorted_fused",
-                      4: "direct_split"}.get(path, path),
+             "path": {0: "sorted_fat", 1: "direct", 2: "sorted_skinny", 3: "sorted_fused"}.get(path, path),
              "layer_bytes": by, "layer_hbm_frac": by / (ms_layer * 1e-3) / 1e9 / HBM_PEAK_GBS,
              "layer_flops": fl, "layer_mfma_frac": fl / (ms_layer * 1e-3) / 1e12 / MFMA_FP8_PEAK_TFS,
              "stage_us": st_us}

@@ -250,16 +250,11 @@ int q36moe_forward_q8(q36moe_ctx *c, const q36moe_weights *w, const uint8_t *xq,
  * applies) and fat tiles above; 1 forces sorted with
  * fat tiles, 4 sorted with skinny tiles as two kernels, 5 sorted with
  * skinny tiles in one kernel per tile (two kernels for an int8 down or
- * shared expert), 2 direct (EINVAL from forward when T > 16), 6 the split
- * decode: one workgroup per (entry, 32-row h block, half of the output
- * rows) runs gate/up, SwiGLU, the h block's quantisation and that block's
- * slice of the down projection, and a second kernel sums each token's
- * slices (T <= 4, every matrix MXFP4; EINVAL from forward otherwise).  Mode
- * 0 takes the split decode for T <= 2 on all-MXFP4 layers.  Mode 3 (a
+ * shared expert), 2 direct (EINVAL from forward when T > 16).  Mode 3 (a
  * one-kernel decode variant, measured slower) no longer exists: EINVAL.
  * last_path: 0 sorted (fat), 1 direct, 2 sorted (skinny, two kernels),
- * 3 sorted (skinny, one kernel per tile), 4 split decode.  With the direct
- * paths (1, 4) the PERM/POS taps are the identity (rows in entry order) and
+ * 3 sorted (skinny, one kernel per tile).  With the
+ * direct path the PERM/POS taps are the identity (rows in entry order) and
  * the EOFF/DNW taps are unavailable. */
 int q36moe_ctx_set_path(q36moe_ctx *c, int mode);
 int q36moe_ctx_last_path(const q36moe_ctx *c);

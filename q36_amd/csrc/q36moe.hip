@@ -57,9 +57,7 @@ constexpr int kRouteTPBSmall = 4;  // tokens per workgroup for small batches (T 
 constexpr int kRouteSmallT = 512;
 constexpr int kRouteD = 2048;     // d_model of k_route (the q36 shape, q36.h:78-84)
 constexpr int kDirectMaxT = 16;    // largest batch routed to the direct (unsorted) path
-constexpr int kDirect2Tiles = 8;
-constexpr int kSplitMaxT = 4;      // split decode (k_split_expert + k_split_sum): largest batch
-constexpr int kSplitAutoT = 2;     // ... and the largest the automatic choice sends there   // direct gate/up: two row tiles per workgroup from this batch on
+constexpr int kDirect2Tiles = 8;   // direct gate/up: two row tiles per workgroup from this batch on
 // Cache policy of weight loads that are read once: non-temporal.  +6% in a
 // stream probe; the one-kernel skinny path at decode32 went 52.7 -> 48.3 us,
 // decode1 10.2 -> 9.8, prefill4096 217 -> 212.5.
@@ -2416,7 +2414,6 @@ struct DirectArgs {
     size_t dn_wstride;                          // bytes per routed down matrix
     int dn_q8;                                  // routed down is q8_0-split
     float *hsf;                                 // int8 h scales (tap, q8_0-split down)
-    float *part;                                // split decode: weighted partial down rows [entries][FF/32][D]
     int sh_q8;                                  // shared expert is q8_0-split
 };
 
@@ -2780,238 +2777,6 @@ __global__ __launch_bounds__(576) void k_direct_down(DirectArgs A) {
     }
 }
 
-
-// ---------------------------------------------------------------------------
-// split decode: gate/up, SwiGLU, h quantisation and a K-slice of the down
-// projection in one workgroup; a second kernel sums the slices
-// ---------------------------------------------------------------------------
-// Workgroup (entry i, h block c = rows 32c..32c+31 of d_ff, output part hp
-// of NH): the 32 gate and up rows of block c against the token's x (K split
-// over the 4 waves, as in k_direct_gateup with two row tiles), SwiGLU and
-// the per-32 quantisation of h block c (the block the down projection's
-// activation quantiser uses, q36_engine.cu:2411-2428), then that block's 32
-// columns of the down matrix for output rows hp*2048/NH.. (the 16-byte
-// chunks of lane group c%4 of the packed tiles), times the routing weight,
-// written as one partial row.  k_split_sum adds a token's partials.  The h
-// handoff between the two projections stays inside the workgroup, so the
-// down weights load in the same latency window as gate/up: one kernel
-// boundary per layer and no down-kernel weight fetch after it.
-//
-// Down MFMA: the 4 lane groups of the A operand carry 4 different row tiles
-// (each lane group's K block is one of them; lane group g = row tile g),
-// and B column n holds h block c in K block n and zeros elsewhere (B's lane
-// group q holds K 16q.. in bytes 0-15 -- block q/2 -- and K 64+16q.. in
-// bytes 16-31 -- block 2+q/2), so column n < 4 of C is row tile n times h:
-// one MFMA gives 64 output rows.
-template <int NH, bool CACHED>
-__global__ __launch_bounds__(256) void k_split_expert(DirectArgs A) {
-    constexpr int RTW = 128 / NH / 4;        // down row tiles per wave
-    constexpr int GW = RTW / 4;              // MFMAs (4-tile groups) per wave
-    static_assert(GW >= 1, "at least one 4-tile group per wave");
-    __shared__ DirectGateupLds L_;
-    __shared__ __align__(16) uint8_t hb[64];   // h codes of block c, then 32 zero bytes
-    __shared__ uint32_t hsb4;                  // its E8M0 byte in all four bytes (op_sel picks any)
-    uint8_t *sx = L_.sx;
-    uint8_t *sxs = L_.sxs;
-    auto &red = L_.red;
-    auto &rlds = L_.rlds;
-    const int i = blockIdx.x, c = blockIdx.y, hp = blockIdx.z;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-    const int nr = A.T * A.k;
-    const bool routed = i < nr;
-    const int t = routed ? i / A.k : i - nr;
-    const int s = routed ? i % A.k : 0;
-
-    const X8 xr = load8_raw(A.x, A.x_fmt, (size_t)t * kDD + wave * 512 + lane * 8);
-    float lv[4];
-    if (routed) route_load(A.logits + (size_t)t * A.ld, A.E, lv);
-    int e = A.E;
-    float wgt = 0.0f;
-    if (routed) e = route_rank(lv, A.E, A.k, rlds[wave], s);
-    else wgt = 1.0f / (1.0f + expf(-A.shg[(size_t)t * A.ld_shg]));
-    const uint8_t *Wg = (e < A.E) ? A.gate + (size_t)e * A.wstride : A.sh_gate;
-    const uint8_t *Wu = (e < A.E) ? A.up + (size_t)e * A.wstride : A.sh_up;
-    const uint8_t *Wd = (e < A.E) ? A.down + (size_t)e * A.dn_wstride : A.sh_down;
-    // gate / up: row tiles 2c, 2c+1, this wave's 4 K-steps
-    const size_t nib = (size_t)kDF * kDD / 2;
-    uint4 ag[2][4], au[2][4];
-    int sag[2], sau[2];
-#pragma unroll
-    for (int u = 0; u < 2; u++) {
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const size_t o = ((size_t)(2 * c + u) * (kDD / 128) + wave * 4 + j) * 1024 + (size_t)lane * 16;
-            { const u32x4 v = direct_ld16<CACHED>(Wg + o); ag[u][j] = make_uint4(v[0], v[1], v[2], v[3]); }
-            { const u32x4 v = direct_ld16<CACHED>(Wu + o); au[u][j] = make_uint4(v[0], v[1], v[2], v[3]); }
-        }
-        const size_t so = nib + ((size_t)(2 * c + u) * 64 + lane) * (kDD / 128) + wave * 4;
-        sag[u] = *reinterpret_cast<const int *>(Wg + so);
-        sau[u] = *reinterpret_cast<const int *>(Wu + so);
-    }
-    // down: row tile mt = hp*128/NH + wave*RTW + 4g + lane/16, lane group c%4
-    // of K tile c/4 (row mt*16 + lane%16, columns 32c..32c+31)
-    const int lr = lane & 15, lg = lane >> 4;
-    uint4 ad[GW];
-    int sad[GW];
-#pragma unroll
-    for (int g = 0; g < GW; g++) {
-        const int mt = hp * (128 / NH) + wave * RTW + 4 * g + lg;
-        const size_t o = ((size_t)mt * (kDF / 128) + (c >> 2)) * 1024 + (size_t)(16 * (c & 3) + lr) * 16;
-        { const u32x4 v = direct_ld16<CACHED>(Wd + o); ad[g] = make_uint4(v[0], v[1], v[2], v[3]); }
-        sad[g] = *reinterpret_cast<const int *>(Wd + (size_t)kDD * kDF / 2 + ((size_t)mt * 64 + 16 * (c & 3) + lr) * 4);
-    }
-    if (routed) {
-        route_sync();
-        wgt = route_weight(rlds[wave], A.k, A.scale, s);
-    }
-    if (A.x_fmt == kFmtE4M3) {
-        *reinterpret_cast<uint2 *>(sx + wave * 512 + lane * 8) = make_uint2(xr.a[0], xr.a[1]);
-        if ((lane & 3) == 0) sxs[wave * 16 + (lane >> 2)] = A.xs_in[(size_t)t * (kDD / 32) + wave * 16 + (lane >> 2)];
-    } else {
-        float xv[8];
-        cvt8(xr, A.x_fmt, xv);
-        quant8_lane(xv, lane, sx + wave * 512 + lane * 8, sxs + wave * 16 + (lane >> 2));
-    }
-    if (threadIdx.x < 8) reinterpret_cast<uint32_t *>(sx + kDD)[threadIdx.x] = 0u;
-    if (threadIdx.x >= 8 && threadIdx.x < 16) reinterpret_cast<uint32_t *>(hb + 32)[threadIdx.x - 8] = 0u;
-    __syncthreads();
-
-    const int q = lane >> 4;
-    const bool col0 = (lane & 15) == 0;
-    v4f cg[2], cu[2];
-#pragma unroll
-    for (int u = 0; u < 2; u++) cg[u] = cu[u] = v4f{0.f, 0.f, 0.f, 0.f};
-    static_for<0, 4>([&](auto J) {
-        constexpr int j = decltype(J)::value;
-        const int kt = wave * 4 + j;
-        const uint8_t *b0p = col0 ? sx + kt * 128 + 16 * q : sx + kDD;
-        const uint8_t *b1p = col0 ? sx + kt * 128 + 64 + 16 * q : sx + kDD + 16;
-        const uint4 b0 = *reinterpret_cast<const uint4 *>(b0p);
-        const uint4 b1 = *reinterpret_cast<const uint4 *>(b1p);
-        const v8i b = v8i{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
-        const int sb = sxs[kt * 4 + q];
-#pragma unroll
-        for (int u = 0; u < 2; u++) {
-            const v8i a0 = v8i{(int)ag[u][j].x, (int)ag[u][j].y, (int)ag[u][j].z, (int)ag[u][j].w, 0, 0, 0, 0};
-            const v8i a1 = v8i{(int)au[u][j].x, (int)au[u][j].y, (int)au[u][j].z, (int)au[u][j].w, 0, 0, 0, 0};
-            cg[u] = mfma_f4xf8<j>(a0, b, cg[u], sag[u], sb);
-            cu[u] = mfma_f4xf8<j>(a1, b, cu[u], sau[u], sb);
-        }
-    });
-    if (col0) {
-#pragma unroll
-        for (int u = 0; u < 2; u++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                red[wave][0][16 * u + 4 * q + r] = cg[u][r];
-                red[wave][1][16 * u + 4 * q + r] = cu[u][r];
-            }
-    }
-    __syncthreads();
-    // h block c: SwiGLU of the wave-ordered sums, per-32 E8M0 + e4m3
-    if (wave == 0) {
-        const int l = lane & 31;
-        const float g = red[0][0][l] + red[1][0][l] + red[2][0][l] + red[3][0][l];
-        const float u = red[0][1][l] + red[1][1][l] + red[2][1][l] + red[3][1][l];
-        const float h = silu(g) * u;
-        float amax = fabsf(h);
-#pragma unroll
-        for (int o = 16; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
-        const int e2 = quant_exp(amax);
-        const uint32_t code = e4m3x4(h * inv_scale(e2), 0.0f, 0.0f, 0.0f) & 0xffu;
-        if (lane < 32) {
-            hb[lane] = (uint8_t)code;
-            if (hp == 0) A.hq[(size_t)i * kDF + 32 * c + lane] = (uint8_t)code;   // tap
-        }
-        if (lane == 0) {
-            hsb4 = (uint32_t)(127 + e2) * 0x01010101u;
-            if (hp == 0) A.hs[(size_t)i * (kDF / 32) + c] = (uint8_t)(127 + e2);
-        }
-    }
-    __syncthreads();
-    // B: column n < 4 holds h block c in K block n (bytes 0-15 of lane group
-    // q are K block q/2, bytes 16-31 K block 2 + q/2), zeros elsewhere
-    const int n = lane & 15;
-    const uint8_t *p0 = ((q >> 1) == n) ? hb + 16 * (q & 1) : hb + 32;
-    const uint8_t *p1 = ((q >> 1) + 2 == n) ? hb + 16 * (q & 1) : hb + 32;
-    const uint4 b0 = *reinterpret_cast<const uint4 *>(p0);
-    const uint4 b1 = *reinterpret_cast<const uint4 *>(p1);
-    const v8i bh = v8i{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
-    const int sbh = (int)hsb4;
-    const int ksel = __builtin_amdgcn_readfirstlane(c >> 2);   // uniform: scalar branch in mfma_sel
-    float *dst = A.part + ((size_t)i * (kDF / 32) + c) * kDD;
-#pragma unroll
-    for (int g = 0; g < GW; g++) {
-        const v8i av = v8i{(int)ad[g].x, (int)ad[g].y, (int)ad[g].z, (int)ad[g].w, 0, 0, 0, 0};
-        const v4f r = mfma_sel(ksel, av, bh, v4f{0.f, 0.f, 0.f, 0.f}, sad[g], sbh);
-        // lane (n, q), n < 4: rows 4q..4q+3 of row tile 4g + n
-        if (n < 4) {
-            const int mt = hp * (128 / NH) + wave * RTW + 4 * g + n;
-            *reinterpret_cast<float4 *>(dst + mt * 16 + 4 * q) =
-                make_float4(r[0] * wgt, r[1] * wgt, r[2] * wgt, r[3] * wgt);
-        }
-    }
-    if (c == 0 && hp == 0) {
-        if (threadIdx.x == 0 && routed) {
-            A.idx[i] = e;
-            A.wt[i] = wgt;
-            A.pos[i] = i;
-            A.perm[i] = i;
-        }
-        if (routed && s == 0) {    // quantised x of token t (tap)
-            for (int cc = threadIdx.x; cc < kDD / 16; cc += 256)
-                *reinterpret_cast<uint4 *>(A.xq + (size_t)t * kDD + cc * 16) =
-                    *reinterpret_cast<const uint4 *>(sx + cc * 16);
-            if (threadIdx.x < kDD / 32) A.xs[(size_t)t * (kDD / 32) + threadIdx.x] = sxs[threadIdx.x];
-        }
-    }
-}
-
-// Output rows 16b..16b+15 of token t: the sum of its entries' partial rows.
-// Term j = slot * 16 + c (slots in order, then the shared expert's entry;
-// c the h block).  Wave w takes rows 16b + 4w..+3; lane l loads terms l,
-// l + 64 and l + 128 (one 16-byte load each, all issued at once), adds them
-// in that order, and the 64 lane sums meet in a fixed butterfly: the same
-// order on every call, so results are deterministic.  The reference adds
-// the slots' full down rows in slot order (k_moe_combine,
-// q36_engine.cu:784-791); the difference is rounding only.
-__device__ __forceinline__ float xor_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
-
-__global__ __launch_bounds__(256) void k_split_sum(DirectArgs A, int has_sh) {
-    const int b = blockIdx.x, t = blockIdx.y;
-    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
-    const int nterm = (A.k + has_sh) * (kDF / 32);
-    const int nr = A.T * A.k;
-    float4 v[3];
-#pragma unroll
-    for (int u = 0; u < 3; u++) {
-        const int term = min(l + 64 * u, nterm - 1);
-        const int slot = term / (kDF / 32), c = term % (kDF / 32);
-        const int i = slot < A.k ? t * A.k + slot : nr + t;
-        v[u] = *reinterpret_cast<const float4 *>(A.part + ((size_t)i * (kDF / 32) + c) * kDD + b * 16 + 4 * w);
-    }
-    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-    for (int u = 0; u < 3; u++) {
-        if (l + 64 * u < nterm) { a.x += v[u].x; a.y += v[u].y; a.z += v[u].z; a.w += v[u].w; }
-    }
-    a.x = xor_sum(a.x); a.y = xor_sum(a.y); a.z = xor_sum(a.z); a.w = xor_sum(a.w);
-    if (l == 0) {
-        const size_t o = (size_t)t * kDD + b * 16 + 4 * w;
-        if (A.out_fmt == Q36MOE_FMT_F32) {
-            *reinterpret_cast<float4 *>(static_cast<float *>(A.out) + o) = a;
-        } else {
-            const uint32_t lo = f32_to_bf16(a.x) | (f32_to_bf16(a.y) << 16);
-            const uint32_t hi = f32_to_bf16(a.z) | (f32_to_bf16(a.w) << 16);
-            *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(A.out) + o) = make_uint2(lo, hi);
-        }
-    }
-}
-
 // ---------------------------------------------------------------------------
 // combine
 // ---------------------------------------------------------------------------
@@ -3158,7 +2923,6 @@ struct q36moe_weights {
 // a stage can be replayed over other weight sets (q36moe_ctx_replay).
 struct Plan {
     int T, has_sh, direct, skinny, fused, tiles, nb;
-    int split;                      // direct path as k_split_expert + k_split_sum
     RouteArgs ra;
     ScanArgs sa;
     GemmArgs ga, da;
@@ -3184,9 +2948,6 @@ struct Scratch {
     int8_t *xq8; float *xsf;        // int8 x + fp32 scales (q8_0-split shared expert, sorted path)
     uint16_t *dnh; uint8_t *dne;    // staged weighted down rows: f16 [rows][D] + exponent per 16 columns
     float *hf;                      // direct path: fp32 SwiGLU rows
-    float *part;                    // split decode: partial down rows [entries][FF/32][D] (aliases dnh/dne:
-                                    // the sorted and direct paths never run in one forward)
-    int split_max_T;                // tokens the part buffer holds
 };
 
 struct q36moe_ctx {
@@ -3280,12 +3041,7 @@ size_t carve_scratch(uint8_t *base, int max_T, int E, int D, int FF, int K, Scra
     const size_t o_hq = take(rows * FF), o_hs = take(rows * FF / 32), o_hs2 = take(rows * FF / 32);
     const size_t o_hsf = take(rows * FF / 32 * 4);
     const size_t o_xq8 = take((size_t)max_T * D), o_xsf = take((size_t)max_T * D / 32 * 4);
-    // the split decode's partial rows share the sorted path's staging
-    c.split_max_T = max_T < kSplitMaxT ? max_T : kSplitMaxT;
-    const size_t part_bytes = (size_t)c.split_max_T * (K + 1) * (FF / 32) * D * 4;
-    const size_t stage_bytes = align256(rows * D * 2) + rows * D / 16;
-    const size_t o_dnh = take(stage_bytes > part_bytes ? stage_bytes : part_bytes);
-    const size_t o_dne = o_dnh + align256(rows * D * 2);
+    const size_t o_dnh = take(rows * D * 2), o_dne = take(rows * D / 16);
     const size_t direct_rows = (size_t)(max_T < kDirectMaxT ? max_T : kDirectMaxT) * (K + 1);
     const size_t o_hf = take(direct_rows * FF * 4);
     if (!base) return off;
@@ -3311,7 +3067,6 @@ size_t carve_scratch(uint8_t *base, int max_T, int E, int D, int FF, int K, Scra
     c.dnh = reinterpret_cast<uint16_t *>(b + o_dnh);
     c.dne = b + o_dne;
     c.hf = reinterpret_cast<float *>(b + o_hf);
-    c.part = reinterpret_cast<float *>(b + o_dnh);
     return off;
 }
 
@@ -3563,26 +3318,8 @@ static void bind_weights(Plan &P, const q36moe_weights *w) {
 // Launches the kernels of one stage (direct path: ST_GATEUP is the routing +
 // gate/up kernel, ST_DOWN the down + combine kernel; its other stages are
 // empty).
-// output parts per entry of the split decode (temporary override for measurement)
-static int split_nh() {
-    static const int nh = [] { const char *e = getenv("Q36_SPLIT_NH"); return e ? atoi(e) : 2; }();
-    return nh;
-}
-
 static void launch_stage(const Scratch &c, const Plan &P, int st, hipStream_t s) {
     const int T = P.T, K = c.K, D = c.D, FF = c.FF;
-    if (P.direct && P.split) {
-        const int n = T * K + (P.has_sh ? T : 0);
-        if (st == ST_GATEUP) {
-            const int nh = split_nh();
-            if (nh == 1) hipLaunchKernelGGL((k_split_expert<1, false>), dim3(n, FF / 32, 1), dim3(256), 0, s, P.di);
-            else if (nh == 4) hipLaunchKernelGGL((k_split_expert<4, false>), dim3(n, FF / 32, 4), dim3(256), 0, s, P.di);
-            else hipLaunchKernelGGL((k_split_expert<2, false>), dim3(n, FF / 32, 2), dim3(256), 0, s, P.di);
-        } else if (st == ST_DOWN) {
-            hipLaunchKernelGGL(k_split_sum, dim3(D / 16, T), dim3(256), 0, s, P.di, P.has_sh);
-        }
-        return;
-    }
     if (P.direct) {
         const int n = T * K + (P.has_sh ? T : 0);
         if (st == ST_GATEUP) {
@@ -3697,9 +3434,8 @@ static int launch_forward(const Scratch &c, Plan &P, int pm, const q36moe_weight
     const int tpb = T <= kRouteSmallT ? kRouteTPBSmall : kRouteTPB;
     const int nb = (T + tpb - 1) / tpb;
 
-    const bool direct = pm == 2 ? (T <= kDirectMaxT) : pm == 6 ? (T <= kSplitMaxT)
-                      : (pm == 1 || pm == 4 || pm == 5) ? false : (T <= kDirectMaxT);
-    if ((pm == 2 || pm == 6) && !direct) return Q36MOE_EINVAL;
+    const bool direct = pm == 2 ? (T <= kDirectMaxT) : (pm == 1 || pm == 4 || pm == 5) ? false : (T <= kDirectMaxT);
+    if (pm == 2 && !direct) return Q36MOE_EINVAL;
     const bool shq8 = has_sh && w->sh_q8;
     // a q8_0-split shared expert quantises x itself (int8 + fp32 per 32):
     // pre-quantised e4m3 input cannot feed it
@@ -3721,18 +3457,14 @@ static int launch_forward(const Scratch &c, Plan &P, int pm, const q36moe_weight
     int tiles = n / tn + (n < E ? n : E) + (has_sh ? (T + tn_sh - 1) / tn_sh : 0);
     tiles = (tiles + 7) & ~7;   // whole groups of 8 for the XCD-major tile order
 
-    // split decode: every matrix MXFP4, a batch its partial rows fit
-    const bool splittable = !w->dn_q8 && !shq8 && T <= c.split_max_T;
-    if (pm == 6 && !splittable) return Q36MOE_EINVAL;
-    const bool split = direct && splittable && (pm == 6 || (pm == 0 && T <= kSplitAutoT));
     P = Plan{};
-    P.T = T; P.has_sh = has_sh; P.direct = direct; P.skinny = skinny; P.fused = fused; P.split = split;
+    P.T = T; P.has_sh = has_sh; P.direct = direct; P.skinny = skinny; P.fused = fused;
     P.tiles = tiles; P.nb = nb; P.out = out; P.out_fmt = out_fmt;
     if (direct) {
         P.di = DirectArgs{logits, ld_logits, T, E, K, scale, x, x_fmt, shg, ld_shg,
                           nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0,
                           c.topk_idx, c.topk_w, c.pos, c.perm, c.xq, c.xs, c.hf,
-                          c.hq, c.hs, out, out_fmt, xs_in, 0, 0, c.hsf, c.part};
+                          c.hq, c.hs, out, out_fmt, xs_in, 0, 0, c.hsf};
     } else {
         P.ra = RouteArgs{logits, ld_logits, T, E, K, scale, x, x_fmt, D, nb,
                          c.topk_idx, c.topk_w, c.xq, c.xs, c.xs2, c.blk_cnt, c.rank, xs_in, nullptr, nullptr, 1};
@@ -3791,7 +3523,7 @@ static int forward_impl(q36moe_ctx *c, const q36moe_weights *w, const void *x, i
     *c->plan = P;
     c->last_T = T;
     c->last_sh = P.has_sh;
-    c->last_path = P.direct ? (P.split ? 4 : 1) : P.fused ? 3 : P.skinny ? 2 : 0;
+    c->last_path = P.direct ? 1 : P.fused ? 3 : P.skinny ? 2 : 0;
     // the sorted path reads pre-quantised codes in place; the direct path
     // copies every token's codes into the context
     const bool in_place = !P.direct && x_fmt == kFmtE4M3;
@@ -3934,7 +3666,7 @@ int q36moe_ctx_copy_tap(q36moe_ctx *c, int tap, void *dst, size_t bytes, size_t 
 }
 
 int q36moe_ctx_set_path(q36moe_ctx *c, int mode) {
-    if (!c || mode < 0 || mode > 6 || mode == 3) return Q36MOE_EINVAL;
+    if (!c || mode < 0 || mode > 5 || mode == 3) return Q36MOE_EINVAL;
     c->path_mode = mode;
     return Q36MOE_OK;
 }

@@ -384,21 +384,18 @@ class MoELayer:
     PATH_AUTO, PATH_SORTED, PATH_DIRECT, PATH_SORTED_SKINNY, PATH_SORTED_FUSED = 0, 1, 2, 4, 5
 
     def set_path(self, mode):
-        """0 auto (the split decode for T <= 2 on all-MXFP4 layers, direct
-        for T <= 16, skinny tiles while T*k <= 8*n_expert -- 16*n_expert in
-        one kernel per tile for MXFP4 layers),
+        """0 auto (direct for T <= 16, skinny tiles while T*k <= 8*n_expert --
+        16*n_expert in one kernel per tile for MXFP4 layers),
         1 sorted (fat tiles), 2 direct, 4 sorted (skinny tiles, gate/up and
         down as two kernels), 5 sorted (skinny tiles, one kernel per tile;
-        layers with an int8 down or shared expert take 4), 6 the split
-        decode (T <= 4, every matrix MXFP4; EINVAL otherwise); 3 is refused
+        layers with an int8 down or shared expert take 4); 3 is refused
         (EINVAL)."""
         check(lib().q36moe_ctx_set_path(self._h, mode), "q36moe_ctx_set_path")
 
     @property
     def last_path(self):
         """0 sorted (fat tiles), 1 direct, 2 sorted (skinny tiles, two
-        kernels), 3 sorted (skinny tiles, one kernel per tile), 4 the split
-        decode."""
+        kernels), 3 sorted (skinny tiles, one kernel per tile)."""
         return lib().q36moe_ctx_last_path(self._h)
 
     def check(self):

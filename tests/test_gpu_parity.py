@@ -322,7 +322,7 @@ def _check_layer(name, dev, oracle, layer_w, x, lg, shg, sample=None, x_dtype=to
     w, dw = layer_w
     T = x.shape[0]
     layer, y32, y16 = _run_layer(dev, dw, x, lg, shg, x_dtype=x_dtype, path=path)
-    name = f"{name}/{({1: 'direct', 2: 'sorted_skinny', 3: 'sorted_fused', 4: 'direct_split'}).get(layer.last_path, 'sorted')}"
+    name = f"{name}/{({1: 'direct', 2: 'sorted_skinny', 3: 'sorted_fused'}).get(layer.last_path, 'sorted')}"
     gi = _check_routing(layer, oracle, lg)
     oq, os_ = oracle.quant_e4m3(x)
     np.testing.assert_array_equal(layer.tap(moe.TAP_XQ).cpu().numpy(), oq)
@@ -407,12 +407,9 @@ def _check_layer(name, dev, oracle, layer_w, x, lg, shg, sample=None, x_dtype=to
 
 PATHS = [pytest.param(1, id="sorted"), pytest.param(4, id="sorted_skinny"),
          pytest.param(5, id="sorted_fused"), pytest.param(2, id="direct")]
-# the split decode (mode 6: k_split_expert + k_split_sum) serves T <= 4
-SPLIT_MAX_T = 4
-PATHS_T1 = PATHS + [pytest.param(6, id="direct_split")]
 
 
-@pytest.mark.parametrize("path", PATHS_T1)
+@pytest.mark.parametrize("path", PATHS)
 def test_forward_decode1(dev, oracle, layer_w, path):
     x, lg, _ = synth.config_inputs("decode1", 1)
     _check_layer("decode1", dev, oracle, layer_w, x, lg, None, path=path)
@@ -441,11 +438,9 @@ def test_forward_batch_sweep(dev, oracle, layer_w, T, path, zipf, shared):
     _check_layer(f"sweep{T}", dev, oracle, layer_w, x, lg, shg, sample=sample, path=path)
 
 
-@pytest.mark.parametrize("path", PATHS_T1)
-@pytest.mark.parametrize("T", [2, 4, 7, 16])
+@pytest.mark.parametrize("path", PATHS)
+@pytest.mark.parametrize("T", [2, 7, 16])
 def test_forward_small_batches(dev, oracle, layer_w, T, path):
-    if path == 6 and T > SPLIT_MAX_T:
-        pytest.skip("the split decode serves T <= 4 (EINVAL above: test_split_refuses_large_batches)")
     rng = np.random.default_rng(300 + T)
     x, lg = synth.hidden(rng, T), synth.normal_logits(rng, T)
     _check_layer(f"small{T}", dev, oracle, layer_w, x, lg, None, path=path)
@@ -466,7 +461,7 @@ def test_direct_equals_sorted_inputs(dev, layer_w, T):
     rng = np.random.default_rng(900 + T)
     x, lg = synth.hidden(rng, T), synth.normal_logits(rng, T)
     outs, taps = [], []
-    for path in (1, 2, 4, 5) + ((6,) if T <= SPLIT_MAX_T else ()):
+    for path in (1, 2, 4, 5):
         layer, y32, _ = _run_layer(dev, dw, x, lg, None, path=path)
         outs.append(y32)
         taps.append([layer.tap(m).cpu().numpy() for m in (moe.TAP_TOPK_IDX, moe.TAP_TOPK_W,
@@ -543,26 +538,6 @@ def test_forward_shared_small(dev, oracle, layer_w, path):
     x, lg = synth.hidden(rng, 5), synth.normal_logits(rng, 5)
     shg = rng.standard_normal(5).astype(np.float32)
     _check_layer("shared5", dev, oracle, layer_w, x, lg, shg, path=path)
-
-
-@pytest.mark.parametrize("T", [1, 3])
-def test_forward_shared_split(dev, oracle, layer_w, T):
-    """The split decode with the shared expert: its entry's partial rows are
-    the last terms of each token's sum."""
-    rng = np.random.default_rng(56 + T)
-    x, lg = synth.hidden(rng, T), synth.normal_logits(rng, T)
-    shg = rng.standard_normal(T).astype(np.float32)
-    _check_layer("shared_split", dev, oracle, layer_w, x, lg, shg, path=6)
-
-
-def test_split_refuses_large_batches(dev, layer_w):
-    _, dw = layer_w
-    rng = np.random.default_rng(57)
-    x, lg = synth.hidden(rng, SPLIT_MAX_T + 1), synth.normal_logits(rng, SPLIT_MAX_T + 1)
-    layer = moe.MoELayer(16)
-    layer.set_path(6)
-    with pytest.raises(moe.Q36MoEError):
-        layer.forward(dw, torch.from_numpy(x).to(dev), torch.from_numpy(lg).to(dev))
 
 
 def test_forward_bf16_input(dev, oracle, layer_w):
@@ -751,7 +726,7 @@ def test_forward_64_experts_top4(dev, oracle, layer_w64, T):
         layer.check()
         seen.add(layer.last_path)
         np.testing.assert_array_equal(layer.tap(moe.TAP_TOPK_IDX).cpu().numpy(), oi)
-        if layer.last_path not in (1, 4):   # sorted paths
+        if layer.last_path != 1:
             np.testing.assert_array_equal(layer.tap(moe.TAP_EOFF).cpu().numpy(), off)
             np.testing.assert_array_equal(layer.tap(moe.TAP_PERM).cpu().numpy(), perm)
             np.testing.assert_array_equal(layer.tap(moe.TAP_POS).cpu().numpy(), pos)
