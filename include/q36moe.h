@@ -324,6 +324,13 @@ int q36moe_router_from_gguf(const q36moe_gguf *g, int layer, float *dst, size_t 
 int q36moe_probe_mfma(const void *a, const void *b, const uint32_t *sa,
                       const uint32_t *sb, int fmt_a, int fmt_b, float *c, void *stream);
 
+/* One v_mfma_scale_f32_32x32x64_f8f6f4 with A e2m1 and B e4m3 on
+ * caller-packed operands (the 32x32 tile the fat gate/up uses): a, b: 64
+ * lanes x 32 bytes; sa, sb: 64 lane scale dwords (byte 0 used); c: 64 x 16
+ * floats.  Calibration harness, like q36moe_probe_mfma. */
+int q36moe_probe_mfma32(const void *a, const void *b, const uint32_t *sa, const uint32_t *sb, float *c,
+                        void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -81,6 +81,7 @@ def lib():
     L.q36moe_stage_name.restype = ctypes.c_char_p
     L.q36moe_num_stages.argtypes = []
     L.q36moe_probe_mfma.argtypes = [vp, vp, vp, vp, i, i, vp, vp]
+    L.q36moe_probe_mfma32.argtypes = [vp, vp, vp, vp, vp, vp]
     L.q36moe_ctx_replay.argtypes = [vp, vp, i]
     u32p, u64p = ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_uint64)
     L.q36moe_gguf_open.argtypes = [ctypes.c_char_p, pp]
@@ -564,6 +565,15 @@ def probe_mfma(a, b, sa, sb, fmt_a, fmt_b):
     check(lib().q36moe_probe_mfma(_dev(a, "a"), _dev(b, "b"), _dev(sa, "sa"), _dev(sb, "sb"),
                                   fmt_a, fmt_b, ctypes.c_void_p(c.data_ptr()), _stream()),
           "q36moe_probe_mfma")
+    return c
+
+
+def probe_mfma32(a, b, sa, sb):
+    """One scaled 32x32x64 MFMA (A e2m1, B e4m3): a, b uint8 [64, 32]; sa, sb
+    int32/uint32 [64] -> [64, 16] lane results."""
+    c = torch.empty((64, 16), dtype=torch.float32, device=a.device)
+    check(lib().q36moe_probe_mfma32(_dev(a, "a"), _dev(b, "b"), _dev(sa, "sa"), _dev(sb, "sb"),
+                                    ctypes.c_void_p(c.data_ptr()), _stream()), "q36moe_probe_mfma32")
     return c
 
 

@@ -139,6 +139,55 @@ def test_mfma_probe_layout(dev, fmt_a, spread):
     assert err < 2e-4, err
 
 
+def _interp32(a_lane, sa, b_lane, sb, tab):
+    """Logical A [32][64] (e2m1) and B [64][32] (e4m3) of the 32x32x64 scaled
+    MFMA from lane bytes, gfx950 layout: A lane L holds row L%32, K
+    32(L/32)..+31 (nibble j -> K 32(L/32)+j); B lane L holds column L%32,
+    bytes 0-15 K 16(L/32)..+15 and bytes 16-31 K 32+16(L/32)..+15; K block kb
+    (32 K) is scaled by lane row/col + 32kb."""
+    A = np.zeros((32, 64))
+    B = np.zeros((64, 32))
+    for L in range(64):
+        h = L // 32
+        for j in range(32):
+            byte = a_lane[L, j // 2]
+            A[L % 32, 32 * h + j] = E2M1[(byte >> 4) if (j & 1) else (byte & 15)]
+            k = 16 * h + j if j < 16 else 32 + 16 * h + j - 16
+            B[k, L % 32] = tab[b_lane[L, j]]
+    for kb in range(2):
+        A[:, 32 * kb:32 * kb + 32] *= (2.0 ** (np.int64(sa[32 * kb:32 * kb + 32] & 255) - 127))[:, None]
+        B[32 * kb:32 * kb + 32, :] *= (2.0 ** (np.int64(sb[32 * kb:32 * kb + 32] & 255) - 127))[None, :]
+    return A, B
+
+
+@pytest.mark.parametrize("spread", [True, False])
+def test_mfma32_probe_layout(dev, spread):
+    """Calibrates v_mfma_scale_f32_32x32x64_f8f6f4 (A e2m1, B e4m3), the tile
+    of the fat gate/up: operand, scale and output layout (C lane L holds
+    column L%32, result i is row 8(i/4) + 4(L/32) + i%4)."""
+    rng = np.random.default_rng(200 + spread)
+    tab = _e4m3_table()
+    codes = rng.integers(0, 16, size=(64, 32)).astype(np.uint8)
+    a_lane = np.zeros((64, 32), dtype=np.uint8)
+    a_lane[:, :16] = codes[:, 0::2] | (codes[:, 1::2] << 4)
+    b_lane = _rand_fp8(rng, (64, 32))
+    hi = lambda: rng.integers(0, 1 << 24, size=64).astype(np.uint32) << 8
+    lo, hi_e = (120, 135) if spread else (127, 128)
+    sa = rng.integers(lo, hi_e, size=64).astype(np.uint32) | hi()
+    sb = rng.integers(lo, hi_e, size=64).astype(np.uint32) | hi()
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+    got = moe.probe_mfma32(t(a_lane), t(b_lane), t(sa.view(np.int32)), t(sb.view(np.int32))).double().cpu().numpy()
+    A, B = _interp32(a_lane, sa, b_lane, sb, tab)
+    C = A @ B
+    want = np.array([[C[8 * (i // 4) + 4 * (L // 32) + i % 4, L % 32] for i in range(16)] for L in range(64)])
+    err = np.abs(got - want).max() / np.abs(want).max()
+    _metrics("mfma32_probe", spread=spread, err=float(err))
+    # a wrong layout gives O(1) errors; the MFMA's own accumulation of
+    # full-range e4m3 products read up to 1.2e-4 of max|C| over six random
+    # probes on gfx950, so the bar is 5e-4
+    assert err < 5e-4, err
+
+
 # ---------------------------------------------------------------------------
 # stage entry points
 # ---------------------------------------------------------------------------
