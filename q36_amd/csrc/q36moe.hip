@@ -1239,212 +1239,6 @@ __device__ __forceinline__ void body(const GemmArgs &A, Lds &L, const uint8_t *W
 }  // namespace gdma
 
 // ---------------------------------------------------------------------------
-// fat gate/up on the 32x32x64 scaled MFMA
-// ---------------------------------------------------------------------------
-// Same workgroup, staging pipeline and LDS layout as gdma::body; the MFMA is
-// v_mfma_scale_f32_32x32x64_f8f6f4 (twice the work per instruction).  Its
-// 32 A rows are 16 gate rows (rows 0-15) and the same 16 up rows (16-31):
-// the result then holds gate row r and up row r in one lane (results i and
-// i + 8), so SwiGLU needs no exchange.  Operand layout (gfx950, calibrated
-// by q36moe_probe_mfma32): A lane L = row L%32, K 32(L/32)..+31 of the
-// 64-K half step; B lane L = column L%32, bytes 0-15 K 16(L/32)..+15, bytes
-// 16-31 K 32+16(L/32)..+15; K block kb is scaled by lane row/col + 32kb; C
-// lane L = column L%32, result i = row 8(i/4) + 4(L/32) + i%4.  In the staged
-// 16x16x128 fragment tiles (lane' = row + 16 * K block), lane L of half step
-// s reads lane' = L%16 + 16(2s + L/32) of the gate (L%32 < 16) or up tile.
-// Waves: a 2 x 2 grid, wave (wa, wt) = gate/up tile pairs 2wa, 2wa+1 against
-// 32-column tiles wt + 2j.  The tile's NT 32-column tiles need 4*NT groups
-// of 8 x rows staged: NT per wave (wave w stages groups w + 4i).
-typedef float v16f __attribute__((ext_vector_type(16)));
-
-template <int SEL>
-__device__ __forceinline__ v16f mfma32_f4xf8(const v8i &a, const v8i &b, const v16f &c, int sa, int sb) {
-    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 4, 0, SEL, sa, SEL, sb);
-}
-
-namespace gdma32 {
-using gdma::Lds;
-using gdma::RT;
-using gdma::W;
-using gdma::STA;
-
-template <int NT, int NJ>
-__device__ __forceinline__ void body(const GemmArgs &A, Lds &L, const uint8_t *Wg, const uint8_t *Wu,
-                                     int mt0, int p0, int p1, bool hq8) {
-    constexpr int KD = 2048, NKT = KD / 128;
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wa = wave & 1, wt = wave >> 1;
-    const int ntok = p1 - p0;
-    const int h = lane >> 5, c32 = lane & 31;
-    const uint32_t aoff = (uint32_t)(mt0 + wave) * NKT * 1024 + lane * 16;
-    uint32_t boff[NT];
-#pragma unroll
-    for (int i = 0; i < NT; i++) {
-        const int m = 4 * (wave + W * i) + (lane >> 4);
-        const int s = (lane & 15) ^ (m & 7);
-        const int r = min(2 * m + (s >> 3), ntok - 1);
-        boff[i] = (uint32_t)A.row_tok[p0 + r] * KD + (s & 7) * 16;
-    }
-    const __amdgpu_buffer_rsrc_t rg = dma_src(Wg), ru = dma_src(Wu), rb = dma_src(A.bq);
-    auto issue_a = [&](int kt, int slot) {
-        dma16<kNt>(rg, aoff + kt * 1024, &L.a[slot][wave * 1024]);
-        dma16<kNt>(ru, aoff + kt * 1024, &L.a[slot][(RT + wave) * 1024]);
-    };
-    auto issue_b = [&](int kt, int slot) {
-#pragma unroll
-        for (int i = 0; i < NT; i++) dma16(rb, boff[i] + kt * 128, &L.b[slot][(wave + W * i) * 1024]);
-    };
-    const uint32_t nib = (uint32_t)512 * KD / 2;
-    dma16(rg, nib + ((uint32_t)(mt0 + wave) * 64 + lane) * 16, &L.sc[wave * 1024]);
-    dma16(ru, nib + ((uint32_t)(mt0 + wave) * 64 + lane) * 16, &L.sc[(RT + wave) * 1024]);
-    // B scales of column tile j, half step s: the token's x scales of K
-    // block 4kt + 2s + h (lane-group-major: byte b*16 + kt), all 16 K-steps
-    constexpr int NJ1 = NJ > 0 ? NJ : 1;
-    u32x4 sb[NJ1][2];
-#pragma unroll
-    for (int j = 0; j < NJ; j++) {
-        const int r = min(32 * (wt + 2 * j) + c32, ntok - 1);
-        const uint8_t *src = A.bs2 + (size_t)A.row_tok[p0 + r] * (KD / 32);
-#pragma unroll
-        for (int s2 = 0; s2 < 2; s2++) sb[j][s2] = *reinterpret_cast<const u32x4 *>(src + (2 * s2 + h) * 16);
-    }
-    issue_a(0, 0);
-    issue_b(0, 0);
-    issue_a(1, 1);
-    issue_a(2, 2);
-
-    // A fragment of gate/up pair u, half step s: byte offset in a stage
-    int a_off[2][2];
-#pragma unroll
-    for (int u = 0; u < 2; u++)
-#pragma unroll
-        for (int s2 = 0; s2 < 2; s2++) {
-            const int slot = (c32 < 16 ? 0 : RT) + 2 * wa + u;
-            a_off[u][s2] = slot * 1024 + ((lane & 15) + 16 * (2 * s2 + h)) * 16;
-        }
-    v16f acc[2][NJ1];
-#pragma unroll
-    for (int u = 0; u < 2; u++)
-#pragma unroll
-        for (int j = 0; j < NJ; j++) acc[u][j] = v16f{};
-    uint32_t sa[2][2];
-    uint32_t sbg[NJ1][2];
-    auto group = [&](int g, auto LASTC) {
-        constexpr bool LAST = decltype(LASTC)::value;
-#pragma unroll
-        for (int j = 0; j < NJ; j++)
-#pragma unroll
-            for (int s2 = 0; s2 < 2; s2++)
-                sbg[j][s2] = (g & 2) ? ((g & 1) ? sb[j][s2][3] : sb[j][s2][2]) : ((g & 1) ? sb[j][s2][1] : sb[j][s2][0]);
-        static_for<0, 4>([&](auto S) {
-            constexpr int st = decltype(S)::value;
-            const int kt = 4 * g + st;
-#pragma unroll
-            for (int u = 0; u < 2; u++)
-#pragma unroll
-                for (int j = 0; j < NJ; j++) asm volatile("" : "+v"(acc[u][j]));
-            if constexpr (LAST && st >= 2) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            else asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
-            dma_barrier();
-            if constexpr (!(LAST && st == 3)) issue_b(kt + 1, (st + 1) & 1);
-            if constexpr (!(LAST && st >= 1)) issue_a(kt + 3, (st + 3) & 3);
-            __builtin_amdgcn_sched_barrier(0);
-            if constexpr (st == 0) {
-#pragma unroll
-                for (int u = 0; u < 2; u++)
-#pragma unroll
-                    for (int s2 = 0; s2 < 2; s2++)
-                        sa[u][s2] = *reinterpret_cast<const uint32_t *>(&L.sc[a_off[u][s2] + 4 * g]);
-            }
-            u32x4 af[2][2];
-#pragma unroll
-            for (int u = 0; u < 2; u++)
-#pragma unroll
-                for (int s2 = 0; s2 < 2; s2++) af[u][s2] = *reinterpret_cast<const u32x4 *>(&L.a[st][a_off[u][s2]]);
-            auto read_b = [&](int j, int s2) {
-                const int r = 32 * (wt + 2 * j) + c32;
-                const u32x4 b0 = *reinterpret_cast<const u32x4 *>(&L.b[st & 1][gd_boff(r, 4 * s2 + h)]);
-                const u32x4 b1 = *reinterpret_cast<const u32x4 *>(&L.b[st & 1][gd_boff(r, 4 * s2 + 2 + h)]);
-                return v8i{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
-            };
-#pragma unroll
-            for (int j = 0; j < NJ; j++) {
-                const v8i b0 = read_b(j, 0), b1 = read_b(j, 1);
-#pragma unroll
-                for (int u = 0; u < 2; u++) {
-                    const v8i a0 = v8i{(int)af[u][0][0], (int)af[u][0][1], (int)af[u][0][2], (int)af[u][0][3], 0, 0, 0, 0};
-                    const v8i a1 = v8i{(int)af[u][1][0], (int)af[u][1][1], (int)af[u][1][2], (int)af[u][1][3], 0, 0, 0, 0};
-                    acc[u][j] = mfma32_f4xf8<st>(a0, b0, acc[u][j], (int)sa[u][0], (int)sbg[j][0]);
-                    acc[u][j] = mfma32_f4xf8<st>(a1, b1, acc[u][j], (int)sa[u][1], (int)sbg[j][1]);
-                }
-            }
-        });
-    };
-#pragma unroll 1
-    for (int g = 0; g < NKT / 4 - 1; g++) group(g, std::false_type{});
-    group(NKT / 4 - 1, std::true_type{});
-
-    // SwiGLU: lane (c32, h) holds rows 8ib + 4h + i (ib = 0, 1; i < 4) of
-    // gate (results 4ib + i) and up (results 8 + 4ib + i) of pair u; the
-    // 32-row h block (pairs 0, 1) of a token is split over lanes c32 and
-    // c32 + 32
-    const int nb = A.ldo / 32, ffb = (mt0 + 2 * wa) * 16, b = ffb / 32;
-#pragma unroll
-    for (int j = 0; j < NJ; j++) {
-        const int p = p0 + 32 * (wt + 2 * j) + c32;
-        float hv[2][8];
-        float amax = 0.0f;
-#pragma unroll
-        for (int u = 0; u < 2; u++)
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                hv[u][i] = silu(acc[u][j][i]) * acc[u][j][8 + i];
-                amax = fmaxf(amax, fabsf(hv[u][i]));
-            }
-        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(amax), __float_as_uint(amax), false, false);
-        amax = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-        const bool valid = p < p1;
-        if (hq8) {
-            const float inv = q8b_inv(amax);
-            if (valid) {
-#pragma unroll
-                for (int u = 0; u < 2; u++)
-#pragma unroll
-                    for (int ib = 0; ib < 2; ib++)
-                        *reinterpret_cast<uint32_t *>(A.hq + (size_t)p * A.ldo + ffb + 16 * u + 8 * ib + 4 * h) =
-                            q8b4(hv[u][4 * ib], hv[u][4 * ib + 1], hv[u][4 * ib + 2], hv[u][4 * ib + 3], inv);
-                if (h == 0) A.hsf[(size_t)p * nb + b] = amax / 127.0f;
-            }
-            continue;
-        }
-        const int e2 = quant_exp(amax);
-        const float mul = inv_scale(e2);
-        if (valid) {
-#pragma unroll
-            for (int u = 0; u < 2; u++)
-#pragma unroll
-                for (int ib = 0; ib < 2; ib++)
-                    *reinterpret_cast<uint32_t *>(A.hq + (size_t)p * A.ldo + ffb + 16 * u + 8 * ib + 4 * h) =
-                        e4m3x4(hv[u][4 * ib] * mul, hv[u][4 * ib + 1] * mul, hv[u][4 * ib + 2] * mul,
-                               hv[u][4 * ib + 3] * mul);
-            if (h == 0) {
-                A.hs[(size_t)p * nb + b] = (uint8_t)(127 + e2);
-                A.hs2[(size_t)p * nb + (b & 3) * (nb / 4) + (b >> 2)] = (uint8_t)(127 + e2);
-            }
-        }
-    }
-}
-
-template <int NT>
-__device__ __forceinline__ void dispatch(const GemmArgs &A, Lds &L, const uint8_t *Wg, const uint8_t *Wu, int mt0,
-                                         int p0, int p1, bool hq8, int wt) {
-    if (wt == 0) body<NT, (NT + 1) / 2>(A, L, Wg, Wu, mt0, p0, p1, hq8);
-    else body<NT, NT / 2>(A, L, Wg, Wu, mt0, p0, p1, hq8);
-}
-}  // namespace gdma32
-
-// ---------------------------------------------------------------------------
 // shared expert gate/up with q8_0-split matrices (sorted path)
 // ---------------------------------------------------------------------------
 // The reference runs a split-Q8 shared expert through pf_gemm's int8 path
@@ -1549,7 +1343,6 @@ __global__ __launch_bounds__(256) void k_shared_gateup_q8(GemmArgs A) {
     shared_gateup_q8_body(A, blockIdx.x, blockIdx.y);
 }
 
-template <bool M32>
 __global__ __launch_bounds__(256, 2) void k_gateup_dma(GemmArgs A) {
     __shared__ gdma::Lds L;
     constexpr int NRB = 512 / (16 * gdma::RT);
@@ -1581,16 +1374,6 @@ __global__ __launch_bounds__(256, 2) void k_gateup_dma(GemmArgs A) {
     const int ntt = (p1 - p0 + 15) >> 4;
     const int wt = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) >> 1;   // uniform: the switch below is a scalar branch
     const bool hq8 = A.hq8 && e < A.E;   // the shared expert's down stays MXFP4
-    if constexpr (M32) {
-        switch ((p1 - p0 + 31) >> 5) {
-            case 1: gdma32::dispatch<1>(A, L, Wg, Wu, mt0, p0, p1, hq8, wt); break;
-            case 2: gdma32::dispatch<2>(A, L, Wg, Wu, mt0, p0, p1, hq8, wt); break;
-            case 3: gdma32::dispatch<3>(A, L, Wg, Wu, mt0, p0, p1, hq8, wt); break;
-            case 4: gdma32::dispatch<4>(A, L, Wg, Wu, mt0, p0, p1, hq8, wt); break;
-            default: gdma32::dispatch<5>(A, L, Wg, Wu, mt0, p0, p1, hq8, wt); break;
-        }
-        return;
-    }
     const int nj = ntt > wt ? (ntt - wt + 1) >> 1 : 0;
     switch (nj) {
         case 0: gdma::body<0>(A, L, Wg, Wu, mt0, p0, p1, hq8); break;
@@ -3104,6 +2887,7 @@ __global__ void k_probe(const v8i *a, const v8i *b, const uint32_t *sa, const ui
 
 // v_mfma_scale_f32_32x32x64_f8f6f4 with the same lane data: 16 results per
 // lane, c[l * 16 + i]
+typedef float v16f __attribute__((ext_vector_type(16)));
 __global__ void k_probe32(const v8i *a, const v8i *b, const uint32_t *sa, const uint32_t *sb, v16f *c) {
     const int l = threadIdx.x;
     v16f acc = {};
@@ -3598,15 +3382,8 @@ static void launch_stage(const Scratch &c, const Plan &P, int st, hipStream_t s)
                     hipLaunchKernelGGL(k_shared_gateup_q8, dim3((T + kShTok - 1) / kShTok, kShRb), dim3(256), 0, s,
                                        P.ga);
             } else
-            {
-                static const bool m32 = [] { const char *e = getenv("Q36_GD32"); return e && atoi(e); }();
-                if (m32)
-                    hipLaunchKernelGGL(k_gateup_dma<true>, dim3(P.tiles * (FF / (16 * gdma::RT)) + P.ga.sh_wgs),
-                                       dim3(64 * gdma::W), 0, s, P.ga);
-                else
-                    hipLaunchKernelGGL(k_gateup_dma<false>, dim3(P.tiles * (FF / (16 * gdma::RT)) + P.ga.sh_wgs),
-                                       dim3(64 * gdma::W), 0, s, P.ga);
-            }
+                hipLaunchKernelGGL(k_gateup_dma, dim3(P.tiles * (FF / (16 * gdma::RT)) + P.ga.sh_wgs),
+                                   dim3(64 * gdma::W), 0, s, P.ga);
             break;
         case ST_DOWN:
             if (P.fused) break;   // in k_skinny_expert
