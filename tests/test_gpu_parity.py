@@ -639,6 +639,14 @@ def test_forward_empty_and_errors(dev, layer_w):
         layer.forward(dw, torch.zeros((5, 2048), device=dev), torch.zeros((5, 256), device=dev))
     with pytest.raises(moe.Q36MoEError):
         moe.MoELayer(4).forward(dw, torch.zeros((1, 2048)), torch.zeros((1, 256)))
+    # shared-gate logits: one per token, at a real stride (no broadcast view)
+    x3, lg3 = torch.zeros((3, 2048), device=dev), torch.zeros((3, 256), device=dev)
+    with pytest.raises(moe.Q36MoEError):
+        layer.forward(dw, x3, lg3, torch.zeros(2, device=dev))
+    with pytest.raises(moe.Q36MoEError):
+        layer.forward(dw, x3, lg3, torch.zeros(1, device=dev).expand(3))
+    with pytest.raises(moe.Q36MoEError):
+        moe.forward_noalloc(dw, x3, lg3, torch.zeros(4, device=dev))
 
 
 @pytest.mark.parametrize("T", [1, 64, 600])
