@@ -761,9 +761,10 @@ def layer_w64():
 def test_forward_64_experts_top4(dev, oracle, layer_w64, T):
     """A layer of 64 experts with top-4 routing (the library takes any
     n_expert <= 256 and top_k <= 8) on every path that serves T: routing,
-    sort and output against the oracle.  The output bar is the 1e-2
-    backstop (h midpoint flips move a token by up to ~2e-3 of its row max);
-    the 2e-3 bars are held on the 256-expert layers above."""
+    sort and output against the oracle, the output through the three staged
+    2e-3 bars on every token (tests/fullcheck.py: h codes equal but for
+    midpoint flips, down + combine from the GPU's h, end to end with the
+    flipped codes substituted)."""
     w, dw = layer_w64
     E, k = 64, 4
     rng = np.random.default_rng(1300 + T)
@@ -787,7 +788,16 @@ def test_forward_64_experts_top4(dev, oracle, layer_w64, T):
             np.testing.assert_array_equal(layer.tap(moe.TAP_EOFF).cpu().numpy(), off)
             np.testing.assert_array_equal(layer.tap(moe.TAP_PERM).cpu().numpy(), perm)
             np.testing.assert_array_equal(layer.tap(moe.TAP_POS).cpu().numpy(), pos)
-        _, normwise = _row_err(y.cpu().numpy().astype(np.float64), ref)
+        gi = layer.tap(moe.TAP_TOPK_IDX).cpu().numpy()
+        gpos = layer.tap(moe.TAP_POS).cpu().numpy()
+        hq, hs = layer.tap(moe.TAP_HQ).cpu().numpy(), layer.tap(moe.TAP_HS).cpu().numpy()
+        y64 = y.cpu().numpy().astype(np.float64)
+        m = fullcheck.check_every_token(oracle, w, x, lg, shg, y64, gi, gpos, hq, hs, k=k)
+        _metrics(f"experts64_top4/T{T}/path{path}", **m)
+        # and the C oracle's own per-token forward with its own h codes, as a
+        # loose backstop (a midpoint flip of a large h code moves a token by
+        # up to ~2e-3 of its row max)
+        _, normwise = _row_err(y64, ref)
         assert normwise <= 1e-2, f"path {path} (ran {layer.last_path}): {normwise:.3g}"
     assert 3 in seen and 2 in seen and 0 in seen
 
