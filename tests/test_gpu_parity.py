@@ -581,6 +581,43 @@ def test_forward_mixed_fresh_weights(dev, oracle, seed):
     del dw
 
 
+@pytest.mark.parametrize("path", [1, 4, 5])
+def test_dnw_tap_staged_rows(dev, oracle, layer_w, path):
+    """The DNW tap: every staged weighted down row (f16 with an exponent per
+    column group, widened to f32) equals w * Down_e(h) of its entry from the
+    GPU's own h codes, to the f16 rounding (2^-11 relative) plus fp32
+    accumulation.  Rows are in sorted-slot order on the sorted paths and in
+    entry order on the one-kernel path that finds its own tiles; shared
+    rows follow at T*k + t."""
+    w, dw = layer_w
+    rng = np.random.default_rng(58)
+    T = 24
+    x, lg = synth.hidden(rng, T), synth.normal_logits(rng, T)
+    shg = rng.standard_normal(T).astype(np.float32)
+    layer, _, _ = _run_layer(dev, dw, x, lg, shg, path=path)
+    gi = layer.tap(moe.TAP_TOPK_IDX).cpu().numpy()
+    pos = layer.tap(moe.TAP_POS).cpu().numpy()
+    hq, hs = layer.tap(moe.TAP_HQ).cpu().numpy(), layer.tap(moe.TAP_HS).cpu().numpy()
+    dnw = layer.tap(moe.TAP_DNW).cpu().numpy().astype(np.float64)
+    _, ow = oracle.router_topk(lg, 8)
+    entry_order = layer.last_path == 3
+    worst = 0.0
+    for t in range(T):
+        for s in range(9):
+            if s < 8:
+                p = int(pos[t * 8 + s])
+                row = t * 8 + s if entry_order else p
+                ref = ow[t, s] * oracle.expert_down(w["down"][gi[t, s]], oracle.dequant_e4m3(hq[p:p + 1], hs[p:p + 1])[0])
+            else:
+                p = row = T * 8 + t
+                ref = (1 / (1 + np.exp(-float(shg[t])))) * oracle.expert_down(
+                    w["sh_down"], oracle.dequant_e4m3(hq[p:p + 1], hs[p:p + 1])[0])
+            err = np.abs(dnw[row] - ref) - 2.0 ** -11 * np.abs(ref)
+            worst = max(worst, float(err.max() / np.abs(ref).max()))
+    _metrics("dnw_tap", path=path, worst_excess=worst)
+    assert worst <= 1e-5, worst
+
+
 @pytest.mark.parametrize("path", PATHS)
 def test_forward_shared_small(dev, oracle, layer_w, path):
     rng = np.random.default_rng(55)
