@@ -487,6 +487,43 @@ def test_forward_batch_sweep(dev, oracle, layer_w, T, path, zipf, shared):
     _check_layer(f"sweep{T}", dev, oracle, layer_w, x, lg, shg, sample=sample, path=path)
 
 
+def _random_case(seed):
+    rng = np.random.default_rng(4000 + seed)
+    T = int(np.exp(rng.uniform(np.log(2), np.log(3000))))
+    paths = [0, 1, 4, 5] + ([2] if T <= 16 else [])
+    path = int(rng.choice(paths))
+    zipf, shared, bf16 = bool(rng.integers(2)), bool(rng.integers(2)), bool(rng.integers(2))
+    return rng, T, path, zipf, shared, bf16
+
+
+RANDOM_CASES = [_random_case(i)[1:] for i in range(8)]
+
+
+@pytest.mark.parametrize("seed", range(8), ids=[f"T{c[0]}_p{c[1]}{'_zipf' if c[2] else ''}{'_sh' if c[3] else ''}"
+                                                 f"{'_bf16' if c[4] else ''}" for c in RANDOM_CASES])
+def test_forward_random_every_token(dev, oracle, layer_w, seed):
+    """Seeded random configurations (T log-uniform in 2..3000, any path that
+    serves T, Zipf or normal routing, with or without the shared expert, f32
+    or bf16 x), every token through the three staged 2e-3 bars."""
+    w, dw = layer_w
+    rng, T, path, zipf, shared, bf16 = _random_case(seed)
+    x = synth.hidden(rng, T)
+    if bf16:
+        x = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    lg = synth.zipf_logits(rng, T) if zipf else synth.normal_logits(rng, T)
+    shg = rng.standard_normal(T).astype(np.float32) if shared else None
+    layer, y32, y16 = _run_layer(dev, dw, x, lg, shg, x_dtype=torch.bfloat16 if bf16 else torch.float32, path=path)
+    gi = _check_routing(layer, oracle, lg)
+    oq, os_ = oracle.quant_e4m3(x)
+    np.testing.assert_array_equal(layer.tap(moe.TAP_XQ).cpu().numpy(), oq)
+    np.testing.assert_array_equal(layer.tap(moe.TAP_XS).cpu().numpy(), os_)
+    np.testing.assert_array_equal(y16, _bf16_of(y32))
+    pos = layer.tap(moe.TAP_POS).cpu().numpy()
+    hq, hs = layer.tap(moe.TAP_HQ).cpu().numpy(), layer.tap(moe.TAP_HS).cpu().numpy()
+    m = fullcheck.check_every_token(oracle, w, x, lg, shg, y32, gi, pos, hq, hs)
+    _metrics(f"random{seed}", T=T, path=path, ran=layer.last_path, zipf=zipf, shared=shared, bf16=bf16, **m)
+
+
 @pytest.mark.parametrize("path", PATHS)
 @pytest.mark.parametrize("T", [2, 7, 16])
 def test_forward_small_batches(dev, oracle, layer_w, T, path):
@@ -585,8 +622,9 @@ def test_forward_mixed_fresh_weights(dev, oracle, seed):
 def test_dnw_tap_staged_rows(dev, oracle, layer_w, path):
     """The DNW tap: every staged weighted down row (f16 with an exponent per
     column group, widened to f32) equals w * Down_e(h) of its entry from the
-    GPU's own h codes, to the f16 rounding (2^-11 relative) plus fp32
-    accumulation.  Rows are in sorted-slot order on the sorted paths and in
+    GPU's own h codes, to the f16 rounding (2^-11 relative) plus the scaled
+    MFMA's own accumulation error (up to ~5e-5 of max|C| on gfx950, as the
+    operand calibration measures; bar 2e-4 of the row maximum).  Rows are in sorted-slot order on the sorted paths and in
     entry order on the one-kernel path that finds its own tiles; shared
     rows follow at T*k + t."""
     w, dw = layer_w
@@ -615,7 +653,7 @@ def test_dnw_tap_staged_rows(dev, oracle, layer_w, path):
             err = np.abs(dnw[row] - ref) - 2.0 ** -11 * np.abs(ref)
             worst = max(worst, float(err.max() / np.abs(ref).max()))
     _metrics("dnw_tap", path=path, worst_excess=worst)
-    assert worst <= 1e-5, worst
+    assert worst <= 2e-4, worst
 
 
 @pytest.mark.parametrize("path", PATHS)
